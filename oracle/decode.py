@@ -24,9 +24,20 @@ import numpy as np
 from . import interp
 
 
+def _aligned_f32(a):
+    """fp32 copy of ``a`` whose data starts on a 64-byte boundary."""
+    a = np.asarray(a)
+    buf = np.empty(a.size + 16, np.float32)
+    off = (-buf.ctypes.data % 64) // 4
+    out = buf[off:off + a.size].reshape(a.shape)
+    out[...] = a
+    return out
+
+
 def oracle_weights(stacked_fp16: dict) -> dict:
-    """fp16 residue arrays -> fp32 arrays holding the same values."""
-    return {k: np.asarray(v).astype(np.float32) for k, v in stacked_fp16.items()}
+    """fp16 residue arrays -> fp32 arrays holding the same values (64-byte
+    aligned, so the interpreter's fast path can read per-layer slabs in place)."""
+    return {k: _aligned_f32(v) for k, v in stacked_fp16.items()}
 
 
 def program_extents(text: str) -> dict:

@@ -1,0 +1,158 @@
+"""The gfx950 lowering on the CPU: analyses, placements, barrier counts, and
+hipRTC compilation of the generated kernels (hipRTC needs no GPU).
+
+Reference behaviour being mirrored: batch lift (reference vesta/lower.py:109-132),
+hoist/alias/inline (:187-310), placement classes (:543-561), Lowered fields
+(:69-79) and lower() (:1294-1329).
+"""
+import os
+import re
+
+import pytest
+
+from vesta import launch
+from vesta.gpt2_program import gpt2_program
+from vesta.interp import parse
+from vesta.lower import LowerError, Lowering, batch_lift, lower
+
+from conftest import PKG, REPO
+
+
+def gpt2_spec(B, tmax, L=12, D=768, H=12, F=3072, V=50257, npos=1024):
+    E = D // H
+    return {'x': ((B,), 'i32'), 't': ((), 'i32'), 'wte': ((V, D), 'f16'), 'wpe': ((npos, D), 'f16'),
+            'ln1w': ((L, D), 'f16'), 'ln1b': ((L, D), 'f16'), 'qkvw': ((L, D, 3 * D), 'f16'),
+            'qkvb': ((L, 3 * D), 'f16'), 'ow': ((L, D, D), 'f16'), 'ob': ((L, D), 'f16'), 'ln2w': ((L, D), 'f16'),
+            'ln2b': ((L, D), 'f16'), 'fcw': ((L, D, F), 'f16'), 'fcb': ((L, F), 'f16'), 'pw': ((L, F, D), 'f16'),
+            'pb': ((L, D), 'f16'), 'lnfw': ((D,), 'f16'), 'lnfb': ((D,), 'f16'),
+            'keys': ((B, L, tmax, H, E), 'f16'), 'vals': ((B, L, tmax, H, E), 'f16')}
+
+
+def lower_gpt2(B=1, tmax=384, shape=(12, 768, 12, 3072, 50257), **kw):
+    L, D, H, F, V = shape
+    text = gpt2_program(L, D, H, F, V)
+    return lower(text, gpt2_spec(B, tmax, L, D, H, F, V), {'s': tmax}, batch=B, per_token=('x', 'keys', 'vals'),
+                 outputs=('logit', 'next'), feedback={'x': 'next', 't': 1}, **kw)
+
+
+def placements(low):
+    out = {}
+    for st, pl in low.plan:
+        name = st.split('[')[0].split(' ')[0] if not st.startswith('residue') else st.split('[')[0]
+        out[name] = pl
+    return out
+
+
+def test_batch_lift_adds_token_axis():
+    stmts = batch_lift(parse('residue x\nresidue w[n]\naxis n = 3\ny[n] = w[n] + x\nz = fold sum n: y[n]\n'), 4, {'x'})
+    assert stmts[0] == ('axis', 'bt', ('num', 4))
+    let_y = [s for s in stmts if s[0] == 'let' and s[1] == 'y'][0]
+    assert let_y[2] == ['bt', 'n']
+    assert ('idx', 'x', [('name', 'bt')]) in [n for n in _nodes(let_y[3])]
+    let_z = [s for s in stmts if s[0] == 'let' and s[1] == 'z'][0]
+    assert let_z[2] == ['bt'] and let_z[3][3] == ('idx', 'y', [('name', 'bt'), ('name', 'n')])
+
+
+def _nodes(e):
+    from vesta.lower import nodes
+    return list(nodes(e))
+
+
+def test_gpt2_small_b1_plan():
+    low = lower_gpt2(1)
+    p = placements(low)
+    for name in ('qkv', 'o', 'oo', 'u', 'z2'):
+        assert p[name].startswith('tile'), (name, p[name])
+    assert p['sc'].startswith('lane') and p['logit'].startswith('lane')
+    assert p['best'] == 'gridred' and p['next'] == 'gridred'
+    assert p['m1'] == p['v1'] == p['a'] == 'private'
+    assert p['residue keys'] == 'epilogue of qkv' and p['residue vals'] == 'epilogue of qkv'
+    assert p['g'] == 'epilogue of u' and p['z1'] == 'epilogue of oo'
+    # softmax denominator hoisted, q / ex / w inlined
+    assert '_h1' in p and 'q' not in p and 'w' not in p and 'ex' not in p
+    assert low.barriers_per_launch <= 76
+    assert set(low.scratch) >= {'logit', 'next'} and low.scratch['logit'][2] == (1, 50257)
+
+
+def test_gpt2_small_b8_plan():
+    low = lower_gpt2(8)
+    p = placements(low)
+    assert p['mx'].startswith('group') and p['_h1'].startswith('group')
+    assert p['qkv'].startswith('tile') and p['logit'].startswith('lane')
+    assert low.barriers_per_launch <= 88
+    assert low.scratch['logit'][2] == (8, 50257) and low.scratch['next'][2] == (8,)
+
+
+def test_params_and_abi():
+    low = lower_gpt2(1)
+    names = [n for n, _, _ in low.params]
+    assert names == list(gpt2_spec(1, 384))
+    written = {n for n, _, w in low.params if w}
+    assert written == {'x', 't', 'keys', 'vals'}
+    sig = re.search(r'vesta_step\((.*?)\) \{', low.src).group(1)
+    assert sig.endswith('const int nsteps, int* __restrict__ tok_out, const int* __restrict__ tok_in')
+    assert 'const vh_half* __restrict__ R_wte' in sig and 'vh_half* __restrict__ R_keys' in sig
+
+
+def test_kernel_has_no_cache_maintenance_fences():
+    """Cross-block data goes through coherent loads/stores: no agent fences."""
+    src = lower_gpt2(1).src
+    assert '__builtin_amdgcn_fence' not in src.split('extern "C"')[1]
+
+
+@pytest.mark.parametrize('B', [1, 8])
+def test_gpt2_small_compiles_for_gfx950(B):
+    low = lower_gpt2(B)
+    code = launch.compile_code(low.src, cache=False)
+    assert code[:4] == b'\x7fELF'
+
+
+def test_tiny_and_medium_compile():
+    tiny = lower_gpt2(1, 20, (2, 16, 4, 64, 37))
+    assert launch.compile_code(tiny.src, cache=False)[:4] == b'\x7fELF'
+    med = lower_gpt2(1, 512, (24, 1024, 16, 4096, 50257))
+    assert placements(med)['qkv'].startswith('tile')
+    assert launch.compile_code(med.src, cache=False)[:4] == b'\x7fELF'
+
+
+def test_errors():
+    with pytest.raises(NameError):
+        lower('residue q[i]\naxis i = 2\ny[i] = q[i]\n', {}, {})
+    with pytest.raises(LowerError):
+        lower('residue q[s]\naxis s = t + 1\nresidue t\ny[s] = q[s]\n', {'q': ((4,), 'f32'), 't': ((), 'i32')}, {})
+    with pytest.raises(NameError):
+        lower('residue q[i]\naxis i = 2\ny[i] = q[i]\n', {'q': ((2,), 'f32')}, {}, outputs=('nope',))
+
+
+def test_hiprtc_error_carries_log():
+    with pytest.raises(RuntimeError, match='hipRTC failed'):
+        launch.compile_code('extern "C" __global__ void vesta_step() { undeclared_thing(); }', cache=False)
+
+
+def test_generic_programs_lower_and_compile():
+    """Small programs of every form lower to kernels that compile."""
+    import json
+    cases = json.load(open(os.path.join(REPO, 'tests', 'golden', 'grammar_cases.json')))
+    for name, case in cases.items():
+        res = {}
+        for k, v in case['inputs'].items():
+            if isinstance(v, dict):
+                import numpy as np
+                res[k] = (tuple(np.array(v['values']).shape), v['dtype'])
+            else:
+                res[k] = ((), 'i32')
+        outs = [r for r in case['record'] if r in case.get('axes', {})]
+        low = lower(case['text'], res, {}, outputs=tuple(outs))
+        assert launch.compile_code(low.src, cache=False)[:4] == b'\x7fELF', name
+
+
+def test_c_abi_exports_every_declared_symbol():
+    import ctypes
+    header = open(os.path.join(REPO, 'include', 'vesta_hip.h')).read()
+    declared = set(re.findall(r'^(?:int|void|const char\*)\s+(vh_\w+)\(', header, re.M))
+    assert {'vh_compile', 'vh_module_load', 'vh_launch_cooperative', 'vh_occupancy'} <= declared
+    lib = ctypes.CDLL(launch.LIB_PATH)
+    for sym in declared:
+        assert hasattr(lib, sym), sym
+    lib.vh_error_string.restype = ctypes.c_char_p
+    assert lib.vh_error_string(0) == b'success'

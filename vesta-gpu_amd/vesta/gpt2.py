@@ -1,0 +1,146 @@
+"""gpt2.vst on the GPU: GPT-2 weights as residues, lowered to one kernel per step.
+
+    m = VestaGPT2(hf, dtype='f16', batch=8, tmax=1024)
+    m.reset(); m.x.copy_(tok); m.t.fill_(p); m.step()     # one decode step
+    m.logits(), m.next()                                    # views, no sync
+
+With feedback on, each step writes its chosen token into x and advances t,
+so generation is back-to-back launches with nothing from the host between.
+
+Same surface as the reference decode API (reference ``vesta/gpt2.py:1-55``:
+``gpt2_weights``, ``VestaGPT2`` with ``x``/``t``/``keys``/``vals``/``W``/
+``low``/``k``/``weight_bytes`` and ``reset``/``step``/``logits``/``next``/
+``kv_bytes``). ``hf`` only needs ``state_dict()`` with Hugging Face GPT-2 names
+(a ``transformers`` GPT-2 model, or ``vesta.weights.RandomGPT2``). Extents
+come from the state dict, so GPT-2 small, medium and XL all work; the program
+defaults to the committed one for those shapes.
+"""
+from __future__ import annotations
+
+from . import PROGRAMS
+from .gpt2_program import gpt2_program
+from .launch import TORCH_DT, Kernel
+from .lower import lower
+
+SHAPE_PROGRAMS = {(12, 768, 12): 'gpt2.vst', (24, 1024, 16): 'gpt2_medium.vst', (48, 1600, 25): 'gpt2_xl.vst'}
+
+
+def _n_layer(sd):
+    n = 0
+    while f'transformer.h.{n}.ln_1.weight' in sd:
+        n += 1
+    return n
+
+
+def gpt2_weights(hf):
+    """HF state dict -> the program's residues: per-layer tensors stacked along
+    a leading layer axis (reference gpt2.py:18-25)."""
+    import torch
+    sd = hf.state_dict()
+    L = _n_layer(sd)
+
+    def st(n):
+        return torch.stack([sd[f'transformer.h.{i}.{n}'] for i in range(L)])
+    return dict(wte=sd['transformer.wte.weight'], wpe=sd['transformer.wpe.weight'],
+                ln1w=st('ln_1.weight'), ln1b=st('ln_1.bias'), qkvw=st('attn.c_attn.weight'), qkvb=st('attn.c_attn.bias'),
+                ow=st('attn.c_proj.weight'), ob=st('attn.c_proj.bias'), ln2w=st('ln_2.weight'), ln2b=st('ln_2.bias'),
+                fcw=st('mlp.c_fc.weight'), fcb=st('mlp.c_fc.bias'), pw=st('mlp.c_proj.weight'), pb=st('mlp.c_proj.bias'),
+                lnfw=sd['transformer.ln_f.weight'], lnfb=sd['transformer.ln_f.bias'])
+
+
+def _n_head(hf, d):
+    cfg = getattr(hf, 'config', None)
+    for attr in ('n_head', 'num_attention_heads'):
+        if cfg is not None and getattr(cfg, attr, None):
+            return int(getattr(cfg, attr))
+    return {768: 12, 1024: 16, 1280: 20, 1600: 25}[d]
+
+
+class VestaGPT2:
+    def __init__(self, hf, dtype='f16', batch=1, tmax=1024, feedback=True, program=None, timing=False,
+                 blocks_per_sm=None):
+        import torch
+        tdt = TORCH_DT[dtype]
+        self.W = {k: v.detach().to('cuda', tdt).contiguous() for k, v in gpt2_weights(hf).items()}
+        L = self.W['qkvw'].shape[0]
+        D = self.W['wte'].shape[1]
+        H = _n_head(hf, D)
+        E = D // H
+        F = self.W['fcw'].shape[2]
+        V = self.W['wte'].shape[0]
+        if tmax > self.W['wpe'].shape[0]:
+            raise ValueError(f'tmax {tmax} exceeds the {self.W["wpe"].shape[0]} learned positions')
+        self.L, self.H, self.E, self.D = L, H, E, D
+        self.B, self.tmax = batch, tmax
+        self.keys = torch.zeros(batch, L, tmax, H, E, device='cuda', dtype=tdt)
+        self.vals = torch.zeros_like(self.keys)
+        self.x = torch.zeros(batch, dtype=torch.int32, device='cuda')
+        self.t = torch.zeros(1, dtype=torch.int32, device='cuda')
+        R = {'x': self.x, 't': self.t, **self.W, 'keys': self.keys, 'vals': self.vals}
+        dts = {torch.int32: 'i32', torch.float16: 'f16', torch.float32: 'f32'}
+        spec = {n: ((), 'i32') if n == 't' else (tuple(v.shape), dts[v.dtype]) for n, v in R.items()}
+        if program is None:
+            name = SHAPE_PROGRAMS.get((L, D, H))
+            text = (PROGRAMS / name).read_text(encoding='utf-8') if name and F == 4 * D and V == 50257 \
+                else gpt2_program(L, D, H, F, V, 'custom')
+        else:
+            text = open(program, encoding='utf-8').read()
+        self._lower_args = (text, spec, dict(axis_max={'s': tmax}, batch=batch, per_token=('x', 'keys', 'vals'),
+                                             outputs=('logit', 'next'),
+                                             feedback={'x': 'next', 't': 1} if feedback else None))
+        self._R, self._bps, self._timing = R, blocks_per_sm, timing
+        self.low = lower(text, spec, **self._lower_args[2], timing=timing, kernel_name=f'vesta_step_b{batch}')
+        self.k = Kernel(self.low, blocks_per_sm=blocks_per_sm)
+        self.k.bind(R)
+        self._kp = None
+        self.weight_bytes = sum(v.numel() * v.element_size() for n, v in self.W.items() if n != 'wpe') \
+            + D * self.W['wpe'].element_size()
+
+    def reset(self):
+        self.keys.zero_()
+        self.vals.zero_()
+        self.t.zero_()
+
+    def step(self, n=1, tokens=None):
+        """One decode step (the reference API); ``n`` > 1 runs n steps in one
+        launch, writing each step's tokens into ``tokens`` [n, B] if given."""
+        if tokens is not None and tokens.numel() < n * self.B:
+            raise ValueError(f'tokens holds {tokens.numel()} ids, {n * self.B} needed')
+        self.k.launch(n, tokens)
+
+    def _prefill_kernel(self):
+        """The same program under its own symbol, for prompt feeding and
+        warm-up (so profiles of the decode kernel hold decode launches only)."""
+        if self._kp is None:
+            text, spec, kw = self._lower_args
+            low = lower(text, spec, **kw, timing=self._timing, kernel_name=f'vesta_prefill_b{self.B}')
+            self._kp = Kernel(low, blocks_per_sm=self._bps)
+            self._kp.bind(self._R)
+        return self._kp
+
+    def prefill(self, prompt, tokens=None):
+        """Feed a prompt [B, P] (int32 device tensor) one token per step in ONE
+        launch; afterwards x holds the token chosen after the last prompt token
+        (as after P reference-style steps)."""
+        P = prompt.shape[1]
+        if prompt.shape[0] != self.B:
+            raise ValueError(f'prompt has {prompt.shape[0]} rows, the model {self.B}')
+        if P < 1:
+            raise ValueError('empty prompt')
+        ins = prompt.t().contiguous().to(dtype=self.x.dtype)
+        self.x.copy_(ins[0])
+        self._prefill_kernel().launch(P, tokens, ins)
+
+    def warm(self, n):
+        """n decode steps through the prefill kernel (untimed warm-up)."""
+        if n > 0:
+            self._prefill_kernel().launch(n)
+
+    def logits(self):
+        return self.k.view('logit')
+
+    def next(self):
+        return self.k.view('next')
+
+    def kv_bytes(self, n_ctx):
+        return 2 * self.L * self.B * n_ctx * self.D * self.keys.element_size()

@@ -1,0 +1,254 @@
+"""Compile a Lowered program with hipRTC and run it as one cooperative launch.
+
+Mirrors the reference's ``vesta/launch.py`` surface (``TORCH_DT``,
+``compile_code`` in place of ``compile_cubin`` :17-27, ``Kernel`` :29-73 with
+``view``/``bind``/``launch``/``__call__``), over the repository's own native
+shim ``libvesta_hip.so`` (C ABI in include/vesta_hip.h) instead of NVRTC and
+the CUDA driver. torch supplies the device buffers and the stream; the shim
+owns only module and function handles.
+
+There is no fallback: if the shim is not built or no GPU is present, the
+calls that need them raise.
+"""
+from __future__ import annotations
+
+import ctypes
+import hashlib
+import os
+import threading
+
+LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), '_lib')
+LIB_PATH = os.path.join(LIB_DIR, 'libvesta_hip.so')
+CACHE_DIR = os.environ.get('VESTA_CACHE', os.path.join(os.path.dirname(os.path.abspath(__file__)), '_cache'))
+ARCH = os.environ.get('VESTA_ARCH', 'gfx950')
+# Packed fp32 vector ops stay off (they have given silent wrong results on
+# these parts); -O3 for the generated kernel.
+RTC_OPTS = ('-O3', '-std=c++17', '-ffp-contract=off',
+            '-mllvm', '-amdgpu-early-inline-all=true',
+            '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops')
+
+_lib = None
+_lib_lock = threading.Lock()
+
+
+def lib():
+    """The loaded shim (ctypes.CDLL). Raises if it has not been built."""
+    global _lib
+    with _lib_lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise RuntimeError(f'{LIB_PATH} is missing: build it with __graft_entry__.build()')
+            L = ctypes.CDLL(LIB_PATH)
+            vp, sz, ip, cp = ctypes.c_void_p, ctypes.c_size_t, ctypes.POINTER(ctypes.c_int), ctypes.c_char_p
+            sig = {
+                'vh_compile': [cp, cp, ctypes.POINTER(cp), ctypes.c_int, ctypes.POINTER(vp), ctypes.POINTER(sz),
+                               ctypes.POINTER(vp)],
+                'vh_module_load': [vp, ctypes.POINTER(vp)],
+                'vh_module_get_function': [vp, cp, ctypes.POINTER(vp)],
+                'vh_module_unload': [vp],
+                'vh_function_set_dynamic_lds': [vp, ctypes.c_int],
+                'vh_function_attrs': [vp, ip, ip, ip, ip],
+                'vh_occupancy': [vp, ctypes.c_int, sz, ip],
+                'vh_device_info': [ctypes.c_int, ip, ip, ip, cp, sz],
+                'vh_launch_cooperative': [vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, vp, ctypes.POINTER(vp)],
+                'vh_launch': [vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, vp, ctypes.POINTER(vp)],
+                'vh_synchronize': [],
+            }
+            for name, args in sig.items():
+                fn = getattr(L, name)
+                fn.argtypes, fn.restype = args, ctypes.c_int
+            L.vh_free.argtypes, L.vh_free.restype = [vp], None
+            L.vh_error_string.argtypes, L.vh_error_string.restype = [ctypes.c_int], ctypes.c_char_p
+            _lib = L
+        return _lib
+
+
+def ok(status, what=''):
+    if status != 0:
+        msg = lib().vh_error_string(status).decode(errors='replace')
+        raise RuntimeError(f'{what}: {msg} (status {status})' if what else f'{msg} (status {status})')
+
+
+def compile_code(src: str, arch: str = ARCH, opts=RTC_OPTS, cache: bool = True) -> bytes:
+    """HIP C++ -> gfx950 code object through hipRTC (replaces NVRTC, reference
+    launch.py:17-27). Failures raise RuntimeError carrying the compile log.
+    Code objects are cached on disk by a hash of source, arch and options."""
+    full = [f'--offload-arch={arch}', *opts]
+    key = hashlib.sha256((src + '\0' + '\0'.join(full)).encode()).hexdigest()[:32]
+    path = os.path.join(CACHE_DIR, key + '.co')
+    if cache and os.path.exists(path):
+        with open(path, 'rb') as fh:
+            return fh.read()
+    L = lib()
+    arr = (ctypes.c_char_p * len(full))(*[o.encode() for o in full])
+    code, size, log = ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_void_p()
+    st = L.vh_compile(src.encode(), b'vesta_step.hip', arr, len(full), ctypes.byref(code), ctypes.byref(size),
+                      ctypes.byref(log))
+    text = ctypes.string_at(log.value).decode(errors='replace') if log.value else ''
+    if log.value:
+        L.vh_free(log)
+    if st != 0:
+        raise RuntimeError(f'hipRTC failed ({L.vh_error_string(st).decode()}):\n{text}')
+    blob = ctypes.string_at(code.value, size.value)
+    L.vh_free(code)
+    if cache:
+        os.makedirs(CACHE_DIR, exist_ok=True)
+        tmp = f'{path}.{os.getpid()}.tmp'
+        with open(tmp, 'wb') as fh:
+            fh.write(blob)
+        os.replace(tmp, path)
+    return blob
+
+
+def device_info(dev: int = 0) -> dict:
+    cu, coop, lds = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    arch = ctypes.create_string_buffer(128)
+    ok(lib().vh_device_info(dev, ctypes.byref(cu), ctypes.byref(coop), ctypes.byref(lds), arch, 128), 'device info')
+    return dict(cu_count=cu.value, cooperative=bool(coop.value), lds_per_block=lds.value, arch=arch.value.decode())
+
+
+def _torch():
+    import torch
+    return torch
+
+
+def torch_dtypes():
+    torch = _torch()
+    return {'f32': torch.float32, 'f16': torch.float16, 'i32': torch.int32}
+
+
+class _LazyDT(dict):
+    def __missing__(self, k):
+        self.update(torch_dtypes())
+        return dict.__getitem__(self, k)
+
+
+TORCH_DT = _LazyDT()
+
+
+class Kernel:
+    """One generated kernel, loaded on the current device and launched
+    cooperatively on torch's current stream (reference launch.py:29-73).
+
+    grid = blocks that fit per CU (occupancy at ``block`` threads and the
+    kernel's LDS) x CUs, optionally capped by ``blocks_per_sm`` and by the
+    lowering's own grid limit. ``S`` (fp32 scratch), ``bar`` (barrier and
+    reduction counters, zeroed once; the kernel leaves them zeroed) and ``TS``
+    (timing sums) are allocated here.
+    """
+
+    def __init__(self, lowered, block=256, device=0, blocks_per_sm=None):
+        torch = _torch()
+        if not torch.cuda.is_available():
+            raise RuntimeError('no GPU: the Vesta kernel needs a ROCm device')
+        torch.cuda.set_device(device)
+        torch.zeros(1, device='cuda')                       # make torch's context current
+        self.device = device
+        self.info = device_info(device)
+        if not self.info['cooperative']:
+            raise RuntimeError('device does not support cooperative launch')
+        if block != lowered.block:
+            raise ValueError(f'kernel was lowered for {lowered.block} threads per block, not {block}')
+        self.code = compile_code(lowered.src)
+        L = lib()
+        mod, fn = ctypes.c_void_p(), ctypes.c_void_p()
+        ok(L.vh_module_load(self.code, ctypes.byref(mod)), 'module load')
+        self.mod = mod
+        ok(L.vh_module_get_function(mod, lowered.name.encode(), ctypes.byref(fn)), 'get function')
+        self.fn = fn
+        self.smem = lowered.shared_bytes
+        if self.smem > 65536:       # up to 64 KB needs no opt-in
+            ok(L.vh_function_set_dynamic_lds(fn, self.smem), 'dynamic LDS')
+        per = ctypes.c_int()
+        ok(L.vh_occupancy(fn, block, self.smem, ctypes.byref(per)), 'occupancy')
+        per_cu = per.value
+        if blocks_per_sm:
+            per_cu = min(per_cu, blocks_per_sm)
+        self.per_cu = per_cu
+        self.cus = self.info['cu_count']
+        self.grid = min(per_cu * self.cus, lowered.grid_max)
+        self.block = block
+        regs, slds, priv, mxb = (ctypes.c_int() for _ in range(4))
+        ok(L.vh_function_attrs(fn, ctypes.byref(regs), ctypes.byref(slds), ctypes.byref(priv), ctypes.byref(mxb)),
+           'function attributes')
+        self.attrs = dict(regs=regs.value, static_lds=slds.value, private_bytes=priv.value, max_block=mxb.value)
+        self.lowered = lowered
+        self.S = torch.zeros(max(1, lowered.scratch_floats), dtype=torch.float32, device='cuda')
+        self.bar = torch.zeros(lowered.counters, dtype=torch.int32, device='cuda')
+        self.TS = torch.zeros(1024, dtype=torch.int64, device='cuda')
+        self.args = None
+
+    def view(self, name):
+        """A torch view of a value kept in global scratch (no copy, no sync)."""
+        off, _, shape = self.lowered.scratch[name]
+        n = 1
+        for s in shape:
+            n *= s
+        return self.S[off:off + max(1, n)].view(*shape) if shape else self.S[off]
+
+    def bind(self, residue):
+        """Fix the argument list once; a launch is then one shim call."""
+        vals = []
+        for name, dt, _ in self.lowered.params:
+            t = residue[name]
+            if not (t.is_cuda and t.dtype == TORCH_DT[dt] and t.is_contiguous()):
+                raise TypeError(f'residue {name}: need a contiguous {dt} device tensor, got {t.dtype} '
+                                f'{"device" if t.is_cuda else "host"} {"contiguous" if t.is_contiguous() else "strided"}')
+            want = self.lowered.shapes[name]
+            if tuple(t.shape) != tuple(want) and not (want == () and t.numel() == 1):
+                raise ValueError(f'residue {name}: shape {tuple(t.shape)} but the kernel was lowered for {want}')
+            vals.append(t.data_ptr())
+        vals += [self.S.data_ptr(), self.bar.data_ptr(), self.TS.data_ptr()]
+        self._slots = [ctypes.c_void_p(v) for v in vals]
+        self._nsteps = ctypes.c_int(1)
+        self._tok = ctypes.c_void_p(0)
+        self._tok_in = ctypes.c_void_p(0)
+        ptrs = [ctypes.cast(ctypes.pointer(x), ctypes.c_void_p) for x in self._slots]
+        ptrs += [ctypes.cast(ctypes.pointer(v), ctypes.c_void_p) for v in (self._nsteps, self._tok, self._tok_in)]
+        self.args = (ctypes.c_void_p * len(ptrs))(*ptrs)
+        self.keep = residue
+
+    def launch(self, steps=1, tokens=None, inputs=None):
+        """Run ``steps`` steps in one cooperative launch on torch's current
+        stream (no sync). With token feedback, ``tokens`` (int32 device tensor,
+        at least steps * B elements) receives each step's chosen tokens, and
+        ``inputs`` (int32 device tensor [steps, B]) forces the input of steps
+        1..steps-1 (the first step reads the residue as usual)."""
+        if self.args is None:
+            raise RuntimeError('bind() the residues before launch()')
+        if steps < 1:
+            raise ValueError('steps must be at least 1')
+        self._nsteps.value = int(steps)
+        if tokens is not None:
+            if not (tokens.is_cuda and tokens.dtype == TORCH_DT['i32'] and tokens.is_contiguous()):
+                raise TypeError('tokens must be a contiguous int32 device tensor')
+            self._tok.value = tokens.data_ptr()
+        else:
+            self._tok.value = 0
+        if inputs is not None:
+            if not (inputs.is_cuda and inputs.dtype == TORCH_DT['i32'] and inputs.is_contiguous()):
+                raise TypeError('inputs must be a contiguous int32 device tensor')
+            self._tok_in.value = inputs.data_ptr()
+        else:
+            self._tok_in.value = 0
+        stream = _torch().cuda.current_stream().cuda_stream
+        ok(lib().vh_launch_cooperative(self.fn, self.grid, self.block, self.smem, ctypes.c_void_p(stream), self.args),
+           'cooperative launch')
+
+    def __call__(self, residue):
+        self.bind(residue)
+        self.launch()
+
+    def close(self):
+        if getattr(self, 'mod', None) is not None and self.mod.value:
+            try:
+                lib().vh_synchronize()          # no launch of this module may still be running
+                lib().vh_module_unload(self.mod)
+            finally:
+                self.mod = None
+
+    def __del__(self):
+        try:
+            self.close()
+        except Exception:
+            pass

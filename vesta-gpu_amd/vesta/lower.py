@@ -1,0 +1,1987 @@
+"""Vesta lowering for gfx950: a program -> HIP C++ for ONE persistent kernel
+that runs the whole program per launch (one GPT-2 decode step per launch).
+
+    lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None, timing=False)
+
+Same signature and result type as the reference compiler (reference
+``vesta/lower.py:1294``, ``Lowered`` :69-79); the generated source is HIP for
+CDNA4 (wave64, 160 KB LDS, agent-scope grid barrier) instead of CUDA.
+
+    res       residue name -> (shape, dtype), dtype 'f32' | 'f16' | 'i32'.
+              Shapes as the kernel sees them (batched where per-token);
+              scalars have shape () and are read through a pointer.
+    axis_max  upper bound of axes whose extent is set at run time (s = t+1)
+    batch     B: the program is asked of B tokens at once (batch lift)
+    per_token residues that differ per token (x, the key/value cache)
+    outputs   named values the host reads; kept in global scratch
+    feedback  {'x': 'next', 't': 1}: after the step, x <- next and t += 1,
+              so steps run back to back with no host round trip
+
+Pipeline (own design; the placement classes keep the reference's names so a
+reader of both can line them up, reference lower.py:21-40):
+
+  batch_lift   every local and per-token residue gains a leading axis 'bt'
+  normalise    a bare read of a local with axes becomes a read at its axes
+  hoist        a fold that ignores some output axis becomes its own
+               statement (the softmax denominator, once per (bt, h))
+  alias        carry <- init / carry <- ret / result <- carry share storage
+  inline       fold-free values are substituted into their readers unless a
+               reader streams a large residue inside its fold
+  place        one placement per statement:
+    tile     sum whose body reads a residue along its contiguous last axis,
+             which is an output axis: 16-byte loads along that axis, rows of
+             the fold split over the 4 waves of a block and over blocks
+             (split-K); partials reduced in a fixed order by the last block
+             to finish the tile, which also runs the epilogue, the statements
+             fused into it and the emits it feeds
+    lane     sum whose body reads a residue along its contiguous last axis,
+             which is the fold axis: a group of lanes per output point,
+             16-byte loads along the fold, butterfly reduction
+    private  small values every block computes for itself into LDS
+    group    consecutive statements that share leading axes and read each
+             other only at those axes: one block per leading point
+    gridred  a fold over a very long axis into a few points: per-block
+             partials, the last block combines them in block order
+    thread   one thread per output point, folds as serial loops
+  barriers     a grid barrier goes where a statement reads a value written
+               since the last barrier, or overwrites one read since then
+  codegen      one kernel; the prelude (hip/prelude.h) supplies fp16
+               conversion, 16-byte loads, wave64/block reductions, the grid
+               barrier and the last-arriver counter
+
+Arithmetic is fp32 with IEEE division and square root and no contraction
+of separate multiply and add (elementwise statements round as NumPy does);
+the inner products of tile and lane sites use fused multiply-add.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+from pathlib import Path
+
+import numpy as np
+
+from .interp import parse
+
+PRELUDE_PATH = Path(__file__).resolve().parent / 'hip' / 'prelude.h'
+
+WAVE, NWAVE = 64, 4
+BLOCK = WAVE * NWAVE          # threads per block: one wave per SIMD of a CU
+KCAP = 32                     # split-K: at most this many partials per tile column block
+GRID_MAX = 1024               # grid reductions keep one partial per block, for up to this many blocks
+REG_MAX = 8                   # register axes: at most this many accumulator rows per lane
+PRIV_SIZE = 8192              # a private value holds at most this many floats
+PRIV_WORK = 1 << 17           # ... and costs at most this many operations per block
+PRIV_BUDGET = 16384           # all live private values together: 64 KB of LDS
+STAGE_MAX = 8192              # a private statement reads at most this many floats of locals
+GROUP_WORK = 1 << 14          # a group statement does at most this much work per leading point
+BIG = 1 << 16                 # a residue this large is streamed, never recomputed per point
+LANE_MIN = 32                 # lane-split a fold only if it is at least this long
+GRIDRED_MIN = 1 << 14         # grid reduction for a fold at least this long into few points
+GRIDRED_POINTS = 8
+UNROLL = 8                    # rows (tile) / vectors (lane) whose loads are issued together
+TILE_LANES = 8                # tile: lanes per row (8 x 16 bytes = one 128-byte line of a weight row)
+LINE_WORDS = 32               # one 128-byte line per counter
+BAR_WORDS = LINE_WORDS * 10   # grid barrier: generation word, top counter, 8 group counters
+
+FOLD_INIT = {'sum': '0.0f', 'max': '-INFINITY', 'min': 'INFINITY'}
+FOLD_OP = {'sum': 'op_sum', 'max': 'op_max', 'min': 'op_min'}
+CFUNC = {'exp': 'expf', 'tanh': 'tanhf', 'sqrt': 'sqrtf'}
+CTYPE = {'f32': 'float', 'f16': 'vh_half', 'i32': 'int'}
+ELEM_BYTES = {'f32': 4, 'f16': 2, 'i32': 4}
+
+
+@dataclass
+class Lowered:
+    src: str
+    params: list                  # (name, dtype, written) in kernel argument order
+    scratch: dict                 # host-visible name -> (offset, axes, static shape)
+    scratch_floats: int
+    shared_bytes: int             # dynamic LDS per block
+    barriers_per_launch: int
+    plan: list = field(default_factory=list)      # (statement, placement) for reading
+    sites: list = field(default_factory=list)     # timing: label of each timed site
+    counters: int = 2                             # length of the bar array
+    block: int = BLOCK
+    grid_max: int = GRID_MAX
+    shapes: dict = field(default_factory=dict)    # residue name -> shape
+    name: str = 'vesta_step'                      # the kernel's symbol
+
+
+# ------------------------------------------------------------------ AST helpers
+def is_node(e):
+    return isinstance(e, tuple) and bool(e) and isinstance(e[0], str)
+
+
+def nodes(e):
+    """Every expression node of e, parents first."""
+    if not is_node(e):
+        return
+    yield e
+    for x in e[1:]:
+        if isinstance(x, list):
+            for y in x:
+                yield from nodes(y)
+        elif is_node(x):
+            yield from nodes(x)
+
+
+def rebuild(e, f):
+    """Apply f bottom-up to every expression node."""
+    if not is_node(e):
+        return e
+    k = e[0]
+    if k == 'idx':
+        e = ('idx', e[1], [rebuild(i, f) for i in e[2]])
+    elif k == 'fold':
+        e = ('fold', e[1], e[2], rebuild(e[3], f))
+    elif k == 'neg':
+        e = ('neg', rebuild(e[1], f))
+    elif k == 'call':
+        e = ('call', e[1], rebuild(e[2], f))
+    elif k == 'bin':
+        e = ('bin', e[1], rebuild(e[2], f), rebuild(e[3], f))
+    elif k == 'fork':
+        e = ('fork', rebuild(e[1], f), rebuild(e[2], f), rebuild(e[3], f))
+    return f(e)
+
+
+def stmt_exprs(s):
+    k = s[0]
+    if k == 'let':
+        return [s[3]]
+    if k == 'emit':
+        return list(s[2]) + [s[3]]
+    if k == 'step':
+        return [s[4]]
+    if k == 'ret':
+        return [s[1]]
+    if k == 'axis':
+        return [s[2]]
+    return []
+
+
+def local_names(stmts, out=None):
+    out = set() if out is None else out
+    for s in stmts:
+        if s[0] in ('let', 'step'):
+            out.add(s[1])
+        if s[0] == 'step':
+            out.add(s[5])
+            local_names(s[6], out)
+    return out
+
+
+def batch_lift(stmts, B, per_token, bax='bt'):
+    """A batch is the same program asked of B tokens at once (reference
+    lower.py:109-132): every named value and every per-token residue gains a
+    leading token axis ``bax`` of extent B."""
+    locs = local_names(stmts)
+    per_token = set(per_token)
+
+    def f(e):
+        if e[0] == 'name' and e[1] in per_token and e[1] not in locs:
+            return ('idx', e[1], [('name', bax)])
+        if e[0] == 'idx' and (e[1] in locs or e[1] in per_token):
+            return ('idx', e[1], [('name', bax)] + list(e[2]))
+        return e
+
+    def lift(ss):
+        out = []
+        for s in ss:
+            k = s[0]
+            if k == 'axis':
+                out.append(('axis', s[1], rebuild(s[2], f)))
+            elif k == 'recv':
+                out.append(s)
+            elif k == 'emit':
+                ix = [rebuild(i, f) for i in s[2]]
+                out.append(('emit', s[1], ([('name', bax)] + ix) if s[1] in per_token else ix, rebuild(s[3], f)))
+            elif k == 'let':
+                out.append(('let', s[1], [bax] + list(s[2]), rebuild(s[3], f)))
+            elif k == 'step':
+                out.append(('step', s[1], [bax] + list(s[2]), s[3], rebuild(s[4], f), s[5], lift(s[6])))
+            elif k == 'ret':
+                out.append(('ret', rebuild(s[1], f)))
+        return out
+
+    return [('axis', bax, ('num', B))] + lift(stmts)
+
+
+def top_folds(e):
+    """Outermost fold nodes of e."""
+    if not is_node(e):
+        return []
+    if e[0] == 'fold':
+        return [e]
+    out = []
+    for x in e[1:]:
+        for y in (x if isinstance(x, list) else [x]):
+            out += top_folds(y)
+    return out
+
+
+def replace_node(e, target, repl):
+    """e with the node ``target`` (by identity) replaced by ``repl``."""
+    if e is target:
+        return repl
+    if not is_node(e):
+        return e
+    k = e[0]
+    if k == 'idx':
+        return ('idx', e[1], [replace_node(i, target, repl) for i in e[2]])
+    if k == 'fold':
+        return ('fold', e[1], e[2], replace_node(e[3], target, repl))
+    if k == 'neg':
+        return ('neg', replace_node(e[1], target, repl))
+    if k == 'call':
+        return ('call', e[1], replace_node(e[2], target, repl))
+    if k == 'bin':
+        return ('bin', e[1], replace_node(e[2], target, repl), replace_node(e[3], target, repl))
+    if k == 'fork':
+        return ('fork',) + tuple(replace_node(x, target, repl) for x in e[1:])
+    return e
+
+
+def show(e):
+    """Expression -> program-like text (for plans and comments)."""
+    if not is_node(e):
+        return str(e)
+    k = e[0]
+    if k == 'num':
+        return repr(e[1])
+    if k == 'name':
+        return e[1]
+    if k == 'neg':
+        return f'-{show(e[1])}'
+    if k == 'call':
+        return f'{e[1]}({show(e[2])})'
+    if k == 'bin':
+        return f'({show(e[2])} {e[1]} {show(e[3])})'
+    if k == 'fork':
+        return f'fork {show(e[1])} ? {show(e[2])} : {show(e[3])}'
+    if k == 'idx':
+        return f'{e[1]}[{", ".join(show(i) for i in e[2])}]'
+    if k == 'fold':
+        return f'fold {e[1]} {e[2]}: {show(e[3])}'
+    return str(e)
+
+
+def show_stmt(s):
+    if s[0] == 'let':
+        return f'{s[1]}[{", ".join(s[2])}] = {show(s[3])}'
+    if s[0] == 'emit':
+        return f'residue {s[1]}[{", ".join(show(i) for i in s[2])}] <- {show(s[3])}'
+    if s[0] == 'step':
+        return f'{s[1]}[{", ".join(s[2])}] = fold step {s[3]}: {show(s[4])} as {s[5]}'
+    return str(s)
+
+
+def c_float(v):
+    """A numeric literal as the fp32 constant NumPy would use (weak scalar)."""
+    f = float(np.float32(v))
+    if math.isinf(f):
+        return 'INFINITY' if f > 0 else '-INFINITY'
+    txt = repr(f)
+    if 'e' not in txt and '.' not in txt:
+        txt += '.0'
+    return txt + 'f'
+
+
+# ------------------------------------------------------------------ placements
+@dataclass
+class Contraction:
+    """A sum fold streaming residue W (tile or lane placement)."""
+    kind: str                 # 'tile' | 'lane'
+    fold: tuple               # the (outermost) fold node
+    fold_axes: list           # flattened fold axes, outermost first
+    W: str
+    widx: list                # W's index expressions
+    A: tuple                  # the other factor
+    epi: tuple                # the statement's expression with the fold replaced by ('name', '__acc')
+    contig: str               # the axis W is contiguous along (output axis j for tile, fold axis for lane)
+    reg_axes: list            # output axes W does not depend on
+    pt_axes: list             # output axes W depends on (besides contig for tile)
+    vec: int = 1
+
+
+class LowerError(ValueError):
+    pass
+
+
+class Lowering:
+    def __init__(self, stmts, res, axis_max, outputs, batch, timing=False):
+        self.res = {n: (tuple(int(x) for x in shp), dt) for n, (shp, dt) in res.items()}
+        self.axis_max = dict(axis_max or {})
+        self.outputs = set(outputs)
+        self.batch = batch
+        self.timing = timing
+        self.static = {}          # axis -> static extent (upper bound for dynamic ones)
+        self.dynamic = {}         # axis -> extent expression (run-time)
+        self.steps = set()        # step variables
+        self.step_ext = {}        # step variable -> loop count
+        self.axes_of = {}         # local -> axes
+        self.emitted = set()
+        self.alias = {}
+        self.tmp = 0
+        self.plan = []
+        self.sites = []
+        self.barriers = 0
+        self.mult = 1
+        self.fresh_id = 0
+        self.step_env = {}
+        self.fb_targets = set()
+        self.inlined = []
+        self.scan(stmts)
+        stmts = self.normalise(stmts)
+        stmts = self.hoist(stmts)
+        self.find_aliases(stmts)
+        stmts = self.inline(stmts)
+        self.stmts = stmts
+        self.place_all(stmts)
+        self.layout(stmts)
+
+    # ------------------------------------------------------------ program facts
+    def scan(self, ss):
+        for s in ss:
+            k = s[0]
+            if k == 'axis':
+                e = s[2]
+                if e[0] == 'num':
+                    self.static[s[1]] = int(e[1])
+                else:
+                    if s[1] not in self.axis_max:
+                        raise LowerError(f'axis {s[1]} is set at run time: give its upper bound in axis_max')
+                    self.static[s[1]] = int(self.axis_max[s[1]])
+                    self.dynamic[s[1]] = e
+            elif k == 'recv':
+                if s[1] not in self.res:
+                    raise NameError(f'residue {s[1]} not supplied')
+            elif k == 'emit':
+                if s[1] not in self.res:
+                    raise NameError(f'residue {s[1]} not supplied')
+                self.emitted.add(s[1])
+            elif k == 'let':
+                self.axes_of[s[1]] = tuple(s[2])
+            elif k == 'step':
+                self.steps.add(s[3])
+                self.axes_of[s[1]] = self.axes_of[s[5]] = tuple(s[2])
+                self.scan(s[6])
+
+    def is_axis(self, n):
+        return n in self.static and n not in self.steps
+
+    def ext_c(self, a):
+        """C expression of an axis extent."""
+        return f'E_{a}' if a in self.dynamic else str(self.static[a])
+
+    def size(self, axes):
+        return math.prod(self.static[a] for a in axes) if axes else 1
+
+    def normalise(self, ss):
+        """Bare reads of locals with axes become reads at their own axes."""
+        def f(e):
+            if e[0] == 'name' and e[1] in self.axes_of and self.axes_of[e[1]]:
+                return ('idx', e[1], [('name', a) for a in self.axes_of[e[1]]])
+            return e
+        out = []
+        for s in ss:
+            k = s[0]
+            if k == 'let':
+                out.append(('let', s[1], s[2], rebuild(s[3], f)))
+            elif k == 'emit':
+                out.append(('emit', s[1], [rebuild(i, f) for i in s[2]], rebuild(s[3], f)))
+            elif k == 'step':
+                out.append(('step', s[1], s[2], s[3], rebuild(s[4], f), s[5], self.normalise(s[6])))
+            elif k == 'ret':
+                out.append(('ret', rebuild(s[1], f)))
+            else:
+                out.append(s)
+        return out
+
+    def free_axes(self, e):
+        """Axes e depends on outside its own folds."""
+        if e[0] == 'name':
+            if self.is_axis(e[1]):
+                return {e[1]}
+            return set(self.axes_of.get(e[1], ()))
+        if e[0] == 'fold':
+            return self.free_axes(e[3]) - {e[2]}
+        out = set()
+        for x in e[1:]:
+            for y in (x if isinstance(x, list) else [x]):
+                if is_node(y):
+                    out |= self.free_axes(y)
+        return out
+
+    def reads(self, e):
+        """Names of locals and emitted residues e reads."""
+        out = set()
+        for n in nodes(e):
+            if n[0] in ('name', 'idx') and (n[1] in self.axes_of or n[1] in self.emitted):
+                out.add(n[1])
+        return out
+
+    def res_reads(self, e):
+        return [n for n in nodes(e) if n[0] == 'idx' and n[1] in self.res]
+
+    def big_reads(self, e):
+        return [n for n in self.res_reads(e)
+                if n[1] not in self.emitted and math.prod(self.res[n[1]][0]) > BIG]
+
+    def fold_work(self, e):
+        if not is_node(e):
+            return 1
+        if e[0] == 'fold':
+            return self.static[e[2]] * self.fold_work(e[3])
+        w = 1
+        for x in e[1:]:
+            for y in (x if isinstance(x, list) else [x]):
+                if is_node(y):
+                    w = max(w, self.fold_work(y))
+        return w
+
+    # ------------------------------------------------------------ rewrites
+    def hoist(self, ss):
+        """Lift folds that ignore an output axis into their own statement."""
+        out = []
+        for s in ss:
+            if s[0] == 'step':
+                out.append(s[:6] + (self.hoist(s[6]),))
+                continue
+            if s[0] != 'let':
+                out.append(s)
+                continue
+            name, axes, e = s[1], list(s[2]), s[3]
+            new = []
+
+            def lift(fnode):
+                fa = self.free_axes(fnode)
+                if fa >= set(axes) or not fa <= set(axes):
+                    return fnode
+                self.tmp += 1
+                h = f'_h{self.tmp}'
+                hax = [a for a in axes if a in fa]
+                self.axes_of[h] = tuple(hax)
+                new.append(('let', h, hax, fnode))
+                return ('idx', h, [('name', a) for a in hax]) if hax else ('name', h)
+
+            e2 = e
+            for fnode in top_folds(e):
+                e2 = replace_node(e2, fnode, lift(fnode))
+            out += new + [('let', name, axes, e2)]
+        return out
+
+    def find_aliases(self, ss):
+        """carry <- init / carry <- ret need no copy when the value is used
+        only there and its statement does not read the carry; the step's
+        result always shares the carry's storage."""
+        defs, uses = {}, {}
+
+        def index(ss):
+            for s in ss:
+                if s[0] == 'let':
+                    defs[s[1]] = s
+                for e in stmt_exprs(s):
+                    for n in nodes(e):
+                        if n[0] in ('name', 'idx') and n[1] in self.axes_of:
+                            uses[n[1]] = uses.get(n[1], 0) + 1
+                if s[0] == 'step':
+                    index(s[6])
+        index(ss)
+
+        def walk(ss):
+            for s in ss:
+                if s[0] != 'step':
+                    continue
+                _, name, axes, var, init, carry, blk = s
+                walk(blk)
+                rets = [b for b in blk if b[0] == 'ret']
+                if len(rets) != 1:
+                    raise SyntaxError(f'step {name} needs exactly one ->')
+                for e in (init, rets[0][1]):
+                    if e[0] == 'idx' and e[1] in defs and uses.get(e[1]) == 1 \
+                            and [('name', a) for a in self.axes_of[e[1]]] == list(e[2]) \
+                            and self.axes_of[e[1]] == tuple(axes) \
+                            and carry not in self.reads(defs[e[1]][3]) and e[1] not in self.outputs:
+                        self.alias[e[1]] = carry
+                self.alias[name] = carry
+        walk(ss)
+
+    def root(self, n):
+        while n in self.alias:
+            n = self.alias[n]
+        return n
+
+    def big_contraction(self, s):
+        e = s[3] if s[0] == 'let' else None
+        return e is not None and any(self.big_reads(f[3]) for f in top_folds(e))
+
+    def inline(self, ss):
+        """Substitute fold-free values into the statements that read them."""
+        out = list(ss)
+        i = 0
+        while i < len(out):
+            s = out[i]
+            if s[0] == 'step':
+                out[i] = s[:6] + (self.inline(s[6]),)
+                i += 1
+                continue
+            if s[0] != 'let':
+                i += 1
+                continue
+            name = s[1]
+
+            def reads_it(t):
+                if t[0] == 'step':
+                    return name in self.reads(t[4]) or any(reads_it(x) for x in t[6])
+                return any(name in self.reads(e) for e in stmt_exprs(t))
+            readers = [t for t in out[i + 1:] if reads_it(t)]
+            carries = set(self.alias.values())
+            if (readers and not top_folds(s[3]) and name not in self.outputs and name not in self.alias
+                    and name not in carries and all(t[0] in ('let', 'emit') and not self.big_contraction(t)
+                                                     for t in readers)):
+                axes, body = list(s[2]), s[3]
+
+                def subst(e, axes=axes, body=body, name=name):
+                    def f(n):
+                        if n[0] == 'idx' and n[1] == name:
+                            m = dict(zip(axes, n[2]))
+                            return rebuild(body, lambda x: m[x[1]] if x[0] == 'name' and x[1] in m else x)
+                        if n[0] == 'name' and n[1] == name:
+                            return body
+                        return n
+                    return rebuild(e, f)
+                for j in range(i + 1, len(out)):
+                    t = out[j]
+                    if t[0] == 'let':
+                        out[j] = ('let', t[1], t[2], subst(t[3]))
+                    elif t[0] == 'emit':
+                        out[j] = ('emit', t[1], [subst(x) for x in t[2]], subst(t[3]))
+                del out[i]
+                self.inlined.append(name)
+                continue
+            i += 1
+        return out
+
+    # ------------------------------------------------------------ placement
+    def place_all(self, ss):
+        self.place = {}           # id(stmt) -> placement string
+        self.info = {}            # id(stmt) -> Contraction / extra info
+        self.groups = {}          # id(first stmt) -> (lead axes, [stmts])
+        self.in_group = set()
+        self.private = set()
+        self._place_block(ss)
+
+    def priv_ok(self, s):
+        name = s[1]
+        if name in self.outputs or name in self.alias or name in set(self.alias.values()):
+            return False
+        size = self.size(s[2])
+        if size > PRIV_SIZE or size * self.fold_work(s[3]) > PRIV_WORK:
+            return False
+        if any(a in self.dynamic for a in s[2]):
+            return False
+        foot = sum(self.size(self.axes_of[n]) for n in self.reads(s[3]) if n in self.axes_of and n not in self.private)
+        if foot > STAGE_MAX:
+            return False
+        return not any(math.prod(self.res[n[1]][0]) > BIG or n[1] in self.emitted for n in self.res_reads(s[3]))
+
+    def _place_block(self, ss):
+        i = 0
+        made, made_axes = set(), None      # results of the last contraction and its epilogue
+        while i < len(ss):
+            s = ss[i]
+            if s[0] == 'step':
+                self._place_block(s[6])
+                made = set()
+                i += 1
+                continue
+            if s[0] != 'let':
+                i += 1
+                continue
+            c = self.contraction(s)
+            if c is not None:
+                self.place[id(s)] = c.kind
+                self.info[id(s)] = c
+                made, made_axes = {s[1]}, list(s[2])
+                i += 1
+                continue
+            if made and self.epilogue_ok(s, made, made_axes):
+                # an elementwise statement right after a contraction runs in its epilogue
+                self.place[id(s)] = 'epilogue'
+                made.add(s[1])
+                i += 1
+                continue
+            made = set()
+            if self.priv_ok(s):
+                self.place[id(s)] = 'private'
+                self.private.add(s[1])
+                i += 1
+                continue
+            g = self.gridred(s)
+            if g:
+                self.place[id(s)] = 'gridred'
+                i += 1
+                continue
+            run = self.group_run(ss, i)
+            if run:
+                lead, members = run
+                self.groups[id(members[0])] = (lead, members)
+                for t in members:
+                    self.place[id(t)] = 'group'
+                    self.in_group.add(id(t))
+                i += len(members)
+                continue
+            if self.block_ok(s):
+                self.groups[id(s)] = (list(s[2]), [s])
+                self.place[id(s)] = 'group'
+                self.in_group.add(id(s))
+                i += 1
+                continue
+            self.place[id(s)] = 'thread'
+            i += 1
+
+    def epilogue_ok(self, s, made, axes):
+        if list(s[2]) != axes or top_folds(s[3]) or s[1] in self.alias or s[1] in set(self.alias.values()):
+            return False
+        same = [('name', a) for a in axes]
+        hits = [n for n in nodes(s[3]) if n[0] == 'idx' and n[1] in made]
+        return bool(hits) and all(list(n[2]) == same for n in hits)
+
+    def block_ok(self, s):
+        """A long fold into many points: one block per point."""
+        e = s[3]
+        return (e[0] == 'fold' and s[2] and not any(a in self.dynamic for a in s[2])
+                and self.static[e[2]] >= 1024 and not self.big_reads(e)
+                and s[1] not in self.alias and s[1] not in set(self.alias.values()))
+
+    def group_ok(self, t, plen):
+        return (t[0] == 'let' and not self.big_reads(t[3]) and self.contraction(t) is None
+                and not self.priv_ok(t) and len(t[2]) >= plen
+                and not any(a in self.dynamic for a in t[2][:plen])
+                and self.size(t[2][plen:]) * self.fold_work(t[3]) <= GROUP_WORK
+                and t[1] not in self.alias and t[1] not in set(self.alias.values()))
+
+    def group_run(self, ss, i):
+        s = ss[i]
+        for plen in range(len(s[2]), 0, -1):
+            if not self.group_ok(s, plen):
+                continue
+            lead = list(s[2][:plen])
+            run, names = [s], {s[1]}
+            for t in ss[i + 1:]:
+                if t[0] != 'let' or list(t[2][:plen]) != lead or not self.group_ok(t, plen):
+                    break
+                bad = False
+                for n in nodes(t[3]):
+                    if n[0] == 'idx' and n[1] in names and list(n[2][:plen]) != [('name', a) for a in lead]:
+                        bad = True
+                if bad:
+                    break
+                run.append(t)
+                names.add(t[1])
+            if len(run) >= 2:
+                return lead, run
+        return None
+
+    def gridred(self, s):
+        e = s[3]
+        if e[0] != 'fold' or self.size(s[2]) > GRIDRED_POINTS or any(a in self.dynamic for a in s[2]):
+            return False
+        return e[2] in self.static and e[2] not in self.dynamic and self.static[e[2]] >= GRIDRED_MIN
+
+    def contraction(self, s):
+        """Tile or lane pattern of a let statement, or None."""
+        if s[0] != 'let':
+            return None
+        name, axes, e = s[1], list(s[2]), s[3]
+        tops = top_folds(e)
+        if len(tops) != 1 or tops[0][1] != 'sum':
+            return None
+        fold = tops[0]
+        fold_axes, body = [fold[2]], fold[3]
+        while body[0] == 'fold' and body[1] == 'sum':
+            fold_axes.append(body[2])
+            body = body[3]
+        if body[0] != 'bin' or body[1] != '*':
+            return None
+        if any(a in axes for a in fold_axes) or len(set(fold_axes)) != len(fold_axes):
+            return None
+        if any(not self.is_axis(a) for a in fold_axes):
+            return None
+        epi = replace_node(e, fold, ('name', '__acc'))
+        if '__acc' not in [n[1] for n in nodes(epi) if n[0] == 'name']:
+            return None
+        for W_node, A in ((body[3], body[2]), (body[2], body[3])):
+            if W_node[0] != 'idx' or W_node[1] not in self.res:
+                continue
+            W, widx = W_node[1], W_node[2]
+            shape, dt = self.res[W]
+            if dt not in ('f16', 'f32') or len(shape) != len(widx) or not shape:
+                continue
+            last = widx[-1]
+            if last[0] != 'name':
+                continue
+            contig = last[1]
+            others = set()
+            for x in widx[:-1]:
+                others |= self.free_axes(x)
+            if contig in others:
+                continue
+            w_axes = others | {contig}
+            a_free = self.free_axes(A) - set(fold_axes)
+            if not a_free <= set(axes):
+                continue
+            if not (self.free_axes(epi) - {'__acc'}) <= set(axes):
+                continue
+            reg = [a for a in axes if a not in w_axes]
+            pt = [a for a in axes if a in w_axes and a != contig]
+            if any(a in self.dynamic for a in reg):
+                continue
+            vec_for = {'f16': (8, 4, 2), 'f32': (4, 2)}[dt]
+            if contig in axes and len(fold_axes) >= 1 and contig not in fold_axes:
+                # tile: contiguous along an output axis
+                if contig in self.dynamic or contig in self.free_axes(A):
+                    continue
+                J = self.static[contig]
+                vec = next((v for v in vec_for if J % v == 0 and shape[-1] % v == 0), 1)
+                if self.size(reg) > 64:
+                    continue
+                return Contraction('tile', fold, fold_axes, W, widx, A, epi, contig, reg, pt, vec)
+            if len(fold_axes) == 1 and contig == fold_axes[0]:
+                # lane: contiguous along the fold axis
+                if contig in self.dynamic or self.static[contig] < LANE_MIN:
+                    continue
+                K = self.static[contig]
+                vec = next((v for v in vec_for if K % v == 0 and shape[-1] % v == 0), 1)
+                if self.size(reg) > 64:
+                    continue
+                return Contraction('lane', fold, fold_axes, W, widx, A, epi, contig, reg, pt, vec)
+        return None
+
+    # ------------------------------------------------------------ storage
+    def layout(self, ss):
+        """Global scratch for values shared across blocks; LDS for private
+        values (intervals over statement order, reused once dead)."""
+        order, live = [], {}
+
+        def flat(ss):
+            for s in ss:
+                if s[0] == 'step':
+                    start = len(order)
+                    flat(s[6])
+                    end = len(order)
+                    for n, (a, b) in list(live.items()):
+                        if a < start <= b < end or (a < start and b >= start):
+                            live[n] = (a, max(b, end))
+                    continue
+                order.append(s)
+                i = len(order) - 1
+                if s[0] == 'let' and s[1] in self.private:
+                    live.setdefault(s[1], (i, i))
+                for e in stmt_exprs(s):
+                    for n in self.reads(e):
+                        if n in live:
+                            live[n] = (live[n][0], i)
+        flat(ss)
+        self.lds = {}
+        used, top = [], 0
+        for n, (a, b) in sorted(live.items(), key=lambda kv: kv[1][0]):
+            size = self.size(self.axes_of[n])
+            used = [u for u in used if u[1] >= a]
+            off = 0
+            for lo, hi, uoff, usize in sorted(used, key=lambda u: u[2]):
+                if off + size <= uoff:
+                    break
+                off = max(off, uoff + usize)
+            if off + size > PRIV_BUDGET:
+                raise LowerError(f'private values exceed the LDS budget at {n}')
+            used.append((a, b, off, size))
+            self.lds[n] = off
+            top = max(top, off + size)
+        self.lds_floats = top
+        self.g, self.goff = {}, 0
+        for n in self.axes_of:
+            r = self.root(n)
+            if r in self.private or r in self.g or n in self.inlined:
+                continue
+            self.g[r] = self.goff
+            self.goff += max(1, self.size(self.axes_of[r]))
+        self.counters = BAR_WORDS
+        self.staged = {}
+        self.stage_floats = 0
+
+    def alloc_scratch(self, n):
+        off = self.goff
+        self.goff += n
+        return off
+
+    def alloc_counters(self, n):
+        """n counters, one 128-byte line each; counter i is at offset + i * LINE_WORDS."""
+        off = self.counters
+        self.counters += n * LINE_WORDS
+        return off
+
+    def strides(self, axes):
+        st, acc = [], 1
+        for a in reversed(axes):
+            st.append(acc)
+            acc *= self.static[a]
+        return list(reversed(st))
+
+    # ------------------------------------------------------------ expressions
+    def fresh(self, base):
+        self.fresh_id += 1
+        return f'{base}{self.fresh_id}'
+
+    def expr(self, e, env, out, ind):
+        """C code of e as (text, type); type is 'int', 'float' or 'bool'.
+        Folds inside e become serial loops appended to ``out``."""
+        k = e[0]
+        if k == 'num':
+            v = e[1]
+            if isinstance(v, int) and not isinstance(v, bool):
+                return str(v), 'int'
+            return c_float(v), 'float'
+        if k == 'name':
+            n = e[1]
+            if n in env:
+                return env[n]
+            if n in self.step_env:
+                return self.step_env[n]
+            if n in self.axes_of:
+                if self.axes_of[n]:
+                    raise LowerError(f'{n} read without its axes')
+                return self.load(n, []), 'float'
+            if n in self.res:
+                shape, dt = self.res[n]
+                if math.prod(shape) != 1:
+                    raise LowerError(f'residue {n} read without an index')
+                if n in self.emitted:
+                    return self.res_value(n, '0')
+                return f'rs_{n}', ('int' if dt == 'i32' else 'float')
+            if n in self.static:
+                raise LowerError(f'axis {n} is not bound here')
+            raise NameError(n)
+        if k == 'neg':
+            a, t = self.expr(e[1], env, out, ind)
+            return f'(-{self.as_num(a, t)})', ('int' if t == 'int' else 'float')
+        if k == 'call':
+            a, t = self.expr(e[2], env, out, ind)
+            return f'{CFUNC[e[1]]}({self.as_float(a, t)})', 'float'
+        if k == 'bin':
+            op = e[1]
+            a, ta = self.expr(e[2], env, out, ind)
+            b, tb = self.expr(e[3], env, out, ind)
+            if op in ('==', '<', '>', '<=', '>='):
+                if ta == 'int' and tb == 'int':
+                    return f'({a} {op} {b})', 'bool'
+                return f'({self.as_float(a, ta)} {op} {self.as_float(b, tb)})', 'bool'
+            if op == '/':
+                return f'({self.as_float(a, ta)} / {self.as_float(b, tb)})', 'float'
+            if ta == 'int' and tb == 'int':
+                return f'({a} {op} {b})', 'int'
+            return f'({self.as_float(a, ta)} {op} {self.as_float(b, tb)})', 'float'
+        if k == 'fork':
+            c, tc = self.expr(e[1], env, out, ind)
+            a, ta = self.expr(e[2], env, out, ind)
+            b, tb = self.expr(e[3], env, out, ind)
+            cond = c if tc == 'bool' else f'({self.as_float(c, tc)} != 0.0f)'
+            if ta == 'int' and tb == 'int':
+                return f'({cond} ? {a} : {b})', 'int'
+            return f'({cond} ? {self.as_float(a, ta)} : {self.as_float(b, tb)})', 'float'
+        if k == 'idx':
+            n = e[1]
+            ix = [self.index(x, env, out, ind) for x in e[2]]
+            if n in self.res:
+                shape = self.res[n][0]
+                if len(ix) != len(shape):
+                    raise LowerError(f'residue {n} has {len(shape)} axes, indexed with {len(ix)}')
+                ix = [self.clamp(i, x, d) for i, x, d in zip(ix, e[2], shape)]
+                return self.res_value(n, self.addr(ix, self.res_strides(n)))
+            if n in self.axes_of:
+                if len(ix) != len(self.axes_of[n]):
+                    raise LowerError(f'{n} has axes {self.axes_of[n]}, indexed with {len(ix)}')
+                return self.load(n, ix), 'float'
+            raise NameError(n)
+        if k == 'fold':
+            op, ax, body = e[1], e[2], e[3]
+            if ax not in self.static:
+                raise ValueError(f'fold over unknown axis {ax}')
+            acc = self.fresh('acc')
+            kv = self.fresh(f'k_{ax}_')
+            out.append(f'{ind}float {acc} = {FOLD_INIT[op]};')
+            out.append(f'{ind}#pragma unroll 8')
+            out.append(f'{ind}for (int {kv} = 0; {kv} < {self.ext_c(ax)}; ++{kv}) {{')
+            inner = []
+            v, t = self.expr(body, {**env, ax: (kv, 'int')}, inner, ind + '  ')
+            out += inner
+            out.append(f'{ind}  {acc} = {FOLD_OP[op]}({acc}, {self.as_float(v, t)});')
+            out.append(f'{ind}}}')
+            return acc, 'float'
+        raise LowerError(f'cannot lower {e}')
+
+    def as_float(self, a, t):
+        if t == 'float':
+            return a
+        return f'((float){a})'
+
+    def as_num(self, a, t):
+        return f'((float){a})' if t == 'bool' else a
+
+    def index(self, e, env, out, ind):
+        v, t = self.expr(e, env, out, ind)
+        if t == 'int':
+            return v
+        if t == 'float' and e[0] == 'idx' and e[1] in self.axes_of:
+            return f'((int){v})'
+        raise LowerError(f'index {show(e)} is not an integer')
+
+    def data_dependent(self, e):
+        """Does index expression e depend on stored data (not only on axes)?"""
+        return any(n[0] == 'idx' or (n[0] == 'name' and (n[1] in self.res or n[1] in self.axes_of))
+                   for n in nodes(e))
+
+    def clamp(self, i, e, dim):
+        """An index computed from data is kept inside the residue, so a bad
+        token id or position cannot read or write outside the buffer."""
+        if not self.data_dependent(e):
+            return i
+        return f'min(max({i}, 0), {dim - 1})'
+
+    def addr(self, ix, strides):
+        terms = []
+        for i, s in zip(ix, strides):
+            if i == '0':
+                continue
+            terms.append(i if s == 1 else f'({i}) * {s}')
+        return ' + '.join(terms) if terms else '0'
+
+    def res_strides(self, n):
+        shape = self.res[n][0]
+        st, acc = [], 1
+        for d in reversed(shape):
+            st.append(acc)
+            acc *= d
+        return list(reversed(st))
+
+    def coherent(self, n):
+        """Residues written during a launch (emits, feedback targets) are
+        read and written through the coherent path."""
+        return n in self.emitted or n in self.fb_targets
+
+    def res_value(self, n, addr):
+        dt = self.res[n][1]
+        if self.coherent(n):
+            if dt == 'f16':
+                return f'ldc_h(rb_{n}, {addr})', 'float'
+            if dt == 'f32':
+                return f'ldc(R_{n} + {addr})', 'float'
+            return f'ldc_i(R_{n} + {addr})', 'int'
+        if dt == 'f16':
+            return f'h2f(R_{n}[{addr}])', 'float'
+        if dt == 'f32':
+            return f'R_{n}[{addr}]', 'float'
+        return f'R_{n}[{addr}]', 'int'
+
+    def load(self, n, ix):
+        """A local: LDS if private or staged, else a coherent load of global scratch."""
+        r = self.root(n)
+        a = self.addr(ix, self.strides(self.axes_of[r]))
+        if r in self.private:
+            return f'sh_f[{self.lds[r]} + {a}]'
+        if r in self.staged:
+            return f'sh_f[{self.staged[r]} + {a}]'
+        return f'ldc(S + {self.g[r]} + {a})'
+
+    def store(self, n, ix, v, t):
+        r = self.root(n)
+        a = self.addr(ix, self.strides(self.axes_of[r]))
+        if r in self.private:
+            return f'sh_f[{self.lds[r]} + {a}] = {self.as_float(v, t)};'
+        return f'stc(S + {self.g[r]} + {a}, {self.as_float(v, t)});'
+
+    def decode(self, var, axes, out, ind, prefix='i_'):
+        """Lines binding prefix+axis for each axis from flat index ``var``
+        (last axis fastest); returns the env entries."""
+        env = {}
+        if not axes:
+            return env
+        if len(axes) == 1:
+            out.append(f'{ind}const int {prefix}{axes[0]} = {var};')
+            env[axes[0]] = (f'{prefix}{axes[0]}', 'int')
+            return env
+        rem = self.fresh('r')
+        out.append(f'{ind}int {rem} = {var};')
+        for a in reversed(axes[1:]):
+            out.append(f'{ind}const int {prefix}{a} = {rem} % {self.ext_c(a)}; {rem} /= {self.ext_c(a)};')
+            env[a] = (f'{prefix}{a}', 'int')
+        out.append(f'{ind}const int {prefix}{axes[0]} = {rem};')
+        env[axes[0]] = (f'{prefix}{axes[0]}', 'int')
+        return env
+
+    def count_c(self, axes):
+        if not axes:
+            return '1'
+        return ' * '.join(self.ext_c(a) for a in axes)
+
+    # ------------------------------------------------------------ hazards
+    def root_reads(self, exprs, exclude=()):
+        out = set()
+        for e in exprs:
+            for n in self.reads(e):
+                if n in exclude:
+                    continue
+                out.add(self.root(n) if n in self.axes_of else n)
+        return out
+
+    def sync(self, reads, writes, out, ind, what):
+        """Grid barrier if a read sees a value written since the last barrier
+        or a write overwrites one read since then (by another site)."""
+        gl_reads = {n for n in reads if n not in self.private}
+        gl_writes = {n for n in writes if n not in self.private}
+        if (gl_reads & self.dirty) or (gl_writes & self.readers) or (gl_writes & self.dirty):
+            self.barrier(out, ind, what)
+        self.readers |= gl_reads
+
+    def barrier(self, out, ind, what=''):
+        out.append(f'{ind}grid_sync(bar, nblk, bgen_);' + (f'  // before {what}' if what else ''))
+        self.barriers += self.mult
+        self.dirty, self.readers = set(), set()
+        self.mark(out, ind, f'barrier before {what}')
+
+    def mark(self, out, ind, label):
+        if not self.timing:
+            return
+        k = len(self.sites)
+        if k >= 1024:
+            return
+        self.sites.append(label)
+        out.append(f'{ind}if (gtid == 0) {{ unsigned long long tn_ = vh_clock(); TS[{k}] += tn_ - tlast_; '
+                   f'tlast_ = tn_; }}')
+
+    # ------------------------------------------------------------ statements
+    def gen(self, ss, out, ind):
+        i = 0
+        while i < len(ss):
+            s = ss[i]
+            k = s[0]
+            if k in ('axis', 'recv', 'ret'):
+                i += 1
+                continue
+            if k == 'step':
+                self.gen_step(s, out, ind)
+                i += 1
+                continue
+            if k == 'emit':
+                self.gen_emit(s, out, ind)
+                i += 1
+                continue
+            if id(s) in self.groups:
+                lead, members = self.groups[id(s)]
+                self.gen_group(lead, members, out, ind)
+                i += len(members)
+                continue
+            p = self.place[id(s)]
+            if p == 'private':
+                run = [s]
+                while i + len(run) < len(ss) and ss[i + len(run)][0] == 'let' \
+                        and self.place.get(id(ss[i + len(run)])) == 'private':
+                    run.append(ss[i + len(run)])
+                self.gen_private(run, out, ind)
+                i += len(run)
+                continue
+            if p in ('tile', 'lane'):
+                fused = self.fusable(ss, i)
+                if p == 'tile':
+                    self.gen_tile(s, self.info[id(s)], fused, out, ind)
+                else:
+                    self.gen_lane(s, self.info[id(s)], fused, out, ind)
+                i += 1 + len(fused)
+                continue
+            if p == 'gridred':
+                self.gen_gridred(s, out, ind)
+            else:                   # thread, or an epilogue statement its contraction could not take
+                self.gen_thread(s, out, ind)
+            i += 1
+
+    # -- fusion into an epilogue
+    def fusable(self, ss, i):
+        """Statements right after contraction ss[i] that its epilogue can run:
+        same-point elementwise lets and emits whose value reads the result at
+        an invertible affine index."""
+        s = ss[i]
+        axes = list(s[2])
+        made = {s[1]}
+        fused = []
+        for t in ss[i + 1:]:
+            if t[0] == 'let':
+                if (list(t[2]) != axes or top_folds(t[3]) or self.place.get(id(t)) in ('private', 'group')
+                        or id(t) in self.groups or t[1] in self.private):
+                    break
+                ok = True
+                for n in nodes(t[3]):
+                    if n[0] == 'idx' and n[1] in made and list(n[2]) != [('name', a) for a in axes]:
+                        ok = False
+                    if n[0] in ('name', 'idx') and n[1] not in made:
+                        nm = n[1]
+                        r = self.root(nm) if nm in self.axes_of else nm
+                        if r in self.dirty or (nm in self.emitted):
+                            ok = False
+                if not ok or self.root(t[1]) in self.readers:
+                    break
+                fused.append(('let', t, None))
+                made.add(t[1])
+                continue
+            if t[0] == 'emit':
+                inv = self.emit_inverse(t, made, axes)
+                if inv is None:
+                    break
+                fused.append(('emit', t, inv))
+                continue
+            break
+        return fused
+
+    def emit_inverse(self, t, made, axes):
+        """For an emit whose value reads one value made here at an affine
+        index of the emit's axes: how to recover those axes from the point."""
+        reads = [n for n in nodes(t[3]) if n[0] == 'idx' and n[1] in made]
+        if len(reads) != 1 or any(n[0] == 'name' and n[1] in made for n in nodes(t[3])):
+            return None
+        src = reads[0]
+        for e in t[2]:
+            if any(n[0] in ('name', 'idx') and n[1] in made for n in nodes(e)):
+                return None
+        e_axes = set()
+        for e in list(t[2]) + [t[3]]:
+            e_axes |= self.free_axes(e)
+        e_axes = [a for a in e_axes if self.is_axis(a)]
+        for n in nodes(t[3]):
+            if n[0] in ('name', 'idx') and n[1] not in made:
+                nm = n[1]
+                r = self.root(nm) if nm in self.axes_of else nm
+                if r in self.dirty or nm in self.emitted:
+                    return None
+        # each position of the source index: an affine form over emit axes
+        plan = []
+        seen = set()
+        for pos, ie in enumerate(src[2]):
+            aff = self.affine(ie)
+            if aff is None:
+                return None
+            const, coefs = aff
+            for a in coefs:
+                if a not in e_axes or a in seen:
+                    return None
+                seen.add(a)
+            terms = sorted(coefs.items(), key=lambda kv: kv[1])
+            radix = 1
+            for a, c in terms:
+                if c != radix or a in self.dynamic:
+                    return None
+                radix *= self.static[a]
+            plan.append((axes[pos], const, [a for a, _ in reversed(terms)], radix))
+        if set(e_axes) != seen:
+            return None
+        return src, plan
+
+    def affine(self, e):
+        """(const, {axis: coef}) if e is an integer affine form of axes."""
+        k = e[0]
+        if k == 'num':
+            return (int(e[1]), {}) if isinstance(e[1], int) else None
+        if k == 'name':
+            return (0, {e[1]: 1}) if self.is_axis(e[1]) else None
+        if k == 'bin' and e[1] in ('+', '-'):
+            a, b = self.affine(e[2]), self.affine(e[3])
+            if a is None or b is None:
+                return None
+            sg = 1 if e[1] == '+' else -1
+            coefs = dict(a[1])
+            for n, c in b[1].items():
+                coefs[n] = coefs.get(n, 0) + sg * c
+            return a[0] + sg * b[0], {n: c for n, c in coefs.items() if c}
+        if k == 'bin' and e[1] == '*':
+            a, b = self.affine(e[2]), self.affine(e[3])
+            if a is None or b is None:
+                return None
+            if not a[1]:
+                a, b = b, a
+            if b[1]:
+                return None
+            return a[0] * b[0], {n: c * b[0] for n, c in a[1].items()}
+        return None
+
+    def epilogue(self, s, c, fused, env, value, out, ind):
+        """Store the contraction's result at the point bound in env, then run
+        the fused statements for that point."""
+        name, axes = s[1], list(s[2])
+        venv = dict(env)
+        venv['__acc'] = (value, 'float')
+        v, t = self.expr(c.epi, venv, out, ind)
+        cur = self.fresh('v')
+        out.append(f'{ind}const float {cur} = {self.as_float(v, t)};')
+        ix = [env[a][0] for a in axes]
+        out.append(f'{ind}{self.store(name, ix, cur, "float")}')
+        made = {name: cur}
+        for kind, t_, inv in fused:
+            if kind == 'let':
+                def sub(n, made=made):
+                    if n[0] == 'idx' and n[1] in made:
+                        return ('name', '__cur_' + n[1])
+                    return n
+                e2 = rebuild(t_[3], sub)
+                fenv = dict(env)
+                for m, cv in made.items():
+                    fenv['__cur_' + m] = (cv, 'float')
+                v2, t2 = self.expr(e2, fenv, out, ind)
+                nv = self.fresh('v')
+                out.append(f'{ind}const float {nv} = {self.as_float(v2, t2)};')
+                out.append(f'{ind}{self.store(t_[1], [env[a][0] for a in t_[2]], nv, "float")}')
+                made[t_[1]] = nv
+            else:
+                src, plan = inv
+                lines, cond, eenv = [], [], dict(env)
+                for axis, const, order, radix in plan:
+                    rel = self.fresh('rel')
+                    lines.append(f'const int {rel} = {env[axis][0]} - ({const});')
+                    cond.append(f'{rel} >= 0 && {rel} < {radix}')
+                    rem = rel
+                    r2 = radix
+                    for a in order:
+                        r2 //= self.static[a]
+                        lines.append(f'const int i_{a} = ({rem}) / {r2};' if r2 > 1 else f'const int i_{a} = {rem};')
+                        if r2 > 1:
+                            nr = self.fresh('rm')
+                            lines.append(f'const int {nr} = ({rem}) % {r2};')
+                            rem = nr
+                        eenv[a] = (f'i_{a}', 'int')
+                out.append(f'{ind}{{')
+                for ln in lines:
+                    out.append(f'{ind}  {ln}')
+                out.append(f'{ind}  if ({" && ".join(cond)}) {{')
+                e2 = replace_node(t_[3], src, ('name', '__cur_' + src[1]))
+                for m, cv in made.items():
+                    eenv['__cur_' + m] = (cv, 'float')
+                inner = []
+                ix = [self.index(x, eenv, inner, ind + '    ') for x in t_[2]]
+                v2, t2 = self.expr(e2, eenv, inner, ind + '    ')
+                out += inner
+                out.append(f'{ind}    {self.res_store(t_[1], ix, v2, t2, t_[2])}')
+                out.append(f'{ind}  }}')
+                out.append(f'{ind}}}')
+
+    def res_store(self, n, ix, v, t, exprs=None):
+        dt = self.res[n][1]
+        if exprs is not None:
+            ix = [self.clamp(i, x, d) for i, x, d in zip(ix, exprs, self.res[n][0])]
+        a = self.addr(ix, self.res_strides(n))
+        if dt == 'f16':
+            return f'stc_h(rb_{n}, {a}, {self.as_float(v, t)});'
+        if dt == 'f32':
+            return f'stc(R_{n} + {a}, {self.as_float(v, t)});'
+        return f'stc_i(R_{n} + {a}, (int)({v}));'
+
+    def site_io(self, s, c, fused):
+        exprs = [s[3]]
+        writes = {self.root(s[1])}
+        for kind, t, _ in fused:
+            exprs += stmt_exprs(t)
+            writes.add(self.root(t[1]) if kind == 'let' else t[1])
+        made = {s[1]} | {t[1] for kind, t, _ in fused if kind == 'let'}
+        return self.root_reads(exprs, exclude=made), writes
+
+    def note(self, reads, writes):
+        self.dirty |= {n for n in writes if n not in self.private}
+
+    # -- tile
+    def gen_tile(self, s, c, fused, out, ind):
+        name, axes = s[1], list(s[2])
+        reads, writes = self.site_io(s, c, fused)
+        self.sync(reads, writes, out, ind, name)
+        self.plan.append((show_stmt(s), 'tile' + (f' +{len(fused)} fused' if fused else '')))
+        for _, t, _ in fused:
+            self.plan.append((show_stmt(t), f'epilogue of {name}'))
+        dt = self.res[c.W][1]
+        vec = c.vec
+        J = self.static[c.contig]
+        nvec = J // vec
+        lpr = 1
+        while lpr * 2 <= TILE_LANES and nvec % (lpr * 2) == 0:
+            lpr *= 2
+        tj = lpr * vec
+        nj = J // tj
+        rpw = WAVE // lpr
+        rpb = rpw * NWAVE
+        reg = c.reg_axes
+        rn = self.size(reg)
+        chunks = [reg[:]]           # register rows are processed in chunks of REG_MAX
+        rch = min(rn, REG_MAX)
+        nrch = (rn + rch - 1) // rch
+        pt = c.pt_axes
+        npt_max = self.size(pt)
+        nt_max = npt_max * nj * nrch
+        poff = self.alloc_scratch(nt_max * KCAP * rch * tj)
+        coff = self.alloc_counters(nt_max)
+        self.red_floats = max(getattr(self, 'red_floats', 4), NWAVE * rch * tj)
+        I = ind + '  '
+        o = out
+        o.append(f'{ind}{{  // tile {name}: W={c.W} VEC={vec} lanes/row={lpr} cols/tile={tj} reg={rn}')
+        o.append(f'{I}const int K_ = {self.count_c(c.fold_axes)};')
+        o.append(f'{I}const int NT_ = {self.count_c(pt)} * {nj * nrch};')
+        o.append(f'{I}int ks_ = (int)nblk / NT_; ks_ = ks_ < 1 ? 1 : (ks_ > {KCAP} ? {KCAP} : ks_);')
+        o.append(f'{I}{{ const int mk_ = (K_ + {rpb - 1}) / {rpb}; if (ks_ > mk_) ks_ = mk_; if (ks_ < 1) ks_ = 1; }}')
+        o.append(f'{I}const int rows_ = (K_ + ks_ - 1) / ks_;')
+        o.append(f'{I}const int nitem_ = NT_ * ks_;')
+        o.append(f'{I}const int sub_ = lane / {lpr}, cl_ = lane % {lpr};')
+        o.append(f'{I}for (int it_ = blockIdx.x; it_ < nitem_; it_ += nblk) {{')
+        J2 = I + '  '
+        o.append(f'{J2}const int c_ = it_ % ks_, tl_ = it_ / ks_;')
+        o.append(f'{J2}const int jt_ = tl_ % {nj}; int pq_ = tl_ / {nj};')
+        o.append(f'{J2}const int rc_ = pq_ % {nrch}; pq_ /= {nrch};')
+        env = self.decode('pq_', pt, o, J2)
+        o.append(f'{J2}const int jc_ = jt_ * {tj} + cl_ * {vec};')
+        o.append(f'{J2}float acc_[{rch}][{vec}];')
+        o.append(f'{J2}#pragma unroll')
+        o.append(f'{J2}for (int r_ = 0; r_ < {rch}; ++r_)')
+        o.append(f'{J2}  #pragma unroll')
+        o.append(f'{J2}  for (int v_ = 0; v_ < {vec}; ++v_) acc_[r_][v_] = 0.0f;')
+        o.append(f'{J2}const int k0_ = c_ * rows_;')
+        o.append(f'{J2}const int k1_ = k0_ + rows_ < K_ ? k0_ + rows_ : K_;')
+        o.append(f'{J2}const int kb_ = k0_ + wave * {rpw} + sub_;')
+        o.append(f'{J2}const int n_ = kb_ < k1_ ? (k1_ - kb_ + {rpb - 1}) / {rpb} : 0;')
+        o.append(f'{J2}for (int b_ = 0; b_ < n_; b_ += {UNROLL}) {{')
+        K3 = J2 + '  '
+        ltype = {8: 'vh_u32x4', 4: 'vh_u32x2', 2: 'unsigned', 1: 'vh_half'}[vec] if dt == 'f16' else \
+            {4: 'vh_f32x4', 2: 'vh_f32x2', 1: 'float'}[vec]
+        o.append(f'{K3}{ltype} wq_[{UNROLL}];')
+        o.append(f'{K3}float av_[{UNROLL}][{rch}];')
+        o.append(f'{K3}#pragma unroll')
+        o.append(f'{K3}for (int u_ = 0; u_ < {UNROLL}; ++u_) {{')
+        K4 = K3 + '  '
+        o.append(f'{K4}if (b_ + u_ < n_) {{')
+        K5 = K4 + '  '
+        o.append(f'{K5}const int kr_ = kb_ + (b_ + u_) * {rpb};')
+        kenv = self.decode('kr_', c.fold_axes, o, K5, prefix='f_')
+        wenv = {**env, **kenv, c.contig: ('jc_', 'int')}
+        for a in reg:
+            wenv[a] = ('0', 'int')
+        pre = []
+        wix = [self.index(x, wenv, pre, K5) for x in c.widx]
+        o += pre
+        waddr = self.addr(wix, self.res_strides(c.W))
+        o.append(f'{K5}wq_[u_] = {self.vec_load(dt, vec, c.W, waddr)};')
+        # the other factor for every register row, read in the same batch as the weights
+        for r in range(rch):
+            renv = {**env, **kenv}
+            if reg:
+                rl = []
+                renv.update(self.decode_const(f'(rc_ * {rch} + {r})', reg, rl, K5))
+                o += rl
+            pre = []
+            av, at = self.expr(c.A, renv, pre, K5)
+            o += pre
+            if rn % rch:
+                o.append(f'{K5}av_[u_][{r}] = (rc_ * {rch} + {r} < {rn}) ? {self.as_float(av, at)} : 0.0f;')
+            else:
+                o.append(f'{K5}av_[u_][{r}] = {self.as_float(av, at)};')
+        o.append(f'{K4}}} else {{')
+        o.append(f'{K5}wq_[u_] = {self.vec_zero(dt, vec)};')
+        o.append(f'{K5}#pragma unroll')
+        o.append(f'{K5}for (int r_ = 0; r_ < {rch}; ++r_) av_[u_][r_] = 0.0f;')
+        o.append(f'{K4}}}')
+        o.append(f'{K3}}}')
+        o.append(f'{K3}#pragma unroll')
+        o.append(f'{K3}for (int u_ = 0; u_ < {UNROLL}; ++u_) {{')
+        o.append(f'{K4}float wf_[{vec}];')
+        o.append(f'{K4}{self.vec_unpack(dt, vec, "wq_[u_]", "wf_")}')
+        o.append(f'{K4}#pragma unroll')
+        o.append(f'{K4}for (int r_ = 0; r_ < {rch}; ++r_)')
+        o.append(f'{K4}  #pragma unroll')
+        o.append(f'{K4}  for (int v_ = 0; v_ < {vec}; ++v_) acc_[r_][v_] = fmaf(av_[u_][r_], wf_[v_], acc_[r_][v_]);')
+        o.append(f'{K3}}}')
+        o.append(f'{J2}}}')
+        # reduce over rows inside the wave, then across waves through LDS
+        if lpr < 64:
+            o.append(f'{J2}#pragma unroll')
+            o.append(f'{J2}for (int r_ = 0; r_ < {rch}; ++r_)')
+            o.append(f'{J2}  #pragma unroll')
+            o.append(f'{J2}  for (int v_ = 0; v_ < {vec}; ++v_) acc_[r_][v_] = wave_red_sum_hi(acc_[r_][v_], {lpr});')
+        o.append(f'{J2}if (sub_ == 0) {{')
+        o.append(f'{J2}  #pragma unroll')
+        o.append(f'{J2}  for (int r_ = 0; r_ < {rch}; ++r_)')
+        o.append(f'{J2}    #pragma unroll')
+        o.append(f'{J2}    for (int v_ = 0; v_ < {vec}; ++v_) red_sh[(wave * {rch} + r_) * {tj} + cl_ * {vec} + v_] = '
+                 f'acc_[r_][v_];')
+        o.append(f'{J2}}}')
+        o.append(f'{J2}__syncthreads();')
+        q = rch * tj
+
+        def finish(val, lines, ind2):
+            lines.append(f'{ind2}const int r_ = q_ / {tj}, col_ = q_ % {tj};')
+            fenv = dict(env)
+            if reg:
+                lines.append(f'{ind2}const int rf_ = rc_ * {rch} + r_;')
+                fenv.update(self.decode('rf_', reg, lines, ind2))
+                lines.append(f'{ind2}if (rf_ < {rn}) {{')
+                ind3 = ind2 + '  '
+            else:
+                ind3 = ind2
+            lines.append(f'{ind3}const int i_{c.contig} = jt_ * {tj} + col_;')
+            fenv[c.contig] = (f'i_{c.contig}', 'int')
+            self.epilogue(s, c, fused, fenv, val, lines, ind3)
+            if reg:
+                lines.append(f'{ind2}}}')
+
+        o.append(f'{J2}if (ks_ == 1) {{')
+        o.append(f'{J2}  for (int q_ = tid; q_ < {q}; q_ += {BLOCK}) {{')
+        o.append(f'{J2}    const float s_ = red_sh[q_] + red_sh[{q} + q_] + red_sh[{2 * q} + q_] + red_sh[{3 * q} + q_];')
+        finish('s_', o, J2 + '    ')
+        o.append(f'{J2}  }}')
+        o.append(f'{J2}}} else {{')
+        o.append(f'{J2}  for (int q_ = tid; q_ < {q}; q_ += {BLOCK})')
+        o.append(f'{J2}    stc(S + {poff} + (size_t)it_ * {q} + q_, red_sh[q_] + red_sh[{q} + q_] + red_sh[{2 * q} + q_] '
+                 f'+ red_sh[{3 * q} + q_]);')
+        o.append(f'{J2}  if (last_arrival(bar + {coff} + tl_ * {LINE_WORDS}, (unsigned)ks_, &flag_sh)) {{')
+        o.append(f'{J2}    for (int q_ = tid; q_ < {q}; q_ += {BLOCK}) {{')
+        o.append(f'{J2}      float p_[{KCAP}];')
+        o.append(f'{J2}      #pragma unroll')
+        o.append(f'{J2}      for (int c2_ = 0; c2_ < {KCAP}; ++c2_) '
+                 f'p_[c2_] = c2_ < ks_ ? ldc(S + {poff} + (size_t)(tl_ * ks_ + c2_) * {q} + q_) : 0.0f;')
+        o.append(f'{J2}      float s_ = p_[0];')
+        o.append(f'{J2}      #pragma unroll')
+        o.append(f'{J2}      for (int c2_ = 1; c2_ < {KCAP}; ++c2_) if (c2_ < ks_) s_ += p_[c2_];')
+        finish('s_', o, J2 + '      ')
+        o.append(f'{J2}    }}')
+        o.append(f'{J2}  }}')
+        o.append(f'{J2}}}')
+        o.append(f'{J2}__syncthreads();')
+        o.append(f'{I}}}')
+        o.append(f'{ind}}}')
+        self.note(reads, writes)
+        self.mark(out, ind, f'tile {name}')
+
+    def decode_const(self, flat, axes, out, ind):
+        """Bind axes from a flat index expression (row-major)."""
+        v = self.fresh('rr')
+        out.append(f'{ind}const int {v} = {flat};')
+        return self.decode(v, axes, out, ind, prefix=self.fresh('g') + '_')
+
+    def vec_load(self, dt, vec, W, addr):
+        if self.coherent(W):
+            if dt == 'f16' and vec == 8:
+                return f'ldc16_h(rb_{W}, {addr})'
+            if dt == 'f16' and vec == 4:
+                return f'ldc8_h(rb_{W}, {addr})'
+            raise LowerError(f'coherent load of {W}: vector width {vec} ({dt}) not supported')
+        if dt == 'f16':
+            if vec == 8:
+                return f'ld16_nt(R_{W} + {addr})'
+            if vec == 4:
+                return f'ld8_nt(R_{W} + {addr})'
+            if vec == 2:
+                return f'*(const unsigned*)(R_{W} + {addr})'
+            return f'R_{W}[{addr}]'
+        if vec == 4:
+            return f'__builtin_nontemporal_load((const vh_f32x4*)(R_{W} + {addr}))'
+        if vec == 2:
+            return f'*(const vh_f32x2*)(R_{W} + {addr})'
+        return f'R_{W}[{addr}]'
+
+    def vec_zero(self, dt, vec):
+        if dt == 'f16':
+            return {8: 'vh_u32x4{0u, 0u, 0u, 0u}', 4: 'vh_u32x2{0u, 0u}', 2: '0u', 1: '(vh_half)0'}[vec]
+        return {4: 'vh_f32x4{0.f, 0.f, 0.f, 0.f}', 2: 'vh_f32x2{0.f, 0.f}', 1: '0.0f'}[vec]
+
+    def vec_unpack(self, dt, vec, src, dst):
+        if dt == 'f16':
+            if vec == 8:
+                return f'unpack8({src}, {dst});'
+            if vec == 4:
+                return f'unpack4({src}, {dst});'
+            if vec == 2:
+                return f'{dst}[0] = h2f_lo({src}); {dst}[1] = h2f_hi({src});'
+            return f'{dst}[0] = h2f({src});'
+        if vec == 4:
+            return f'{dst}[0] = {src}.x; {dst}[1] = {src}.y; {dst}[2] = {src}.z; {dst}[3] = {src}.w;'
+        if vec == 2:
+            return f'{dst}[0] = {src}.x; {dst}[1] = {src}.y;'
+        return f'{dst}[0] = {src};'
+
+    # -- lane
+    def gen_lane(self, s, c, fused, out, ind):
+        name, axes = s[1], list(s[2])
+        reads, writes = self.site_io(s, c, fused)
+        self.sync(reads, writes, out, ind, name)
+        self.plan.append((show_stmt(s), 'lane' + (f' +{len(fused)} fused' if fused else '')))
+        for _, t, _ in fused:
+            self.plan.append((show_stmt(t), f'epilogue of {name}'))
+        dt = self.res[c.W][1]
+        vec = c.vec
+        K = self.static[c.contig]
+        nv = K // vec
+        lpp = 1
+        while lpp * 2 <= 64 and nv % (lpp * 2) == 0:
+            lpp *= 2
+        if lpp < 8 and nv >= 64:
+            lpp = 64
+        per_lane = (nv + lpp - 1) // lpp
+        exact = nv % lpp == 0
+        ppw = WAVE // lpp
+        reg, pt = c.reg_axes, c.pt_axes
+        rn = self.size(reg)
+        rch = min(rn, REG_MAX)
+        nrch = (rn + rch - 1) // rch
+        I = ind + '  '
+        o = out
+        o.append(f'{ind}{{  // lane {name}: W={c.W} VEC={vec} lanes/point={lpp} reg={rn}')
+        o.append(f'{I}const int NP_ = {self.count_c(pt)} * {nrch};')
+        o.append(f'{I}const int sub_ = lane / {lpp}, cl_ = lane % {lpp};')
+        o.append(f'{I}const int gw_ = blockIdx.x * {NWAVE} + wave, nw_ = nblk * {NWAVE};')
+        o.append(f'{I}for (int p0_ = gw_ * {ppw}; p0_ < NP_; p0_ += nw_ * {ppw}) {{')
+        J2 = I + '  '
+        o.append(f'{J2}const int p_ = p0_ + sub_;')
+        o.append(f'{J2}const bool ok_ = p_ < NP_;')
+        o.append(f'{J2}int pq_ = ok_ ? p_ : 0;')
+        o.append(f'{J2}const int rc_ = pq_ % {nrch}; pq_ /= {nrch};')
+        env = self.decode('pq_', pt, o, J2)
+        o.append(f'{J2}float acc_[{rch}];')
+        o.append(f'{J2}#pragma unroll')
+        o.append(f'{J2}for (int r_ = 0; r_ < {rch}; ++r_) acc_[r_] = 0.0f;')
+        ltype = {8: 'vh_u32x4', 4: 'vh_u32x2', 2: 'unsigned', 1: 'vh_half'}[vec] if dt == 'f16' else \
+            {4: 'vh_f32x4', 2: 'vh_f32x2', 1: 'float'}[vec]
+        U = min(UNROLL, per_lane)
+        o.append(f'{J2}for (int m0_ = 0; m0_ < {per_lane}; m0_ += {U}) {{')
+        K3 = J2 + '  '
+        o.append(f'{K3}{ltype} wq_[{U}];')
+        o.append(f'{K3}#pragma unroll')
+        o.append(f'{K3}for (int u_ = 0; u_ < {U}; ++u_) {{')
+        K4 = K3 + '  '
+        o.append(f'{K4}const int kv_ = (cl_ + (m0_ + u_) * {lpp}) * {vec};')
+        cond = f'm0_ + u_ < {per_lane}' + ('' if exact else f' && kv_ < {K}')
+        o.append(f'{K4}if ({cond}) {{')
+        wenv = {**env, c.contig: ('kv_', 'int')}
+        for a in reg:
+            wenv[a] = ('0', 'int')
+        pre = []
+        wix = [self.index(x, wenv, pre, K4 + '  ') for x in c.widx]
+        o += pre
+        waddr = self.addr(wix, self.res_strides(c.W))
+        o.append(f'{K4}  wq_[u_] = {self.vec_load(dt, vec, c.W, waddr)};')
+        o.append(f'{K4}}} else {{')
+        o.append(f'{K4}  wq_[u_] = {self.vec_zero(dt, vec)};')
+        o.append(f'{K4}}}')
+        o.append(f'{K3}}}')
+        o.append(f'{K3}#pragma unroll')
+        o.append(f'{K3}for (int u_ = 0; u_ < {U}; ++u_) {{')
+        o.append(f'{K4}const int kv_ = (cl_ + (m0_ + u_) * {lpp}) * {vec};')
+        o.append(f'{K4}if ({cond}) {{')
+        K5 = K4 + '  '
+        o.append(f'{K5}float wf_[{vec}];')
+        o.append(f'{K5}{self.vec_unpack(dt, vec, "wq_[u_]", "wf_")}')
+        o.append(f'{K5}#pragma unroll')
+        o.append(f'{K5}for (int v_ = 0; v_ < {vec}; ++v_) {{')
+        K6 = K5 + '  '
+        o.append(f'{K6}const int kk_ = kv_ + v_;')
+        for r in range(rch):
+            renv = {**env, c.contig: ('kk_', 'int')}
+            if reg:
+                rl = []
+                renv.update(self.decode_const(f'(rc_ * {rch} + {r})', reg, rl, K6))
+                o += rl
+            pre = []
+            av, at = self.expr(c.A, renv, pre, K6)
+            o += pre
+            guard = f'rc_ * {rch} + {r} < {rn}' if rn % rch else None
+            if guard:
+                o.append(f'{K6}if ({guard}) acc_[{r}] = fmaf({self.as_float(av, at)}, wf_[v_], acc_[{r}]);')
+            else:
+                o.append(f'{K6}acc_[{r}] = fmaf({self.as_float(av, at)}, wf_[v_], acc_[{r}]);')
+        o.append(f'{K5}}}')
+        o.append(f'{K4}}}')
+        o.append(f'{K3}}}')
+        o.append(f'{J2}}}')
+        if lpp > 1:
+            o.append(f'{J2}#pragma unroll')
+            o.append(f'{J2}for (int r_ = 0; r_ < {rch}; ++r_) acc_[r_] = group_red_sum(acc_[r_], {lpp});')
+        o.append(f'{J2}if (ok_ && cl_ == 0) {{')
+        K3 = J2 + '  '
+        for r in range(rch):
+            fenv = dict(env)
+            lines = []
+            if reg:
+                lines.append(f'{K3}if (rc_ * {rch} + {r} < {rn}) {{')
+                K4 = K3 + '  '
+                fenv.update(self.decode_const(f'(rc_ * {rch} + {r})', reg, lines, K4))
+            else:
+                K4 = K3
+            self.epilogue(s, c, fused, fenv, f'acc_[{r}]', lines, K4)
+            if reg:
+                lines.append(f'{K3}}}')
+            o += lines
+        o.append(f'{J2}}}')
+        o.append(f'{I}}}')
+        o.append(f'{ind}}}')
+        self.note(reads, writes)
+        self.mark(out, ind, f'lane {name}')
+
+    # -- private
+    def gen_private(self, run, out, ind):
+        reads = self.root_reads([t[3] for t in run], exclude={t[1] for t in run})
+        self.sync(reads, set(), out, ind, run[0][1])
+        out.append(f'{ind}__syncthreads();')
+        # global values the run reads are staged into LDS once (coherent loads)
+        base = off = self.lds_floats
+        staged = {}
+        for r in sorted(reads):
+            if r in self.g and r not in self.private:
+                size = self.size(self.axes_of[r])
+                if off - base + size <= STAGE_MAX:
+                    staged[r] = off
+                    out.append(f'{ind}stage_ldc(sh_f + {off}, S + {self.g[r]}, {size});  // stage {r}')
+                    off += size
+        self.stage_floats = max(self.stage_floats, off - base)
+        if staged:
+            out.append(f'{ind}__syncthreads();')
+        self.staged = staged
+        for s in run:
+            self.plan.append((show_stmt(s), 'private'))
+            name, axes, e = s[1], list(s[2]), s[3]
+            npts = self.size(axes)
+            o = out
+            if e[0] == 'fold' and npts <= 64 and self.static[e[2]] >= 64:
+                op, ax, body = e[1], e[2], e[3]
+                o.append(f'{ind}for (int p_ = wave; p_ < {npts}; p_ += {NWAVE}) {{  // private {name}')
+                I = ind + '  '
+                env = self.decode('p_', axes, o, I)
+                o.append(f'{I}float a_ = {FOLD_INIT[op]};')
+                o.append(f'{I}for (int k_ = lane; k_ < {self.ext_c(ax)}; k_ += {WAVE}) {{')
+                pre = []
+                v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '  ')
+                o += pre
+                o.append(f'{I}  a_ = {FOLD_OP[op]}(a_, {self.as_float(v, t)});')
+                o.append(f'{I}}}')
+                o.append(f'{I}a_ = wave_red_{op}(a_);')
+                o.append(f'{I}if (lane == 0) {self.store(name, [env[a][0] for a in axes], "a_", "float")}')
+                o.append(f'{ind}}}')
+            else:
+                o.append(f'{ind}for (int p_ = tid; p_ < {npts}; p_ += {BLOCK}) {{  // private {name}')
+                I = ind + '  '
+                env = self.decode('p_', axes, o, I)
+                pre = []
+                v, t = self.expr(e, env, pre, I)
+                o += pre
+                o.append(f'{I}{self.store(name, [env[a][0] for a in axes], v, t)}')
+                o.append(f'{ind}}}')
+            out.append(f'{ind}__syncthreads();')
+        self.staged = {}
+        self.mark(out, ind, f'private {run[0][1]}..{run[-1][1]}')
+
+    # -- group
+    def gen_group(self, lead, members, out, ind):
+        names = {t[1] for t in members}
+        reads = self.root_reads([t[3] for t in members], exclude=names)
+        writes = {self.root(t[1]) for t in members}
+        self.sync(reads, writes, out, ind, members[0][1])
+        for t in members:
+            self.plan.append((show_stmt(t), f'group[{", ".join(lead)}]'))
+        o = out
+        I = ind + '  '
+        o.append(f'{ind}for (int gp_ = blockIdx.x; gp_ < {self.count_c(lead)}; gp_ += nblk) {{  // group')
+        env = self.decode('gp_', lead, o, I)
+        for t in members:
+            name, axes, e = t[1], list(t[2]), t[3]
+            rest = axes[len(lead):]
+            if not rest and e[0] == 'fold':
+                op, ax, body = e[1], e[2], e[3]
+                o.append(f'{I}{{  // {name}')
+                I2 = I + '  '
+                o.append(f'{I2}float a_ = {FOLD_INIT[op]};')
+                o.append(f'{I2}for (int k_ = tid; k_ < {self.ext_c(ax)}; k_ += {BLOCK}) {{')
+                pre = []
+                v, ty = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I2 + '  ')
+                o += pre
+                o.append(f'{I2}  a_ = {FOLD_OP[op]}(a_, {self.as_float(v, ty)});')
+                o.append(f'{I2}}}')
+                o.append(f'{I2}a_ = block_red_{op}(a_, red_sh);')
+                o.append(f'{I2}if (tid == 0) {self.store(name, [env[a][0] for a in axes], "a_", "float")}')
+                o.append(f'{I}}}')
+            else:
+                o.append(f'{I}for (int q_ = tid; q_ < {self.count_c(rest)}; q_ += {BLOCK}) {{  // {name}')
+                I2 = I + '  '
+                env2 = {**env, **self.decode('q_', rest, o, I2)}
+                pre = []
+                v, ty = self.expr(e, env2, pre, I2)
+                o += pre
+                o.append(f'{I2}{self.store(name, [env2[a][0] for a in axes], v, ty)}')
+                o.append(f'{I}}}')
+            o.append(f'{I}block_sync();')
+        o.append(f'{ind}}}')
+        self.note(reads, writes)
+        self.mark(out, ind, f'group {members[0][1]}..{members[-1][1]}')
+
+    # -- grid reduction
+    def gen_gridred(self, s, out, ind):
+        name, axes, e = s[1], list(s[2]), s[3]
+        reads = self.root_reads([e])
+        writes = {self.root(name)}
+        self.sync(reads, writes, out, ind, name)
+        self.plan.append((show_stmt(s), 'gridred'))
+        op, ax, body = e[1], e[2], e[3]
+        npts = self.size(axes)
+        poff = self.alloc_scratch(npts * GRID_MAX)
+        coff = self.alloc_counters(1)
+        o = out
+        I = ind + '  '
+        o.append(f'{ind}{{  // gridred {name}')
+        for p in range(npts):
+            env = {}
+            lines = []
+            if axes:
+                env = self.decode_const(str(p), axes, lines, I)
+            o += lines
+            o.append(f'{I}{{')
+            o.append(f'{I}  float a_ = {FOLD_INIT[op]};')
+            o.append(f'{I}  for (int k_ = gtid; k_ < {self.static[ax]}; k_ += nthr) {{')
+            pre = []
+            v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '    ')
+            o += pre
+            o.append(f'{I}    a_ = {FOLD_OP[op]}(a_, {self.as_float(v, t)});')
+            o.append(f'{I}  }}')
+            o.append(f'{I}  a_ = block_red_{op}(a_, red_sh);')
+            o.append(f'{I}  if (tid == 0) stc(S + {poff + p * GRID_MAX} + blockIdx.x, a_);')
+            o.append(f'{I}}}')
+        o.append(f'{I}if (last_arrival(bar + {coff}, nblk, &flag_sh)) {{')
+        for p in range(npts):
+            env = {}
+            lines = []
+            if axes:
+                env = self.decode_const(str(p), axes, lines, I + '  ')
+            o += lines
+            o.append(f'{I}  {{')
+            o.append(f'{I}    float a_ = {FOLD_INIT[op]};')
+            o.append(f'{I}    for (int b_ = tid; b_ < (int)nblk; b_ += {BLOCK}) a_ = {FOLD_OP[op]}(a_, '
+                     f'ldc(S + {poff + p * GRID_MAX} + b_));')
+            o.append(f'{I}    a_ = block_red_{op}(a_, red_sh);')
+            o.append(f'{I}    if (tid == 0) {self.store(name, [env[a][0] for a in axes], "a_", "float")}')
+            o.append(f'{I}  }}')
+        o.append(f'{I}}}')
+        o.append(f'{ind}}}')
+        self.note(reads, writes)
+        self.mark(out, ind, f'gridred {name}')
+
+    # -- one thread per point
+    def gen_thread(self, s, out, ind):
+        name, axes, e = s[1], list(s[2]), s[3]
+        reads = self.root_reads([e])
+        writes = {self.root(name)}
+        self.sync(reads, writes, out, ind, name)
+        self.plan.append((show_stmt(s), 'thread'))
+        I = ind + '  '
+        out.append(f'{ind}for (int p_ = gtid; p_ < {self.count_c(axes)}; p_ += nthr) {{  // thread {name}')
+        env = self.decode('p_', axes, out, I)
+        pre = []
+        v, t = self.expr(e, env, pre, I)
+        out += pre
+        out.append(f'{I}{self.store(name, [env[a][0] for a in axes], v, t)}')
+        out.append(f'{ind}}}')
+        self.note(reads, writes)
+        self.mark(out, ind, f'thread {name}')
+
+    def gen_emit(self, s, out, ind):
+        name = s[1]
+        ax = set()
+        for x in list(s[2]) + [s[3]]:
+            ax |= self.free_axes(x)
+        axes = [a for a in self.static if a in ax and self.is_axis(a)]
+        reads = self.root_reads(stmt_exprs(s))
+        self.sync(reads, {name}, out, ind, f'emit {name}')
+        self.plan.append((show_stmt(s), 'thread emit'))
+        I = ind + '  '
+        out.append(f'{ind}for (int p_ = gtid; p_ < {self.count_c(axes)}; p_ += nthr) {{  // emit {name}')
+        env = self.decode('p_', axes, out, I)
+        pre = []
+        ix = [self.index(x, env, pre, I) for x in s[2]]
+        v, t = self.expr(s[3], env, pre, I)
+        out += pre
+        out.append(f'{I}{self.res_store(name, ix, v, t, s[2])}')
+        out.append(f'{ind}}}')
+        self.note(reads, {name})
+        self.mark(out, ind, f'emit {name}')
+
+    def gen_copy(self, dst, src_e, axes, out, ind, what):
+        """dst[axes] = src_e, one thread per point (carry copies)."""
+        reads = self.root_reads([src_e])
+        writes = {self.root(dst)}
+        self.sync(reads, writes, out, ind, what)
+        I = ind + '  '
+        out.append(f'{ind}for (int p_ = gtid; p_ < {self.count_c(axes)}; p_ += nthr) {{  // {what}')
+        env = self.decode('p_', list(axes), out, I)
+        pre = []
+        v, t = self.expr(src_e, env, pre, I)
+        out += pre
+        out.append(f'{I}{self.store(dst, [env[a][0] for a in axes], v, t)}')
+        out.append(f'{ind}}}')
+        self.note(reads, writes)
+
+    # -- the layer loop
+    def gen_step(self, s, out, ind):
+        _, name, axes, var, init, carry, blk = s
+        self.plan.append((show_stmt(s), 'step loop'))
+        if not (init[0] == 'idx' and self.alias.get(init[1]) == carry):
+            self.gen_copy(carry, init, axes, out, ind, f'{carry} <- init')
+        if var not in self.static:
+            raise LowerError(f'step variable {var} needs an axis declaration')
+        if self.dirty:
+            self.barrier(out, ind, f'step {name}')
+        n = self.static[var]
+        lv = f'l_{var}'
+        out.append(f'{ind}for (int {lv} = 0; {lv} < {self.ext_c(var)}; ++{lv}) {{  // fold step {var}')
+        saved = self.step_env.get(var)
+        self.step_env[var] = (lv, 'int')
+        self.mult *= n
+        body = [b for b in blk if b[0] != 'ret']
+        ret = [b for b in blk if b[0] == 'ret'][0][1]
+        self.gen(body, out, ind + '  ')
+        if not (ret[0] == 'idx' and self.alias.get(ret[1]) == carry):
+            self.gen_copy(carry, ret, axes, out, ind + '  ', f'{carry} <- ret')
+        self.barrier(out, ind + '  ', f'next {var}')
+        self.mult //= n
+        out.append(f'{ind}}}')
+        if saved is None:
+            del self.step_env[var]
+        else:
+            self.step_env[var] = saved
+
+    # ------------------------------------------------------------ the kernel
+    def kernel(self, feedback):
+        """Body of one step, the feedback stores, and the history of chosen tokens."""
+        self.dirty, self.readers = set(), set()
+        self.red_floats = 4
+        body = []
+        ind = '    '
+        self.gen(self.stmts, body, ind)
+        self.history = None
+        if feedback:
+            self.barrier(body, ind, 'feedback')
+            for dst, src in feedback.items():
+                if dst not in self.res:
+                    raise NameError(f'feedback target {dst} not supplied')
+                dt = self.res[dst][1]
+                if isinstance(src, int):
+                    if dt == 'i32':
+                        body.append(f'{ind}if (gtid == 0) stc_i(R_{dst}, ldc_i(R_{dst}) + {src});')
+                    elif dt == 'f32':
+                        body.append(f'{ind}if (gtid == 0) stc(R_{dst}, ldc(R_{dst}) + {src});')
+                    else:
+                        raise LowerError(f'feedback into fp16 scalar {dst}')
+                    continue
+                if src not in self.axes_of:
+                    raise NameError(f'feedback source {src} is not a value of the program')
+                r = self.root(src)
+                n = self.size(self.axes_of[r])
+                if math.prod(self.res[dst][0]) != n:
+                    raise LowerError(f'feedback {dst} <- {src}: {math.prod(self.res[dst][0])} vs {n} elements')
+                v = f'ldc(S + {self.g[r]} + gtid)'
+                if dt == 'i32' and self.history is None:
+                    # token feedback: recorded in tok_out; tok_in (prefill) overrides the next input
+                    self.history = n
+                    body.append(f'{ind}if (gtid < {n}) {{')
+                    body.append(f'{ind}  const int nx_ = (int){v};')
+                    body.append(f'{ind}  if (tok_out != nullptr) tok_out[st_ * {n} + gtid] = nx_;')
+                    body.append(f'{ind}  stc_i(R_{dst} + gtid, (tok_in != nullptr && st_ + 1 < nsteps) ? '
+                                f'tok_in[(st_ + 1) * {n} + gtid] : nx_);')
+                    body.append(f'{ind}}}')
+                elif dt == 'i32':
+                    body.append(f'{ind}if (gtid < {n}) stc_i(R_{dst} + gtid, (int){v});')
+                elif dt == 'f32':
+                    body.append(f'{ind}if (gtid < {n}) stc(R_{dst} + gtid, {v});')
+                else:
+                    body.append(f'{ind}if (gtid < {n}) stc_h(rb_{dst}, gtid, {v});')
+        return body
+
+
+def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None, timing=False,
+          kernel_name='vesta_step'):
+    """Program text -> Lowered: HIP source of one persistent kernel.
+
+    Kernel ABI: ``<kernel_name>(R_<residue>... in spec order, float* S,
+    unsigned* bar, unsigned long long* TS, int nsteps, int* tok_out,
+    const int* tok_in)``. One launch runs ``nsteps`` steps back to back
+    (feedback between them; reference launches always run one). With token
+    feedback, the token chosen at step k of the launch is stored in
+    ``tok_out[k * B + b]`` when ``tok_out`` is not null, and when ``tok_in``
+    is not null the input of step k + 1 is ``tok_in[(k + 1) * B + b]``
+    instead (prefill: a prompt in one launch). ``bar`` must be zero before
+    the first launch and is left consistent by every launch.
+    """
+    stmts = batch_lift(parse(text), batch, set(per_token))
+    low = Lowering(stmts, res, axis_max, outputs, batch, timing)
+    for o in outputs:
+        if o not in low.axes_of:
+            raise NameError(f'output {o} is not a value of the program')
+        if low.root(o) in low.private:
+            raise LowerError(f'output {o} was placed in LDS')
+    low.fb_targets = set(feedback or {})
+    body = low.kernel(feedback)
+    written = set(low.emitted) | low.fb_targets
+    params, args = [], []
+    for name, (shape, dt) in low.res.items():
+        w = name in written
+        params.append((name, dt, w))
+        args.append(f'{"" if w else "const "}{CTYPE[dt]}* __restrict__ R_{name}')
+    args += ['float* __restrict__ S', 'unsigned* __restrict__ bar', 'unsigned long long* __restrict__ TS',
+             'const int nsteps', 'int* __restrict__ tok_out', 'const int* __restrict__ tok_in']
+    pre = []
+    for name in sorted(written):
+        shape, dt = low.res[name]
+        if dt == 'f16':
+            nbytes = math.prod(shape) * 2
+            if nbytes >= 1 << 32:
+                raise LowerError(f'residue {name} is {nbytes} bytes; coherent fp16 access is limited to 4 GiB')
+            pre.append(f'  const vh_rsrc rb_{name} = mk_rsrc(R_{name}, {nbytes}u);')
+    head = []
+    # scalar residues read by name: once per step (before any barrier of the step)
+    for name, (shape, dt) in low.res.items():
+        if math.prod(shape) == 1 and len(shape) <= 1 and name not in low.emitted:
+            cty = {'i32': 'int', 'f32': 'float', 'f16': 'float'}[dt]
+            if low.coherent(name):
+                val = {'i32': f'ldc_i(R_{name})', 'f32': f'ldc(R_{name})', 'f16': f'ldc_h(rb_{name}, 0)'}[dt]
+            else:
+                val = f'h2f(R_{name}[0])' if dt == 'f16' else f'R_{name}[0]'
+            head.append(f'    const {cty} rs_{name} = {val};')
+    for a, e in low.dynamic.items():
+        lines = []
+        v = low.index(e, {}, lines, '    ')
+        head += lines
+        head.append(f'    const int E_{a} = {v};')
+        head.append(f'    if (E_{a} > {low.static[a]} || E_{a} < 1) break;  // beyond its bound: stop')
+    red = max(low.red_floats, 4)
+    prelude = PRELUDE_PATH.read_text()
+    src = (prelude + '\n'
+           + f'extern "C" __global__ void __launch_bounds__({BLOCK}) {kernel_name}(' + ', '.join(args) + ') {\n'
+           + '  extern __shared__ float sh_f[];\n'
+           + f'  __shared__ float red_sh[{red}];\n'
+           + '  __shared__ int flag_sh;\n'
+           + '  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;\n'
+           + f'  const int gtid = blockIdx.x * {BLOCK} + tid;\n'
+           + f'  const int nthr = gridDim.x * {BLOCK};\n'
+           + '  const unsigned nblk = gridDim.x;\n'
+           + '  unsigned bgen_ = tid == 0 ? ldc_u(bar) : 0u;\n'
+           + ('  unsigned long long tlast_ = vh_clock();\n' if timing else '')
+           + '\n'.join(pre) + '\n'
+           + '  for (int st_ = 0; st_ < nsteps; ++st_) {\n'
+           + '\n'.join(head) + '\n'
+           + '\n'.join(body) + '\n'
+           + '    if (st_ + 1 < nsteps) grid_sync(bar, nblk, bgen_);  // feedback visible to the next step\n'
+           + '  }\n}\n')
+    scratch = {}
+    for n in low.axes_of:
+        r = low.root(n)
+        if r in low.g:
+            axes = low.axes_of[n]
+            scratch[n] = (low.g[r], axes, tuple(low.static[a] for a in axes))
+    return Lowered(src, params, scratch, low.goff, (low.lds_floats + low.stage_floats) * 4, low.barriers,
+                   low.plan, low.sites, low.counters, BLOCK, GRID_MAX, {n: shp for n, (shp, _) in low.res.items()},
+                   kernel_name)
