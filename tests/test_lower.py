@@ -61,25 +61,28 @@ def _nodes(e):
 def test_gpt2_small_b1_plan():
     low = lower_gpt2(1)
     p = placements(low)
-    for name in ('qkv', 'o', 'oo', 'u', 'z2'):
+    for name in ('qkv', 'oo', 'u', 'z2'):
         assert p[name].startswith('tile'), (name, p[name])
-    assert p['sc'].startswith('lane') and p['logit'].startswith('lane')
-    assert p['best'] == 'gridred' and p['next'] == 'gridred'
+    # attention: scores, softmax statistics and weighted values in one block per (bt, h)
+    assert p['sc'] == 'group[bt, h] lane (LDS)' and p['o'] == 'group[bt, h] tile'
+    assert p['mx'] == p['_h1'] == 'group[bt, h] (LDS)'
+    assert p['logit'].startswith('lane')
+    assert p['best'] == 'gridred argmax' and p['next'] == 'gridred argmax'
     assert p['m1'] == p['v1'] == p['a'] == 'private'
     assert p['residue keys'] == 'epilogue of qkv' and p['residue vals'] == 'epilogue of qkv'
     assert p['g'] == 'epilogue of u' and p['z1'] == 'epilogue of oo'
     # softmax denominator hoisted, q / ex / w inlined
     assert '_h1' in p and 'q' not in p and 'w' not in p and 'ex' not in p
-    assert low.barriers_per_launch <= 76
+    assert low.barriers_per_launch <= 63
     assert set(low.scratch) >= {'logit', 'next'} and low.scratch['logit'][2] == (1, 50257)
 
 
 def test_gpt2_small_b8_plan():
     low = lower_gpt2(8)
     p = placements(low)
-    assert p['mx'].startswith('group') and p['_h1'].startswith('group')
+    assert p['mx'].startswith('group') and p['_h1'].startswith('group') and p['o'].startswith('group')
     assert p['qkv'].startswith('tile') and p['logit'].startswith('lane')
-    assert low.barriers_per_launch <= 88
+    assert low.barriers_per_launch <= 75
     assert low.scratch['logit'][2] == (8, 50257) and low.scratch['next'][2] == (8,)
 
 

@@ -93,6 +93,20 @@ VH_BLOCK_RED(block_red_sum, wave_red_sum, op_sum)
 VH_BLOCK_RED(block_red_max, wave_red_max, op_max)
 VH_BLOCK_RED(block_red_min, wave_red_min, op_min)
 
+// (value, index) pairs: the larger value wins, equal values go to the lower
+// index. Every thread gets the block's pair; `rv`/`ri` are VNWAVE slots of LDS.
+__device__ __forceinline__ void argmax_pair(float& v, int& i, float ov, int oi) {
+  if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
+}
+__device__ __forceinline__ void block_argmax(float& v, int& i, float* rv, int* ri) {
+  for (int o = 32; o > 0; o >>= 1) argmax_pair(v, i, __shfl_xor(v, o, 64), __shfl_xor(i, o, 64));
+  __syncthreads();
+  if ((threadIdx.x & 63) == 0) { rv[threadIdx.x >> 6] = v; ri[threadIdx.x >> 6] = i; }
+  __syncthreads();
+  v = rv[0]; i = ri[0];
+  for (int w = 1; w < VNWAVE; ++w) argmax_pair(v, i, rv[w], ri[w]);
+}
+
 // ---------------------------------------------------------------- coherence
 // Values one block writes and another reads within a launch never rely on
 // cache maintenance: they are stored with agent-scope coherent stores (sc1,

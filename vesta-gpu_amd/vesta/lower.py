@@ -75,6 +75,7 @@ PRIV_WORK = 1 << 17           # ... and costs at most this many operations per b
 PRIV_BUDGET = 16384           # all live private values together: 64 KB of LDS
 STAGE_MAX = 8192              # a private statement reads at most this many floats of locals
 GROUP_WORK = 1 << 14          # a group statement does at most this much work per leading point
+ATTN_WORK = 1 << 17           # ... or this much in a group that streams the key/value cache
 BIG = 1 << 16                 # a residue this large is streamed, never recomputed per point
 LANE_MIN = 32                 # lane-split a fold only if it is at least this long
 GRIDRED_MIN = 1 << 14         # grid reduction for a fold at least this long into few points
@@ -571,6 +572,17 @@ class Lowering:
         self.groups = {}          # id(first stmt) -> (lead axes, [stmts])
         self.in_group = set()
         self.private = set()
+        self.argmax = {}          # id(max statement) -> the lowest-index statement that reads it
+        self.group_local = {}     # id(first stmt of a group) -> names kept in LDS
+        self.readers_of = {}      # name -> ids of statements reading it
+        def index(ss):
+            for t in ss:
+                for e in stmt_exprs(t):
+                    for n in self.reads(e):
+                        self.readers_of.setdefault(n, set()).add(id(t))
+                if t[0] == 'step':
+                    index(t[6])
+        index(ss)
         self._place_block(ss)
 
     def priv_ok(self, s):
@@ -600,6 +612,20 @@ class Lowering:
             if s[0] != 'let':
                 i += 1
                 continue
+            run = self.attn_run(ss, i)
+            if run:
+                lead, members = run
+                self.groups[id(members[0])] = (lead, members)
+                ids = {id(t) for t in members}
+                self.group_local[id(members[0])] = [
+                    t[1] for t in members
+                    if t[1] not in self.outputs and not (self.readers_of.get(t[1], set()) - ids)]
+                for t in members:
+                    self.place[id(t)] = 'group'
+                    self.in_group.add(id(t))
+                made = set()
+                i += len(members)
+                continue
             c = self.contraction(s)
             if c is not None:
                 self.place[id(s)] = c.kind
@@ -622,6 +648,13 @@ class Lowering:
             g = self.gridred(s)
             if g:
                 self.place[id(s)] = 'gridred'
+                if i + 1 < len(ss) and self.argmin_of_max(s, ss[i + 1]):
+                    # max and lowest index of the max: one grid reduction of (value, index) pairs
+                    self.place[id(s)] = 'argmax'
+                    self.place[id(ss[i + 1])] = 'argmax'
+                    self.argmax[id(s)] = ss[i + 1]
+                    i += 2
+                    continue
                 i += 1
                 continue
             run = self.group_run(ss, i)
@@ -656,6 +689,48 @@ class Lowering:
                 and self.static[e[2]] >= 1024 and not self.big_reads(e)
                 and s[1] not in self.alias and s[1] not in set(self.alias.values()))
 
+    def attn_run(self, ss, i):
+        """Consecutive statements sharing leading axes that stream the
+        key/value cache (contractions over emitted residues) and read each
+        other only at the leading point: one block per leading point."""
+        s = ss[i]
+        if s[0] != 'let' or len(s[2]) < 2:
+            return None
+        carries = set(self.alias.values())
+        for plen in range(len(s[2]) - 1, 0, -1):
+            lead = list(s[2][:plen])
+            if any(a in self.dynamic for a in lead):
+                continue
+            same = [('name', a) for a in lead]
+            run, names, has_c = [], set(), False
+            for t in ss[i:]:
+                if t[0] != 'let' or len(t[2]) < plen or list(t[2][:plen]) != lead:
+                    break
+                if t[1] in self.alias or t[1] in carries or self.big_reads(t[3]):
+                    break
+                if any(n[0] == 'idx' and n[1] in names and list(n[2][:plen]) != same for n in nodes(t[3])):
+                    break
+                if self.size(t[2][plen:]) * self.fold_work(t[3]) > ATTN_WORK:
+                    break
+                c = self.contraction(t)
+                if c is not None:
+                    if not self.block_contraction_ok(c, t, plen):
+                        break
+                    has_c = True
+                run.append(t)
+                names.add(t[1])
+            if len(run) >= 2 and has_c:
+                return lead, run
+        return None
+
+    def block_contraction_ok(self, c, t, plen):
+        rest = list(t[2][plen:])
+        if c.reg_axes:
+            return False
+        if c.kind == 'lane':
+            return True
+        return rest == [c.contig] and c.contig not in self.dynamic
+
     def group_ok(self, t, plen):
         return (t[0] == 'let' and not self.big_reads(t[3]) and self.contraction(t) is None
                 and not self.priv_ok(t) and len(t[2]) >= plen
@@ -684,6 +759,20 @@ class Lowering:
             if len(run) >= 2:
                 return lead, run
         return None
+
+    def argmin_of_max(self, s1, s2):
+        """s2 = fold min n: fork E[n] == s1 ? n : C, with s1 = fold max n: E[n]."""
+        e1, e2 = s1[3], s2[3]
+        if s2[0] != 'let' or list(s2[2]) != list(s1[2]) or e1[1] != 'max' or e2[0] != 'fold' or e2[1] != 'min' \
+                or e2[2] != e1[2] or s2[1] in self.alias or s1[1] in self.alias:
+            return False
+        body = e2[3]
+        if body[0] != 'fork' or body[2] != ('name', e1[2]) or body[3][0] != 'num':
+            return False
+        cond = body[1]
+        me = ('idx', s1[1], [('name', a) for a in s1[2]]) if s1[2] else ('name', s1[1])
+        return cond[0] == 'bin' and cond[1] == '==' and (
+            (cond[2] == e1[3] and cond[3] == me) or (cond[3] == e1[3] and cond[2] == me))
 
     def gridred(self, s):
         e = s[3]
@@ -810,6 +899,7 @@ class Lowering:
             self.goff += max(1, self.size(self.axes_of[r]))
         self.counters = BAR_WORDS
         self.staged = {}
+        self.glocal = {}
         self.stage_floats = 0
 
     def alloc_scratch(self, n):
@@ -993,6 +1083,9 @@ class Lowering:
             return f'sh_f[{self.lds[r]} + {a}]'
         if r in self.staged:
             return f'sh_f[{self.staged[r]} + {a}]'
+        if r in self.glocal:
+            off, plen = self.glocal[r]
+            return f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}]'
         return f'ldc(S + {self.g[r]} + {a})'
 
     def store(self, n, ix, v, t):
@@ -1000,6 +1093,9 @@ class Lowering:
         a = self.addr(ix, self.strides(self.axes_of[r]))
         if r in self.private:
             return f'sh_f[{self.lds[r]} + {a}] = {self.as_float(v, t)};'
+        if r in self.glocal:
+            off, plen = self.glocal[r]
+            return f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}] = {self.as_float(v, t)};'
         return f'stc(S + {self.g[r]} + {a}, {self.as_float(v, t)});'
 
     def decode(self, var, axes, out, ind, prefix='i_'):
@@ -1099,6 +1195,10 @@ class Lowering:
                 else:
                     self.gen_lane(s, self.info[id(s)], fused, out, ind)
                 i += 1 + len(fused)
+                continue
+            if p == 'argmax':
+                self.gen_argmax(s, self.argmax[id(s)], out, ind)
+                i += 2
                 continue
             if p == 'gridred':
                 self.gen_gridred(s, out, ind)
@@ -1511,56 +1611,101 @@ class Lowering:
 
     # -- lane
     def gen_lane(self, s, c, fused, out, ind):
-        name, axes = s[1], list(s[2])
+        name = s[1]
         reads, writes = self.site_io(s, c, fused)
         self.sync(reads, writes, out, ind, name)
         self.plan.append((show_stmt(s), 'lane' + (f' +{len(fused)} fused' if fused else '')))
         for _, t, _ in fused:
             self.plan.append((show_stmt(t), f'epilogue of {name}'))
+        self.emit_lane(s, c, fused, out, ind, c.pt_axes, {}, 'blockIdx.x * %d + wave' % NWAVE, f'nblk * {NWAVE}')
+        self.note(reads, writes)
+        self.mark(out, ind, f'lane {name}')
+
+    def emit_lane(self, s, c, fused, out, ind, pt, base_env, wave_c, nwave_c):
+        """A group of lanes per output point, 16-byte loads along the fold.
+        Each wave takes PI points per lane group at once (PI x per-lane loads
+        in flight); when the other factor does not depend on the point (the
+        LM head's c[bt, d]) each lane keeps its slice of it in registers.
+        Points are the axes ``pt`` (others come bound in ``base_env``), taken
+        by waves ``wave_c`` of ``nwave_c``."""
+        name = s[1]
         dt = self.res[c.W][1]
         vec = c.vec
         K = self.static[c.contig]
         nv = K // vec
+        reg = c.reg_axes
+        rn = self.size(reg)
+        rch = min(rn, REG_MAX)
+        nrch = (rn + rch - 1) // rch
+        preload = nrch == 1 and (self.free_axes(c.A) - {c.contig}) <= set(reg) | set(base_env)
         lpp = 1
         while lpp * 2 <= 64 and nv % (lpp * 2) == 0:
             lpp *= 2
         if lpp < 8 and nv >= 64:
             lpp = 64
-        per_lane = (nv + lpp - 1) // lpp
+        if preload and -(-nv // lpp) * vec * rch > 128 and nv >= 64:
+            lpp = 64
+        pl = -(-nv // lpp)                       # vectors per lane
         exact = nv % lpp == 0
         ppw = WAVE // lpp
-        reg, pt = c.reg_axes, c.pt_axes
-        rn = self.size(reg)
-        rch = min(rn, REG_MAX)
-        nrch = (rn + rch - 1) // rch
+        PI = max(1, min(8, 12 // pl, 32 // rch))
+        step = ppw * PI
         I = ind + '  '
         o = out
-        o.append(f'{ind}{{  // lane {name}: W={c.W} VEC={vec} lanes/point={lpp} reg={rn}')
-        o.append(f'{I}const int NP_ = {self.count_c(pt)} * {nrch};')
-        o.append(f'{I}const int sub_ = lane / {lpp}, cl_ = lane % {lpp};')
-        o.append(f'{I}const int gw_ = blockIdx.x * {NWAVE} + wave, nw_ = nblk * {NWAVE};')
-        o.append(f'{I}for (int p0_ = gw_ * {ppw}; p0_ < NP_; p0_ += nw_ * {ppw}) {{')
-        J2 = I + '  '
-        o.append(f'{J2}const int p_ = p0_ + sub_;')
-        o.append(f'{J2}const bool ok_ = p_ < NP_;')
-        o.append(f'{J2}int pq_ = ok_ ? p_ : 0;')
-        o.append(f'{J2}const int rc_ = pq_ % {nrch}; pq_ /= {nrch};')
-        env = self.decode('pq_', pt, o, J2)
-        o.append(f'{J2}float acc_[{rch}];')
-        o.append(f'{J2}#pragma unroll')
-        o.append(f'{J2}for (int r_ = 0; r_ < {rch}; ++r_) acc_[r_] = 0.0f;')
         ltype = {8: 'vh_u32x4', 4: 'vh_u32x2', 2: 'unsigned', 1: 'vh_half'}[vec] if dt == 'f16' else \
             {4: 'vh_f32x4', 2: 'vh_f32x2', 1: 'float'}[vec]
-        U = min(UNROLL, per_lane)
-        o.append(f'{J2}for (int m0_ = 0; m0_ < {per_lane}; m0_ += {U}) {{')
-        K3 = J2 + '  '
-        o.append(f'{K3}{ltype} wq_[{U}];')
-        o.append(f'{K3}#pragma unroll')
-        o.append(f'{K3}for (int u_ = 0; u_ < {U}; ++u_) {{')
-        K4 = K3 + '  '
-        o.append(f'{K4}const int kv_ = (cl_ + (m0_ + u_) * {lpp}) * {vec};')
-        cond = f'm0_ + u_ < {per_lane}' + ('' if exact else f' && kv_ < {K}')
-        o.append(f'{K4}if ({cond}) {{')
+        o.append(f'{ind}{{  // lane {name}: W={c.W} VEC={vec} lanes/point={lpp} points/iter={PI} reg={rn}'
+                 f'{" preloaded" if preload else ""}')
+        o.append(f'{I}const int NP_ = {self.count_c(pt)} * {nrch};')
+        o.append(f'{I}const int sub_ = lane / {lpp}, cl_ = lane % {lpp};')
+        o.append(f'{I}const int gw_ = {wave_c}, nw_ = {nwave_c};')
+        kcond = '' if exact else f' && kv_ < {K}'
+        if preload:
+            o.append(f'{I}float ap_[{pl}][{vec}][{rch}];')
+            o.append(f'{I}#pragma unroll')
+            o.append(f'{I}for (int m_ = 0; m_ < {pl}; ++m_) {{')
+            o.append(f'{I}  const int kv_ = (cl_ + m_ * {lpp}) * {vec};')
+            o.append(f'{I}  #pragma unroll')
+            o.append(f'{I}  for (int v_ = 0; v_ < {vec}; ++v_) {{')
+            o.append(f'{I}    const int kk_ = kv_ + v_;')
+            for r in range(rch):
+                renv = {**base_env, c.contig: ('kk_', 'int')}
+                if reg:
+                    rl = []
+                    renv.update(self.decode_const(str(r), reg, rl, I + '    '))
+                    o += rl
+                pre = []
+                av, at = self.expr(c.A, renv, pre, I + '    ')
+                o += pre
+                o.append(f'{I}    ap_[m_][v_][{r}] = {"" if exact else f"kk_ >= {K} ? 0.0f : "}{self.as_float(av, at)};')
+            o.append(f'{I}  }}')
+            o.append(f'{I}}}')
+        o.append(f'{I}for (int p0_ = gw_ * {step}; p0_ < NP_; p0_ += nw_ * {step}) {{')
+        J2 = I + '  '
+        o.append(f'{J2}bool ok_[{PI}];')
+        o.append(f'{J2}int prc_[{PI}];')
+        for a in pt:
+            o.append(f'{J2}int px_{a}[{PI}];')
+        o.append(f'{J2}#pragma unroll')
+        o.append(f'{J2}for (int pi_ = 0; pi_ < {PI}; ++pi_) {{')
+        o.append(f'{J2}  const int p_ = p0_ + pi_ * {ppw} + sub_;')
+        o.append(f'{J2}  ok_[pi_] = p_ < NP_;')
+        o.append(f'{J2}  int pq_ = ok_[pi_] ? p_ : 0;')
+        o.append(f'{J2}  prc_[pi_] = pq_ % {nrch}; pq_ /= {nrch};')
+        for a in reversed(pt[1:]):
+            o.append(f'{J2}  px_{a}[pi_] = pq_ % {self.ext_c(a)}; pq_ /= {self.ext_c(a)};')
+        if pt:
+            o.append(f'{J2}  px_{pt[0]}[pi_] = pq_;')
+        o.append(f'{J2}}}')
+        env = {**base_env, **{a: (f'px_{a}[pi_]', 'int') for a in pt}}
+        o.append(f'{J2}{ltype} wq_[{PI}][{pl}];')
+        o.append(f'{J2}#pragma unroll')
+        o.append(f'{J2}for (int pi_ = 0; pi_ < {PI}; ++pi_)')
+        o.append(f'{J2}  #pragma unroll')
+        o.append(f'{J2}  for (int m_ = 0; m_ < {pl}; ++m_) {{')
+        K4 = J2 + '    '
+        o.append(f'{K4}const int kv_ = (cl_ + m_ * {lpp}) * {vec};')
+        o.append(f'{K4}if (ok_[pi_]{kcond}) {{')
         wenv = {**env, c.contig: ('kv_', 'int')}
         for a in reg:
             wenv[a] = ('0', 'int')
@@ -1568,63 +1713,77 @@ class Lowering:
         wix = [self.index(x, wenv, pre, K4 + '  ') for x in c.widx]
         o += pre
         waddr = self.addr(wix, self.res_strides(c.W))
-        o.append(f'{K4}  wq_[u_] = {self.vec_load(dt, vec, c.W, waddr)};')
+        o.append(f'{K4}  wq_[pi_][m_] = {self.vec_load(dt, vec, c.W, waddr)};')
         o.append(f'{K4}}} else {{')
-        o.append(f'{K4}  wq_[u_] = {self.vec_zero(dt, vec)};')
+        o.append(f'{K4}  wq_[pi_][m_] = {self.vec_zero(dt, vec)};')
         o.append(f'{K4}}}')
-        o.append(f'{K3}}}')
-        o.append(f'{K3}#pragma unroll')
-        o.append(f'{K3}for (int u_ = 0; u_ < {U}; ++u_) {{')
-        o.append(f'{K4}const int kv_ = (cl_ + (m0_ + u_) * {lpp}) * {vec};')
-        o.append(f'{K4}if ({cond}) {{')
-        K5 = K4 + '  '
+        o.append(f'{J2}  }}')
+        o.append(f'{J2}float acc_[{PI}][{rch}];')
+        o.append(f'{J2}#pragma unroll')
+        o.append(f'{J2}for (int pi_ = 0; pi_ < {PI}; ++pi_) {{')
+        o.append(f'{J2}  #pragma unroll')
+        o.append(f'{J2}  for (int r_ = 0; r_ < {rch}; ++r_) acc_[pi_][r_] = 0.0f;')
+        o.append(f'{J2}  #pragma unroll')
+        o.append(f'{J2}  for (int m_ = 0; m_ < {pl}; ++m_) {{')
+        K5 = J2 + '    '
+        o.append(f'{K5}const int kv_ = (cl_ + m_ * {lpp}) * {vec};')
         o.append(f'{K5}float wf_[{vec}];')
-        o.append(f'{K5}{self.vec_unpack(dt, vec, "wq_[u_]", "wf_")}')
+        o.append(f'{K5}{self.vec_unpack(dt, vec, "wq_[pi_][m_]", "wf_")}')
         o.append(f'{K5}#pragma unroll')
         o.append(f'{K5}for (int v_ = 0; v_ < {vec}; ++v_) {{')
         K6 = K5 + '  '
         o.append(f'{K6}const int kk_ = kv_ + v_;')
         for r in range(rch):
+            if preload:
+                o.append(f'{K6}acc_[pi_][{r}] = fmaf(ap_[m_][v_][{r}], wf_[v_], acc_[pi_][{r}]);')
+                continue
             renv = {**env, c.contig: ('kk_', 'int')}
             if reg:
                 rl = []
-                renv.update(self.decode_const(f'(rc_ * {rch} + {r})', reg, rl, K6))
+                renv.update(self.decode_const(f'(prc_[pi_] * {rch} + {r})', reg, rl, K6))
                 o += rl
             pre = []
             av, at = self.expr(c.A, renv, pre, K6)
             o += pre
-            guard = f'rc_ * {rch} + {r} < {rn}' if rn % rch else None
-            if guard:
-                o.append(f'{K6}if ({guard}) acc_[{r}] = fmaf({self.as_float(av, at)}, wf_[v_], acc_[{r}]);')
+            guards = []
+            if rn % rch:
+                guards.append(f'prc_[pi_] * {rch} + {r} < {rn}')
+            if not exact:
+                guards.append(f'kk_ < {K}')
+            g = ' && '.join(guards)
+            if g:
+                o.append(f'{K6}if ({g}) acc_[pi_][{r}] = fmaf({self.as_float(av, at)}, wf_[v_], acc_[pi_][{r}]);')
             else:
-                o.append(f'{K6}acc_[{r}] = fmaf({self.as_float(av, at)}, wf_[v_], acc_[{r}]);')
+                o.append(f'{K6}acc_[pi_][{r}] = fmaf({self.as_float(av, at)}, wf_[v_], acc_[pi_][{r}]);')
         o.append(f'{K5}}}')
-        o.append(f'{K4}}}')
-        o.append(f'{K3}}}')
+        o.append(f'{J2}  }}')
         o.append(f'{J2}}}')
         if lpp > 1:
             o.append(f'{J2}#pragma unroll')
-            o.append(f'{J2}for (int r_ = 0; r_ < {rch}; ++r_) acc_[r_] = group_red_sum(acc_[r_], {lpp});')
-        o.append(f'{J2}if (ok_ && cl_ == 0) {{')
-        K3 = J2 + '  '
+            o.append(f'{J2}for (int pi_ = 0; pi_ < {PI}; ++pi_)')
+            o.append(f'{J2}  #pragma unroll')
+            o.append(f'{J2}  for (int r_ = 0; r_ < {rch}; ++r_) acc_[pi_][r_] = group_red_sum(acc_[pi_][r_], {lpp});')
+        o.append(f'{J2}#pragma unroll')
+        o.append(f'{J2}for (int pi_ = 0; pi_ < {PI}; ++pi_) {{')
+        o.append(f'{J2}  if (ok_[pi_] && cl_ == 0) {{')
+        K3 = J2 + '    '
         for r in range(rch):
             fenv = dict(env)
             lines = []
             if reg:
-                lines.append(f'{K3}if (rc_ * {rch} + {r} < {rn}) {{')
+                lines.append(f'{K3}if (prc_[pi_] * {rch} + {r} < {rn}) {{')
                 K4 = K3 + '  '
-                fenv.update(self.decode_const(f'(rc_ * {rch} + {r})', reg, lines, K4))
+                fenv.update(self.decode_const(f'(prc_[pi_] * {rch} + {r})', reg, lines, K4))
             else:
                 K4 = K3
-            self.epilogue(s, c, fused, fenv, f'acc_[{r}]', lines, K4)
+            self.epilogue(s, c, fused, fenv, f'acc_[pi_][{r}]', lines, K4)
             if reg:
                 lines.append(f'{K3}}}')
             o += lines
+        o.append(f'{J2}  }}')
         o.append(f'{J2}}}')
         o.append(f'{I}}}')
         o.append(f'{ind}}}')
-        self.note(reads, writes)
-        self.mark(out, ind, f'lane {name}')
 
     # -- private
     def gen_private(self, run, out, ind):
@@ -1644,6 +1803,7 @@ class Lowering:
         self.stage_floats = max(self.stage_floats, off - base)
         if staged:
             out.append(f'{ind}__syncthreads();')
+            self.mark(out, ind, f'stage {",".join(staged)}')
         self.staged = staged
         for s in run:
             self.plan.append((show_stmt(s), 'private'))
@@ -1666,6 +1826,7 @@ class Lowering:
                 o.append(f'{I}if (lane == 0) {self.store(name, [env[a][0] for a in axes], "a_", "float")}')
                 o.append(f'{ind}}}')
             else:
+                o.append(f'{ind}#pragma unroll 4')
                 o.append(f'{ind}for (int p_ = tid; p_ < {npts}; p_ += {BLOCK}) {{  // private {name}')
                 I = ind + '  '
                 env = self.decode('p_', axes, o, I)
@@ -1675,17 +1836,27 @@ class Lowering:
                 o.append(f'{I}{self.store(name, [env[a][0] for a in axes], v, t)}')
                 o.append(f'{ind}}}')
             out.append(f'{ind}__syncthreads();')
+            self.mark(out, ind, f'private {name}')
         self.staged = {}
-        self.mark(out, ind, f'private {run[0][1]}..{run[-1][1]}')
 
     # -- group
     def gen_group(self, lead, members, out, ind):
         names = {t[1] for t in members}
+        local = self.group_local.get(id(members[0]), [])
         reads = self.root_reads([t[3] for t in members], exclude=names)
-        writes = {self.root(t[1]) for t in members}
+        writes = {self.root(t[1]) for t in members if t[1] not in local}
         self.sync(reads, writes, out, ind, members[0][1])
         for t in members:
-            self.plan.append((show_stmt(t), f'group[{", ".join(lead)}]'))
+            kind = self.contraction(t)
+            self.plan.append((show_stmt(t), f'group[{", ".join(lead)}]' + (f' {kind.kind}' if kind else '')
+                              + (' (LDS)' if t[1] in local else '')))
+        # values read only inside the group live in LDS, one leading point at a time
+        off = self.lds_floats
+        self.glocal = {}
+        for n in local:
+            self.glocal[n] = (off, len(lead))
+            off += max(1, self.size(self.axes_of[n][len(lead):]))
+        self.stage_floats = max(self.stage_floats, off - self.lds_floats)
         o = out
         I = ind + '  '
         o.append(f'{ind}for (int gp_ = blockIdx.x; gp_ < {self.count_c(lead)}; gp_ += nblk) {{  // group')
@@ -1693,7 +1864,13 @@ class Lowering:
         for t in members:
             name, axes, e = t[1], list(t[2]), t[3]
             rest = axes[len(lead):]
-            if not rest and e[0] == 'fold':
+            c = self.contraction(t)
+            if c is not None and self.block_contraction_ok(c, t, len(lead)):
+                if c.kind == 'lane':
+                    self.emit_lane(t, c, [], o, I, rest, env, 'wave', str(NWAVE))
+                else:
+                    self.emit_group_tile(t, c, env, o, I)
+            elif not rest and e[0] == 'fold':
                 op, ax, body = e[1], e[2], e[3]
                 o.append(f'{I}{{  // {name}')
                 I2 = I + '  '
@@ -1708,6 +1885,7 @@ class Lowering:
                 o.append(f'{I2}if (tid == 0) {self.store(name, [env[a][0] for a in axes], "a_", "float")}')
                 o.append(f'{I}}}')
             else:
+                o.append(f'{I}#pragma unroll 4')
                 o.append(f'{I}for (int q_ = tid; q_ < {self.count_c(rest)}; q_ += {BLOCK}) {{  // {name}')
                 I2 = I + '  '
                 env2 = {**env, **self.decode('q_', rest, o, I2)}
@@ -1718,8 +1896,97 @@ class Lowering:
                 o.append(f'{I}}}')
             o.append(f'{I}block_sync();')
         o.append(f'{ind}}}')
+        self.glocal = {}
         self.note(reads, writes)
         self.mark(out, ind, f'group {members[0][1]}..{members[-1][1]}')
+
+    def emit_group_tile(self, t, c, env, o, ind):
+        """One block computes all of t[lead point, j] = sum over the fold of
+        A * W[.., j]: lanes along j (16-byte loads), rows of the fold over the
+        block's waves, butterfly + LDS reduction over rows."""
+        name = t[1]
+        dt = self.res[c.W][1]
+        vec = c.vec
+        J = self.static[c.contig]
+        nvec = J // vec
+        lpr = 1
+        while lpr * 2 <= TILE_LANES and nvec % (lpr * 2) == 0:
+            lpr *= 2
+        tj = lpr * vec
+        nj = J // tj
+        rpw = WAVE // lpr
+        rpb = rpw * NWAVE
+        self.red_floats = max(getattr(self, 'red_floats', 4), NWAVE * tj)
+        ltype = {8: 'vh_u32x4', 4: 'vh_u32x2', 2: 'unsigned', 1: 'vh_half'}[vec] if dt == 'f16' else \
+            {4: 'vh_f32x4', 2: 'vh_f32x2', 1: 'float'}[vec]
+        I = ind + '  '
+        o.append(f'{ind}{{  // group tile {name}: W={c.W} VEC={vec} lanes/row={lpr}')
+        o.append(f'{I}const int K_ = {self.count_c(c.fold_axes)};')
+        o.append(f'{I}const int sub_ = lane / {lpr}, cl_ = lane % {lpr};')
+        o.append(f'{I}const int kb_ = wave * {rpw} + sub_;')
+        o.append(f'{I}const int n_ = kb_ < K_ ? (K_ - kb_ + {rpb - 1}) / {rpb} : 0;')
+        o.append(f'{I}for (int jt_ = 0; jt_ < {nj}; ++jt_) {{')
+        J2 = I + '  '
+        o.append(f'{J2}const int jc_ = jt_ * {tj} + cl_ * {vec};')
+        o.append(f'{J2}float acc_[{vec}];')
+        o.append(f'{J2}#pragma unroll')
+        o.append(f'{J2}for (int v_ = 0; v_ < {vec}; ++v_) acc_[v_] = 0.0f;')
+        o.append(f'{J2}for (int b_ = 0; b_ < n_; b_ += {UNROLL}) {{')
+        K3 = J2 + '  '
+        o.append(f'{K3}{ltype} wq_[{UNROLL}];')
+        o.append(f'{K3}float av_[{UNROLL}];')
+        o.append(f'{K3}#pragma unroll')
+        o.append(f'{K3}for (int u_ = 0; u_ < {UNROLL}; ++u_) {{')
+        K4 = K3 + '  '
+        o.append(f'{K4}if (b_ + u_ < n_) {{')
+        K5 = K4 + '  '
+        o.append(f'{K5}const int kr_ = kb_ + (b_ + u_) * {rpb};')
+        kenv = self.decode('kr_', c.fold_axes, o, K5, prefix='f_')
+        wenv = {**env, **kenv, c.contig: ('jc_', 'int')}
+        pre = []
+        wix = [self.index(x, wenv, pre, K5) for x in c.widx]
+        o += pre
+        o.append(f'{K5}wq_[u_] = {self.vec_load(dt, vec, c.W, self.addr(wix, self.res_strides(c.W)))};')
+        pre = []
+        av, at = self.expr(c.A, {**env, **kenv}, pre, K5)
+        o += pre
+        o.append(f'{K5}av_[u_] = {self.as_float(av, at)};')
+        o.append(f'{K4}}} else {{')
+        o.append(f'{K5}wq_[u_] = {self.vec_zero(dt, vec)};')
+        o.append(f'{K5}av_[u_] = 0.0f;')
+        o.append(f'{K4}}}')
+        o.append(f'{K3}}}')
+        o.append(f'{K3}#pragma unroll')
+        o.append(f'{K3}for (int u_ = 0; u_ < {UNROLL}; ++u_) {{')
+        o.append(f'{K4}float wf_[{vec}];')
+        o.append(f'{K4}{self.vec_unpack(dt, vec, "wq_[u_]", "wf_")}')
+        o.append(f'{K4}#pragma unroll')
+        o.append(f'{K4}for (int v_ = 0; v_ < {vec}; ++v_) acc_[v_] = fmaf(av_[u_], wf_[v_], acc_[v_]);')
+        o.append(f'{K3}}}')
+        o.append(f'{J2}}}')
+        if lpr < 64:
+            o.append(f'{J2}#pragma unroll')
+            o.append(f'{J2}for (int v_ = 0; v_ < {vec}; ++v_) acc_[v_] = wave_red_sum_hi(acc_[v_], {lpr});')
+        o.append(f'{J2}if (sub_ == 0) {{')
+        o.append(f'{J2}  #pragma unroll')
+        o.append(f'{J2}  for (int v_ = 0; v_ < {vec}; ++v_) red_sh[wave * {tj} + cl_ * {vec} + v_] = acc_[v_];')
+        o.append(f'{J2}}}')
+        o.append(f'{J2}__syncthreads();')
+        o.append(f'{J2}if (tid < {tj}) {{')
+        K3 = J2 + '  '
+        o.append(f'{K3}const float s_ = ' + ' + '.join(f'red_sh[{w * tj} + tid]' for w in range(NWAVE)) + ';')
+        o.append(f'{K3}const int i_{c.contig} = jt_ * {tj} + tid;')
+        fenv = {**env, c.contig: (f'i_{c.contig}', 'int')}
+        venv = dict(fenv)
+        venv['__acc'] = ('s_', 'float')
+        pre = []
+        v, ty = self.expr(c.epi, venv, pre, K3)
+        o += pre
+        o.append(f'{K3}{self.store(name, [fenv[a][0] for a in t[2]], v, ty)}')
+        o.append(f'{J2}}}')
+        o.append(f'{J2}__syncthreads();')
+        o.append(f'{I}}}')
+        o.append(f'{ind}}}')
 
     # -- grid reduction
     def gen_gridred(self, s, out, ind):
@@ -1771,6 +2038,65 @@ class Lowering:
         self.note(reads, writes)
         self.mark(out, ind, f'gridred {name}')
 
+    def gen_argmax(self, s1, s2, out, ind):
+        """best = fold max n: E[n]; next = lowest n with E[n] == best: one pass
+        over E keeping (value, index) pairs, ties to the lower index; per-block
+        pairs combined in block order by the last block."""
+        name, axes, e = s1[1], list(s1[2]), s1[3]
+        ax, body = e[2], e[3]
+        reads = self.root_reads([e])
+        writes = {self.root(name), self.root(s2[1])}
+        self.sync(reads, writes, out, ind, name)
+        self.plan.append((show_stmt(s1), 'gridred argmax'))
+        self.plan.append((show_stmt(s2), 'gridred argmax'))
+        npts = self.size(axes)
+        poff = self.alloc_scratch(2 * npts * GRID_MAX)
+        coff = self.alloc_counters(1)
+        o = out
+        I = ind + '  '
+        o.append(f'{ind}{{  // argmax {name}, {s2[1]}')
+        envs = []
+        for p in range(npts):
+            lines = []
+            env = self.decode_const(str(p), axes, lines, I) if axes else {}
+            envs.append(env)
+            o += lines
+            o.append(f'{I}{{')
+            o.append(f'{I}  float bv_ = -INFINITY; int bi_ = 0x7fffffff;')
+            o.append(f'{I}  for (int k_ = gtid; k_ < {self.static[ax]}; k_ += nthr) {{')
+            pre = []
+            v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '    ')
+            o += pre
+            o.append(f'{I}    const float v_ = {self.as_float(v, t)};')
+            o.append(f'{I}    if (v_ > bv_ || (v_ == bv_ && k_ < bi_)) {{ bv_ = v_; bi_ = k_; }}')
+            o.append(f'{I}  }}')
+            o.append(f'{I}  block_argmax(bv_, bi_, red_sh, (int*)(red_sh + {NWAVE}));')
+            o.append(f'{I}  if (tid == 0) {{ stc(S + {poff + p * GRID_MAX} + blockIdx.x, bv_); '
+                     f'stc(S + {poff + (npts + p) * GRID_MAX} + blockIdx.x, (float)bi_); }}')
+            o.append(f'{I}}}')
+        o.append(f'{I}if (last_arrival(bar + {coff}, nblk, &flag_sh)) {{')
+        cval = s2[3][3][3][1]
+        for p in range(npts):
+            env = envs[p]
+            o.append(f'{I}  {{')
+            o.append(f'{I}    float bv_ = -INFINITY; int bi_ = 0x7fffffff;')
+            o.append(f'{I}    for (int b_ = tid; b_ < (int)nblk; b_ += {BLOCK}) {{')
+            o.append(f'{I}      const float v_ = ldc(S + {poff + p * GRID_MAX} + b_);')
+            o.append(f'{I}      const int i_ = (int)ldc(S + {poff + (npts + p) * GRID_MAX} + b_);')
+            o.append(f'{I}      if (v_ > bv_ || (v_ == bv_ && i_ < bi_)) {{ bv_ = v_; bi_ = i_; }}')
+            o.append(f'{I}    }}')
+            o.append(f'{I}    block_argmax(bv_, bi_, red_sh, (int*)(red_sh + {NWAVE}));')
+            o.append(f'{I}    if (tid == 0) {{')
+            o.append(f'{I}      {self.store(name, [env[a][0] for a in axes], "bv_", "float")}')
+            o.append(f'{I}      {self.store(s2[1], [env[a][0] for a in axes], f"(bi_ == 0x7fffffff ? {c_float(cval)} : (float)bi_)", "float")}')
+            o.append(f'{I}    }}')
+            o.append(f'{I}  }}')
+        o.append(f'{I}}}')
+        o.append(f'{ind}}}')
+        self.note(reads, writes)
+        self.red_floats = max(getattr(self, 'red_floats', 4), 2 * NWAVE)
+        self.mark(out, ind, f'argmax {name}')
+
     # -- one thread per point
     def gen_thread(self, s, out, ind):
         name, axes, e = s[1], list(s[2]), s[3]
@@ -1779,6 +2105,7 @@ class Lowering:
         self.sync(reads, writes, out, ind, name)
         self.plan.append((show_stmt(s), 'thread'))
         I = ind + '  '
+        out.append(f'{ind}#pragma unroll 4')
         out.append(f'{ind}for (int p_ = gtid; p_ < {self.count_c(axes)}; p_ += nthr) {{  // thread {name}')
         env = self.decode('p_', axes, out, I)
         pre = []
@@ -1799,6 +2126,7 @@ class Lowering:
         self.sync(reads, {name}, out, ind, f'emit {name}')
         self.plan.append((show_stmt(s), 'thread emit'))
         I = ind + '  '
+        out.append(f'{ind}#pragma unroll 4')
         out.append(f'{ind}for (int p_ = gtid; p_ < {self.count_c(axes)}; p_ += nthr) {{  // emit {name}')
         env = self.decode('p_', axes, out, I)
         pre = []
