@@ -21,6 +21,8 @@ reference interpreter) timed on this host on a bounded sample of the same
 workload.
 """
 import argparse
+import csv
+import hashlib
 import json
 import os
 import sys
@@ -32,6 +34,7 @@ for p in (os.path.join(ROOT, 'vesta-gpu_amd'), ROOT):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'traffic.json')
 PROMPT, GEN = 128, 256
 
 
@@ -84,10 +87,92 @@ def run_config(B, steps, warmup, chunk, seed=0):
                kernel_ms_per_launch=sum(kern_ms) / len(kern_ms), steps_per_launch=chunk,
                bytes_per_step_MB=step_bytes(m, pos0 + steps // 2) / 1e6, achieved_GBps=achieved,
                grid=m.k.grid, regs=m.k.attrs['regs'], barriers_per_step=m.low.barriers_per_launch + 1,
-               weight_MB=m.weight_bytes / 1e6, tmax=tmax)
+               weight_MB=m.weight_bytes / 1e6, tmax=tmax, kernel=m.low.name,
+               src_sha=hashlib.sha256(m.low.src.encode()).hexdigest()[:16],
+               algorithmic_bytes_per_launch=sum(per_launch_bytes) / len(per_launch_bytes))
     del m
     torch.cuda.empty_cache()
     return out
+
+
+def measured_traffic(kernel, src_sha):
+    """HBM bytes per launch of this exact kernel source as measured by two
+    rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE; see --pmc-summary), or None
+    when the committed measurement is for another source."""
+    try:
+        with open(TRAFFIC_FILE) as fh:
+            table = json.load(fh)
+    except (OSError, ValueError):
+        return None
+    rec = table.get(kernel)
+    if not rec or rec.get('src_sha') != src_sha:
+        return None
+    return rec
+
+
+def pmc_summary(fetch_csv, write_csv, bench_log, calib_mib):
+    """Turn the counter CSVs of two profiled bench runs into HBM bytes per
+    launch of each Vesta kernel. FETCH_SIZE and WRITE_SIZE (KiB per dispatch)
+    are scaled so that the calibration copy of ``calib_mib`` MiB reads and
+    writes exactly its size. Updates profiles/traffic.json and prints a
+    markdown table."""
+    want = calib_mib * 1024.0
+
+    def load(path):
+        rows = list(csv.DictReader(open(path)))
+        copies = [float(r['Counter_Value']) for r in rows if 'copyBuffer' in r['Kernel_Name']
+                  or 'copy' in r['Kernel_Name'].lower()]
+        calib = max(copies)
+        per = {}
+        for r in rows:
+            if r['Kernel_Name'].startswith('vesta_step'):
+                per.setdefault(r['Kernel_Name'], []).append(float(r['Counter_Value']))
+        return calib, per
+    fc, fper = load(fetch_csv)
+    wc, wper = load(write_csv)
+    fscale, wscale = want / fc, want / wc
+    line = None
+    for ln in open(bench_log):
+        if ln.startswith('{') and '"metric"' in ln:
+            line = json.loads(ln)
+    if line is None:
+        raise SystemExit(f'no bench JSON line in {bench_log}')
+    cfgs = {line['roofline']['kernel']: line['roofline'], line['b1']['kernel']: line['b1']}
+    table = {}
+    if os.path.exists(TRAFFIC_FILE):
+        table = json.load(open(TRAFFIC_FILE))
+    print(f'| kernel | FETCH_SIZE KiB/launch | WRITE_SIZE KiB/launch | fetch bytes | write bytes | '
+          f'algorithmic bytes | traffic / algorithmic |')
+    print('|---|---|---|---|---|---|---|')
+    for k in sorted(fper):
+        f = sum(fper[k]) / len(fper[k])
+        w = sum(wper.get(k, [0.0])) / max(1, len(wper.get(k, [])))
+        fb, wb = f * 1024 * fscale, w * 1024 * wscale
+        c = cfgs[k]
+        alg = c['algorithmic_bytes_per_launch']
+        table[k] = dict(src_sha=c['src_sha'], fetch_bytes=fb, write_bytes=wb, traffic=fb + wb,
+                        algorithmic_bytes=alg, steps_per_launch=c['steps_per_launch'],
+                        fetch_scale=fscale, write_scale=wscale)
+        print(f'| {k} | {f:.0f} | {w:.0f} | {fb / 1e6:.1f} MB | {wb / 1e6:.1f} MB | {alg / 1e6:.1f} MB | '
+              f'{(fb + wb) / alg:.3f} |')
+    print(f'\nscale factors (calibration copy of {calib_mib} MiB): FETCH_SIZE x{fscale:.3f}, WRITE_SIZE x{wscale:.3f}')
+    os.makedirs(os.path.dirname(TRAFFIC_FILE), exist_ok=True)
+    with open(TRAFFIC_FILE, 'w') as fh:
+        json.dump(table, fh, indent=1, sort_keys=True)
+
+
+def calibration_copy(mib):
+    """One device-to-device copy of ``mib`` MiB (reads and writes exactly that
+    many bytes): the reference point for HBM traffic counters."""
+    import torch
+    n = mib << 20
+    src = torch.ones(n // 4, dtype=torch.float32, device='cuda')
+    dst = torch.empty_like(src)
+    torch.cuda.synchronize()
+    dst.copy_(src)
+    torch.cuda.synchronize()
+    del src, dst
+    torch.cuda.empty_cache()
 
 
 def cpu_baseline(B, sample_steps):
@@ -125,6 +210,23 @@ def cpu_baseline(B, sample_steps):
                        f'BLAS threads {threads})')
 
 
+def roofline(cfg, peak):
+    """The roofline object of one configuration's kernel: algorithmic bytes
+    per launch over the launch duration (HIP events on the launch stream),
+    and the counter-measured HBM traffic per launch when profiles/traffic.json
+    holds a measurement of this exact kernel source."""
+    rec = measured_traffic(cfg['kernel'], cfg['src_sha'])
+    return {'bound': 'hbm', 'achieved': round(cfg['achieved_GBps'], 1), 'peak': peak, 'unit': 'GB/s',
+            'frac': round(cfg['achieved_GBps'] / peak, 4),
+            'traffic': round(rec['traffic']) if rec else None,
+            'traffic_vs_algorithmic': round(rec['traffic'] / rec['algorithmic_bytes'], 3) if rec else None,
+            'kernel': cfg['kernel'], 'src_sha': cfg['src_sha'], 'grid': cfg['grid'],
+            'steps_per_launch': cfg['steps_per_launch'],
+            'algorithmic_bytes_per_launch': round(cfg['algorithmic_bytes_per_launch']),
+            'bytes_per_step_MB': round(cfg['bytes_per_step_MB'], 2),
+            'kernel_ms_per_launch': round(cfg['kernel_ms_per_launch'], 4)}
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -134,13 +236,24 @@ def main():
     ap.add_argument('--chunk', type=int, default=32)
     ap.add_argument('--cpu-steps', type=int, default=2)
     ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--pmc-summary', nargs=3, metavar=('FETCH_CSV', 'WRITE_CSV', 'BENCH_LOG'),
+                    help='summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of '
+                         '"bench.py --calibrate-copy N" into profiles/traffic.json and exit')
+    ap.add_argument('--calibrate-copy', type=int, default=0, metavar='MiB',
+                    help='first run one plain device-to-device copy of this many MiB (a kernel of known '
+                         'traffic, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)')
     args = ap.parse_args()
+    if args.pmc_summary:
+        pmc_summary(*args.pmc_summary, calib_mib=args.calibrate_copy or 1024)
+        return
     if args.gpus != 1:
         print(json.dumps({'error': 'this build runs on one GPU: the decode step is one persistent kernel on one '
                                    'device; multi-GPU sharding is designed but not built (run with --gpus 1)'}))
         sys.exit(2)
     if args.steps + args.warmup + PROMPT > 1024:
         sys.exit('prompt + warmup + steps must stay within the 1024 learned positions')
+    if args.calibrate_copy > 0:
+        calibration_copy(args.calibrate_copy)
     main_cfg = run_config(args.batch, args.steps, args.warmup, args.chunk)
     b1 = run_config(1, args.steps, args.warmup, args.chunk)
     peak = HBM_PEAK_GBPS
@@ -160,16 +273,10 @@ def main():
         'config': {'workload': f'GPT-2 small greedy decode, B={args.batch}, {PROMPT}-token prompts, '
                                f'{args.steps} generated tokens (BASELINE.json configs[1])',
                    'batch': args.batch, 'prompt': PROMPT, 'storage': 'f16 weights and key/value cache, f32 math',
-                   'steps_per_launch': args.chunk, 'grid': main_cfg['grid'],
-                   'barriers_per_step': main_cfg['barriers_per_step']},
-        'roofline': {'bound': 'hbm', 'achieved': round(main_cfg['achieved_GBps'], 1), 'peak': peak, 'unit': 'GB/s',
-                     'frac': round(main_cfg['achieved_GBps'] / peak, 4), 'traffic': None,
-                     'kernel': f'vesta_step_b{args.batch}', 'bytes_per_step_MB': round(main_cfg['bytes_per_step_MB'], 2),
-                     'kernel_ms_per_launch': round(main_cfg['kernel_ms_per_launch'], 4)},
+                   'steps_per_launch': args.chunk, 'barriers_per_step': main_cfg['barriers_per_step']},
+        'roofline': roofline(main_cfg, peak),
         'b1': {'tok_s': round(b1['tok_s'], 1), 'ms_per_step': round(b1['ms_per_step'], 4),
-               'achieved_GBps': round(b1['achieved_GBps'], 1), 'frac': round(b1['achieved_GBps'] / peak, 4),
-               'bytes_per_step_MB': round(b1['bytes_per_step_MB'], 2), 'grid': b1['grid'],
-               'barriers_per_step': b1['barriers_per_step']},
+               'barriers_per_step': b1['barriers_per_step'], **roofline(b1, peak)},
     }
     if not args.no_cpu:
         line['cpu_baseline'] = cpu_baseline(args.batch, args.cpu_steps)
