@@ -7,8 +7,10 @@
 // vector-memory atomics; nothing here writes through the scalar cache.
 
 #define VWAVE 64
-#define VBLOCK 256
-#define VNWAVE 4
+#ifndef VBLOCK
+#define VBLOCK 512
+#endif
+#define VNWAVE (VBLOCK / VWAVE)
 #ifndef INFINITY
 #define INFINITY __builtin_huge_valf()
 #endif
@@ -156,6 +158,38 @@ __device__ __forceinline__ vh_u32x2 ldc8_h(vh_rsrc r, unsigned i) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, i * 2u, 0, VH_SC1);
 }
 
+// Loads and stores through buffer descriptors: a 32-bit element offset per
+// lane (one register per address) over a base held in scalar registers.
+#define VH_NT 2     // cache-policy bit: nontemporal (streamed once)
+__device__ __forceinline__ float ldcs(vh_rsrc r, unsigned i) {       // coherent fp32
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, VH_SC1));
+}
+__device__ __forceinline__ void stcs(vh_rsrc r, unsigned i, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), r, i * 4u, 0, VH_SC1);
+}
+__device__ __forceinline__ float ldg_h(vh_rsrc r, unsigned i) {      // read-only residues
+  return h2f(__builtin_bit_cast(vh_half, __builtin_amdgcn_raw_buffer_load_b16(r, i * 2u, 0, 0)));
+}
+__device__ __forceinline__ unsigned short ldg_raw16(vh_rsrc r, unsigned i) {
+  return __builtin_amdgcn_raw_buffer_load_b16(r, i * 2u, 0, 0);
+}
+__device__ __forceinline__ float ldg_f(vh_rsrc r, unsigned i) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, 0));
+}
+__device__ __forceinline__ int ldg_i(vh_rsrc r, unsigned i) {
+  return (int)__builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, 0);
+}
+// 16 / 8 / 4 bytes of fp16 starting at element i, streamed (nontemporal).
+__device__ __forceinline__ vh_u32x4 ldg16_nt(vh_rsrc r, unsigned i) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, i * 2u, 0, VH_NT);
+}
+__device__ __forceinline__ vh_u32x2 ldg8_nt(vh_rsrc r, unsigned i) {
+  return __builtin_amdgcn_raw_buffer_load_b64(r, i * 2u, 0, VH_NT);
+}
+__device__ __forceinline__ unsigned ldg4_nt(vh_rsrc r, unsigned i) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, i * 2u, 0, VH_NT);
+}
+
 // Wait until every memory operation this wave issued has completed. The
 // signal fences keep the compiler from moving memory operations across it.
 __device__ __forceinline__ void drain() {
@@ -168,6 +202,34 @@ __device__ __forceinline__ void drain() {
 __device__ __forceinline__ void block_sync() {
   drain();
   __syncthreads();
+}
+
+// Four floats of global scratch at float index i (a multiple of 4), coherent.
+__device__ __forceinline__ vh_f32x4 ldc4(vh_rsrc r, unsigned i) {
+  return __builtin_bit_cast(vh_f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, i * 4u, 0, VH_SC1));
+}
+
+// Copy n floats of global scratch starting at float index `off` (a multiple
+// of 4) into LDS (16-byte aligned) with every thread of the block: 16-byte
+// coherent loads, up to 8 in flight per thread; the tail past n reads zeros.
+// Every block reads the same vector at about the same time: each block starts
+// at its own rotation of it so the requests spread over memory channels.
+__device__ __forceinline__ void stage_ldc4(float* dst, vh_rsrc S, unsigned off, int n) {
+  const int nv = (n + 3) >> 2;
+  const int rot = (int)((blockIdx.x * 37u) % (unsigned)nv);
+  for (int base = threadIdx.x; base < nv; base += VBLOCK * 8) {
+    vh_f32x4 v[8];
+    int ix[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      int j = base + u * VBLOCK + rot;
+      ix[u] = j >= nv ? j - nv : j;
+      v[u] = base + u * VBLOCK < nv ? ldc4(S, off + 4u * (unsigned)ix[u]) : vh_f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (base + u * VBLOCK < nv) *(vh_f32x4*)(dst + 4 * ix[u]) = v[u];
+  }
 }
 
 // Copy n floats of global scratch (coherent loads) into LDS with every
@@ -184,38 +246,69 @@ __device__ __forceinline__ void stage_ldc(float* dst, const float* src, int n) {
 }
 
 // ---------------------------------------------------------------- grid sync
-// Two-level arrival: block b arrives on the counter of group b % 8 (one
-// 128-byte line each); the last arriver of a group arrives on the top
-// counter; the last of those publishes generation `gen` in bar[0], which
-// every block's thread 0 polls. Counters are reset by their last arriver, so
-// they are zero between launches. bar[0] keeps the last generation; the
-// caller starts from the value it reads at kernel start and adds one per
-// barrier (only thread 0's copy is used).
+// Split-phase grid barrier over monotonic arrival counters, one per XCD
+// (block b arrives on counter b % 8, one 128-byte line each; consecutive
+// blocks are dispatched to consecutive XCDs). grid_arrive() publishes that
+// everything the block stored so far is complete; grid_wait(k) returns once
+// every block has arrived k times in this launch. Between the two a block may
+// issue work that does not depend on other blocks (weight loads). Counters only
+// grow during a launch; grid_exit() lets the last block out of the kernel zero
+// them, so they are zero between launches.
 #define VH_BAR_GROUPS 8
 #define VH_BAR_LINE 32
 #define VH_BAR_WORDS (VH_BAR_LINE * (VH_BAR_GROUPS + 2))
-__device__ __forceinline__ void grid_sync(unsigned* bar, unsigned nblk, unsigned& gen) {
+#define VH_SPIN_LIMIT (1u << 24)
+__device__ __forceinline__ void grid_arrive(unsigned* bar) {
   drain();
   __syncthreads();
-  if (threadIdx.x == 0) {
-    gen += 1u;
-    const unsigned ng = nblk < VH_BAR_GROUPS ? nblk : VH_BAR_GROUPS;
-    const unsigned g = blockIdx.x % ng;
-    const unsigned members = (nblk - g + ng - 1u) / ng;
-    unsigned* gc = bar + VH_BAR_LINE * (2u + g);
-    unsigned* top = bar + VH_BAR_LINE;
-    if (__hip_atomic_fetch_add(gc, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == members - 1u) {
-      stc_u(gc, 0u);
-      drain();
-      if (__hip_atomic_fetch_add(top, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == ng - 1u) {
-        stc_u(top, 0u);
-        drain();
-        stc_u(bar, gen);
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(bar + VH_BAR_LINE * (blockIdx.x % VH_BAR_GROUPS), 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+}
+// Lanes 0..7 of the polling wave (the block's last wave, which never has
+// loads issued ahead of time in flight, so its polls complete as soon as the
+// counters answer) each watch one counter. A wait that does not end within
+// VH_SPIN_LIMIT polls (seconds) gives up and raises the error word
+// bar[VH_BAR_LINE * 9 + 1] (only a broken launch configuration can get there).
+#define VH_POLL_WAVE (VNWAVE - 1)
+__device__ __forceinline__ unsigned ldc_ub(vh_rsrc r, unsigned i) {
+  return __builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, VH_SC1);
+}
+__device__ __forceinline__ void grid_wait(unsigned* bar, unsigned nblk, unsigned k) {
+  if ((int)(threadIdx.x >> 6) == VH_POLL_WAVE) {
+    const vh_rsrc rb = mk_rsrc(bar, VH_BAR_WORDS * 4u);
+    const unsigned g = threadIdx.x & 63u;
+    bool done = g >= VH_BAR_GROUPS || g >= nblk;
+    const unsigned target = done ? 0u : k * ((nblk - g + VH_BAR_GROUPS - 1u) / VH_BAR_GROUPS);
+    unsigned n = 0;
+    while (true) {
+      if (!done) done = ldc_ub(rb, VH_BAR_LINE * g) >= target;
+      if (__all(done)) break;
+      __builtin_amdgcn_s_sleep(1);
+      if (++n > VH_SPIN_LIMIT) {
+        if (g == 0) stc_u(bar + VH_BAR_LINE * 9 + 1, 1u);
+        break;
       }
     }
-    while (ldc_u(bar) != gen) __builtin_amdgcn_s_sleep(1);
   }
   __syncthreads();
+}
+__device__ __forceinline__ void grid_sync(unsigned* bar, unsigned nblk, unsigned& k) {
+  k += 1u;
+  grid_arrive(bar);
+  grid_wait(bar, nblk, k);
+}
+// Called by every block once it will wait no more: the last block to get
+// here zeroes the arrival counters and the exit counter.
+__device__ __forceinline__ void grid_exit(unsigned* bar, unsigned nblk) {
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned* ex = bar + VH_BAR_LINE * VH_BAR_GROUPS;
+    if (__hip_atomic_fetch_add(ex, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nblk - 1u) {
+      for (unsigned g = 0; g < VH_BAR_GROUPS; ++g) stc_u(bar + VH_BAR_LINE * g, 0u);
+      stc_u(ex, 0u);
+    }
+  }
 }
 
 // Split reductions: after storing its partial (coherent stores), a block
@@ -236,3 +329,11 @@ __device__ __forceinline__ bool last_arrival(unsigned* cnt, unsigned total, int*
 }
 
 __device__ __forceinline__ unsigned long long vh_clock() { return wall_clock64(); }
+
+// The thread index as a value the compiler cannot see through: rebinding it
+// at the top of a loop body keeps per-site address arithmetic inside the
+// site instead of being hoisted out of the loop (which spills registers).
+__device__ __forceinline__ int vh_opaque(int v) {
+  asm volatile("" : "+v"(v));
+  return v;
+}

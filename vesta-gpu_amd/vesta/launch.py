@@ -131,13 +131,13 @@ class Kernel:
     cooperatively on torch's current stream (reference launch.py:29-73).
 
     grid = blocks that fit per CU (occupancy at ``block`` threads and the
-    kernel's LDS) x CUs, optionally capped by ``blocks_per_sm`` and by the
-    lowering's own grid limit. ``S`` (fp32 scratch), ``bar`` (barrier and
+    kernel's LDS, at most the lowering's ``per_cu_max``) x CUs, optionally
+    capped by ``blocks_per_sm`` and by the lowering's own grid limit. ``S`` (fp32 scratch), ``bar`` (barrier and
     reduction counters, zeroed once; the kernel leaves them zeroed) and ``TS``
     (timing sums) are allocated here.
     """
 
-    def __init__(self, lowered, block=256, device=0, blocks_per_sm=None):
+    def __init__(self, lowered, block=None, device=0, blocks_per_sm=None):
         torch = _torch()
         if not torch.cuda.is_available():
             raise RuntimeError('no GPU: the Vesta kernel needs a ROCm device')
@@ -147,6 +147,7 @@ class Kernel:
         self.info = device_info(device)
         if not self.info['cooperative']:
             raise RuntimeError('device does not support cooperative launch')
+        block = lowered.block if block is None else block
         if block != lowered.block:
             raise ValueError(f'kernel was lowered for {lowered.block} threads per block, not {block}')
         self.code = compile_code(lowered.src)
@@ -161,12 +162,15 @@ class Kernel:
             ok(L.vh_function_set_dynamic_lds(fn, self.smem), 'dynamic LDS')
         per = ctypes.c_int()
         ok(L.vh_occupancy(fn, block, self.smem, ctypes.byref(per)), 'occupancy')
-        per_cu = per.value
+        per_cu = min(per.value, lowered.per_cu_max)
         if blocks_per_sm:
             per_cu = min(per_cu, blocks_per_sm)
         self.per_cu = per_cu
         self.cus = self.info['cu_count']
-        self.grid = min(per_cu * self.cus, lowered.grid_max)
+        if per_cu * self.cus < lowered.grid_max:
+            raise RuntimeError(f'the kernel is laid out for {lowered.grid_max} resident blocks; this device holds '
+                               f'{per_cu} per CU x {self.cus} CUs')
+        self.grid = lowered.grid_max
         self.block = block
         regs, slds, priv, mxb = (ctypes.c_int() for _ in range(4))
         ok(L.vh_function_attrs(fn, ctypes.byref(regs), ctypes.byref(slds), ctypes.byref(priv), ctypes.byref(mxb)),
@@ -187,10 +191,18 @@ class Kernel:
         return self.S[off:off + max(1, n)].view(*shape) if shape else self.S[off]
 
     def bind(self, residue):
-        """Fix the argument list once; a launch is then one shim call."""
+        """Fix the argument list once; a launch is then one shim call. Residues
+        the kernel reads through a transposed copy are copied here: bind again
+        after changing them."""
         vals = []
+        self._packed = {}
         for name, dt, _ in self.lowered.params:
-            t = residue[name]
+            if name in self.lowered.packs:
+                # a copy of a read-only residue transposed in its last two axes (made once, here)
+                t = residue[self.lowered.packs[name]].transpose(-1, -2).contiguous()
+                self._packed[name] = t
+            else:
+                t = residue[name]
             if not (t.is_cuda and t.dtype == TORCH_DT[dt] and t.is_contiguous()):
                 raise TypeError(f'residue {name}: need a contiguous {dt} device tensor, got {t.dtype} '
                                 f'{"device" if t.is_cuda else "host"} {"contiguous" if t.is_contiguous() else "strided"}')

@@ -56,19 +56,22 @@ the inner products of tile and lane sites use fused multiply-add.
 from __future__ import annotations
 
 import math
+import re
 from dataclasses import dataclass, field
 from pathlib import Path
 
 import numpy as np
 
 from .interp import parse
+from .stream import StreamMixin
 
 PRELUDE_PATH = Path(__file__).resolve().parent / 'hip' / 'prelude.h'
 
-WAVE, NWAVE = 64, 4
-BLOCK = WAVE * NWAVE          # threads per block: one wave per SIMD of a CU
+WAVE, NWAVE = 64, 8
+BLOCK = WAVE * NWAVE          # threads per block: two waves per SIMD, one block per CU
 KCAP = 32                     # split-K: at most this many partials per tile column block
 GRID_MAX = 1024               # grid reductions keep one partial per block, for up to this many blocks
+GRID_DEFAULT = 256            # blocks per launch: one per CU of an MI355X
 REG_MAX = 8                   # register axes: at most this many accumulator rows per lane
 PRIV_SIZE = 8192              # a private value holds at most this many floats
 PRIV_WORK = 1 << 17           # ... and costs at most this many operations per block
@@ -83,7 +86,7 @@ GRIDRED_POINTS = 8
 UNROLL = 8                    # rows (tile) / vectors (lane) whose loads are issued together
 TILE_LANES = 8                # tile: lanes per row (8 x 16 bytes = one 128-byte line of a weight row)
 LINE_WORDS = 32               # one 128-byte line per counter
-BAR_WORDS = LINE_WORDS * 10   # grid barrier: generation word, top counter, 8 group counters
+BAR_WORDS = LINE_WORDS * 10   # grid barrier: 8 per-XCD arrival counters, exit counter, error word
 
 FOLD_INIT = {'sum': '0.0f', 'max': '-INFINITY', 'min': 'INFINITY'}
 FOLD_OP = {'sum': 'op_sum', 'max': 'op_max', 'min': 'op_min'}
@@ -107,6 +110,8 @@ class Lowered:
     grid_max: int = GRID_MAX
     shapes: dict = field(default_factory=dict)    # residue name -> shape
     name: str = 'vesta_step'                      # the kernel's symbol
+    per_cu_max: int = 1                           # resident blocks per CU the kernel is laid out for
+    packs: dict = field(default_factory=dict)     # transposed copy -> residue it is made from (at bind)
 
 
 # ------------------------------------------------------------------ AST helpers
@@ -310,8 +315,11 @@ class LowerError(ValueError):
     pass
 
 
-class Lowering:
-    def __init__(self, stmts, res, axis_max, outputs, batch, timing=False):
+class Lowering(StreamMixin):
+    NWAVE, BLOCK, REG_MAX = NWAVE, BLOCK, REG_MAX
+    show_stmt = staticmethod(show_stmt)
+
+    def __init__(self, stmts, res, axis_max, outputs, batch, timing=False, grid=None):
         self.res = {n: (tuple(int(x) for x in shp), dt) for n, (shp, dt) in res.items()}
         self.axis_max = dict(axis_max or {})
         self.outputs = set(outputs)
@@ -333,6 +341,14 @@ class Lowering:
         self.step_env = {}
         self.fb_targets = set()
         self.inlined = []
+        self.grid = int(grid or GRID_DEFAULT)
+        self.packs = {}           # transposed copy -> the residue it is made from
+        self.decls = []           # kernel-scope declarations (prefetch registers)
+        self.pf_slots = []        # prefetch code per grid barrier
+        self.last_pf = None
+        self.loops = []
+        self.stage_top = 0
+        self.capture = None
         self.scan(stmts)
         stmts = self.normalise(stmts)
         stmts = self.hoist(stmts)
@@ -883,20 +899,20 @@ class Lowering:
             for lo, hi, uoff, usize in sorted(used, key=lambda u: u[2]):
                 if off + size <= uoff:
                     break
-                off = max(off, uoff + usize)
+                off = max(off, -(-(uoff + usize) // 4) * 4)     # 16-byte aligned for vector LDS reads
             if off + size > PRIV_BUDGET:
                 raise LowerError(f'private values exceed the LDS budget at {n}')
             used.append((a, b, off, size))
             self.lds[n] = off
             top = max(top, off + size)
-        self.lds_floats = top
+        self.lds_floats = -(-top // 4) * 4
         self.g, self.goff = {}, 0
         for n in self.axes_of:
             r = self.root(n)
             if r in self.private or r in self.g or n in self.inlined:
                 continue
             self.g[r] = self.goff
-            self.goff += max(1, self.size(self.axes_of[r]))
+            self.goff += -(-max(1, self.size(self.axes_of[r])) // LINE_WORDS) * LINE_WORDS
         self.counters = BAR_WORDS
         self.staged = {}
         self.glocal = {}
@@ -904,7 +920,7 @@ class Lowering:
 
     def alloc_scratch(self, n):
         off = self.goff
-        self.goff += n
+        self.goff += -(-n // LINE_WORDS) * LINE_WORDS
         return off
 
     def alloc_counters(self, n):
@@ -999,6 +1015,16 @@ class Lowering:
             op, ax, body = e[1], e[2], e[3]
             if ax not in self.static:
                 raise ValueError(f'fold over unknown axis {ax}')
+            saved_cap, self.capture = self.capture, None
+            try:
+                return self.expr_fold(e, env, out, ind)
+            finally:
+                self.capture = saved_cap
+        raise LowerError(f'cannot lower {e}')
+
+    def expr_fold(self, e, env, out, ind):
+        if True:
+            op, ax, body = e[1], e[2], e[3]
             acc = self.fresh('acc')
             kv = self.fresh(f'k_{ax}_')
             out.append(f'{ind}float {acc} = {FOLD_INIT[op]};')
@@ -1010,7 +1036,6 @@ class Lowering:
             out.append(f'{ind}  {acc} = {FOLD_OP[op]}({acc}, {self.as_float(v, t)});')
             out.append(f'{ind}}}')
             return acc, 'float'
-        raise LowerError(f'cannot lower {e}')
 
     def as_float(self, a, t):
         if t == 'float':
@@ -1069,11 +1094,46 @@ class Lowering:
             if dt == 'f32':
                 return f'ldc(R_{n} + {addr})', 'float'
             return f'ldc_i(R_{n} + {addr})', 'int'
+        rr = self.rsrc(n)
         if dt == 'f16':
-            return f'h2f(R_{n}[{addr}])', 'float'
+            return self.captured(f'ldg_h({rr}, {addr})', raw=(f'ldg_raw16({rr}, {addr})', 'unsigned short', 'h2f')), 'float'
         if dt == 'f32':
-            return f'R_{n}[{addr}]', 'float'
-        return f'R_{n}[{addr}]', 'int'
+            return self.captured(f'ldg_f({rr}, {addr})'), 'float'
+        return self.captured(f'ldg_i({rr}, {addr})', 'int'), 'int'
+
+    def rsrc(self, n):
+        """Buffer descriptor over residue n."""
+        shape, dt = self.res[n]
+        nbytes = max(1, math.prod(shape)) * ELEM_BYTES[dt]
+        if nbytes >= 1 << 32:
+            raise LowerError(f'residue {n} is {nbytes} bytes; buffer access is limited to 4 GiB')
+        return f'mk_rsrc(R_{n}, {nbytes}u)'
+
+    def captured(self, text, kind='float', root=None, raw=None):
+        """Inside a capture (code generated for a site whose loads are issued
+        early, at its barrier), a load becomes a register filled there; loads
+        of values that may be written after that point stay in place."""
+        cap = self.capture
+        if cap is None or (root is not None and (root in cap['unsafe'] or root in self.dirty)):
+            return text
+        if any(re.search(r'\b' + re.escape(v) + r'\b', text) for v in cap.get('forbid', ())):
+            return text
+        dd = cap.get('dedupe')
+        if dd is not None and text in dd:
+            return dd[text]
+        name = f"{cap['prefix']}{len(cap['loads'])}"
+        if raw is not None:
+            # keep the loaded bits; convert where the value is used, so nothing
+            # waits for the load where it is issued
+            load, ctype, conv = raw
+            cap['loads'].append((name, load, ctype))
+            use = f'{conv}({name})'
+        else:
+            cap['loads'].append((name, text, kind))
+            use = name
+        if dd is not None:
+            dd[text] = use
+        return use
 
     def load(self, n, ix):
         """A local: LDS if private or staged, else a coherent load of global scratch."""
@@ -1086,7 +1146,7 @@ class Lowering:
         if r in self.glocal:
             off, plen = self.glocal[r]
             return f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}]'
-        return f'ldc(S + {self.g[r]} + {a})'
+        return self.captured(f'ldcs(rb_S, {self.g[r]} + {a})', 'float', r)
 
     def store(self, n, ix, v, t):
         r = self.root(n)
@@ -1096,7 +1156,7 @@ class Lowering:
         if r in self.glocal:
             off, plen = self.glocal[r]
             return f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}] = {self.as_float(v, t)};'
-        return f'stc(S + {self.g[r]} + {a}, {self.as_float(v, t)});'
+        return f'stcs(rb_S, {self.g[r]} + {a}, {self.as_float(v, t)});'
 
     def decode(self, var, axes, out, ind, prefix='i_'):
         """Lines binding prefix+axis for each axis from flat index ``var``
@@ -1141,20 +1201,28 @@ class Lowering:
             self.barrier(out, ind, what)
         self.readers |= gl_reads
 
-    def barrier(self, out, ind, what=''):
-        out.append(f'{ind}grid_sync(bar, nblk, bgen_);' + (f'  // before {what}' if what else ''))
+    def barrier(self, out, ind, what='', pre_wait=()):
+        out.append(f'{ind}bk_ += 1u; grid_arrive(bar);' + (f'  // before {what}' if what else ''))
+        out += [ind + x for x in pre_wait]
+        self.pf_open(out, ind, self.dirty)
+        out.append(f'{ind}grid_wait(bar, nblk, bk_);')
+        if self.loops:
+            self.loops[-1]['body_barrier'] = True
         self.barriers += self.mult
         self.dirty, self.readers = set(), set()
         self.mark(out, ind, f'barrier before {what}')
 
     def mark(self, out, ind, label):
         if not self.timing:
+            # a site boundary the compiler keeps: code is not scheduled across
+            # it, which keeps register live ranges inside their site
+            out.append(f'{ind}asm volatile("");')
             return
         k = len(self.sites)
         if k >= 1024:
             return
         self.sites.append(label)
-        out.append(f'{ind}if (gtid == 0) {{ unsigned long long tn_ = vh_clock(); TS[{k}] += tn_ - tlast_; '
+        out.append(f'{ind}if (gtid == 0) {{ unsigned long long tn_ = vh_clock(); ts_sh[{k}] += tn_ - tlast_; '
                    f'tlast_ = tn_; }}')
 
     # ------------------------------------------------------------ statements
@@ -1190,7 +1258,10 @@ class Lowering:
                 continue
             if p in ('tile', 'lane'):
                 fused = self.fusable(ss, i)
-                if p == 'tile':
+                st = self.stream_of(self.info[id(s)])
+                if st is not None:
+                    self.gen_stream(s, self.info[id(s)], st, fused, out, ind)
+                elif p == 'tile':
                     self.gen_tile(s, self.info[id(s)], fused, out, ind)
                 else:
                     self.gen_lane(s, self.info[id(s)], fused, out, ind)
@@ -1341,6 +1412,13 @@ class Lowering:
                 out.append(f'{ind}{self.store(t_[1], [env[a][0] for a in t_[2]], nv, "float")}')
                 made[t_[1]] = nv
             else:
+                saved_cap, self.capture = self.capture, None
+                self.epilogue_emit(t_, inv, env, made, out, ind)
+                self.capture = saved_cap
+
+    def epilogue_emit(self, t_, inv, env, made, out, ind):
+        if True:
+            if True:
                 src, plan = inv
                 lines, cond, eenv = [], [], dict(env)
                 for axis, const, order, radix in plan:
@@ -1536,13 +1614,13 @@ class Lowering:
 
         o.append(f'{J2}if (ks_ == 1) {{')
         o.append(f'{J2}  for (int q_ = tid; q_ < {q}; q_ += {BLOCK}) {{')
-        o.append(f'{J2}    const float s_ = red_sh[q_] + red_sh[{q} + q_] + red_sh[{2 * q} + q_] + red_sh[{3 * q} + q_];')
+        o.append(f'{J2}    const float s_ = ' + ' + '.join(f'red_sh[{w * q} + q_]' for w in range(NWAVE)) + ';')
         finish('s_', o, J2 + '    ')
         o.append(f'{J2}  }}')
         o.append(f'{J2}}} else {{')
         o.append(f'{J2}  for (int q_ = tid; q_ < {q}; q_ += {BLOCK})')
-        o.append(f'{J2}    stc(S + {poff} + (size_t)it_ * {q} + q_, red_sh[q_] + red_sh[{q} + q_] + red_sh[{2 * q} + q_] '
-                 f'+ red_sh[{3 * q} + q_]);')
+        o.append(f'{J2}    stc(S + {poff} + (size_t)it_ * {q} + q_, '
+                 + ' + '.join(f'red_sh[{w * q} + q_]' for w in range(NWAVE)) + ');')
         o.append(f'{J2}  if (last_arrival(bar + {coff} + tl_ * {LINE_WORDS}, (unsigned)ks_, &flag_sh)) {{')
         o.append(f'{J2}    for (int q_ = tid; q_ < {q}; q_ += {BLOCK}) {{')
         o.append(f'{J2}      float p_[{KCAP}];')
@@ -1798,8 +1876,8 @@ class Lowering:
                 size = self.size(self.axes_of[r])
                 if off - base + size <= STAGE_MAX:
                     staged[r] = off
-                    out.append(f'{ind}stage_ldc(sh_f + {off}, S + {self.g[r]}, {size});  // stage {r}')
-                    off += size
+                    out.append(f'{ind}stage_ldc4(sh_f + {off}, rb_S, {self.g[r]}, {size});  // stage {r}')
+                    off += -(-size // 4) * 4
         self.stage_floats = max(self.stage_floats, off - base)
         if staged:
             out.append(f'{ind}__syncthreads();')
@@ -1811,33 +1889,159 @@ class Lowering:
             npts = self.size(axes)
             o = out
             if e[0] == 'fold' and npts <= 64 and self.static[e[2]] >= 64:
-                op, ax, body = e[1], e[2], e[3]
-                o.append(f'{ind}for (int p_ = wave; p_ < {npts}; p_ += {NWAVE}) {{  // private {name}')
-                I = ind + '  '
-                env = self.decode('p_', axes, o, I)
-                o.append(f'{I}float a_ = {FOLD_INIT[op]};')
-                o.append(f'{I}for (int k_ = lane; k_ < {self.ext_c(ax)}; k_ += {WAVE}) {{')
-                pre = []
-                v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '  ')
-                o += pre
-                o.append(f'{I}  a_ = {FOLD_OP[op]}(a_, {self.as_float(v, t)});')
-                o.append(f'{I}}}')
-                o.append(f'{I}a_ = wave_red_{op}(a_);')
-                o.append(f'{I}if (lane == 0) {self.store(name, [env[a][0] for a in axes], "a_", "float")}')
-                o.append(f'{ind}}}')
+                self.private_fold(name, axes, e, npts, o, ind)
+            elif axes and -(-self.static[axes[-1]] // ((NWAVE - 1) * WAVE)) <= 8:
+                self.private_points(s, npts, o, ind)
             else:
-                o.append(f'{ind}#pragma unroll 4')
-                o.append(f'{ind}for (int p_ = tid; p_ < {npts}; p_ += {BLOCK}) {{  // private {name}')
+                T = -(-npts // BLOCK)
+                o.append(f'{ind}#pragma unroll' + ('' if T <= 16 else ' 8'))
+                o.append(f'{ind}for (int it_ = 0; it_ < {T}; ++it_) {{  // private {name}')
                 I = ind + '  '
-                env = self.decode('p_', axes, o, I)
+                o.append(f'{I}const int p_ = tid + it_ * {BLOCK};')
+                o.append(f'{I}if (p_ < {npts}) {{')
+                I2 = I + '  '
+                env = self.decode('p_', axes, o, I2)
                 pre = []
-                v, t = self.expr(e, env, pre, I)
+                v, t = self.expr(e, env, pre, I2)
                 o += pre
-                o.append(f'{I}{self.store(name, [env[a][0] for a in axes], v, t)}')
+                o.append(f'{I2}{self.store(name, [env[a][0] for a in axes], v, t)}')
+                o.append(f'{I}}}')
                 o.append(f'{ind}}}')
             out.append(f'{ind}__syncthreads();')
             self.mark(out, ind, f'private {name}')
         self.staged = {}
+
+    def private_points(self, s, npts, o, ind):
+        """An elementwise private statement: the last axis runs over the threads
+        (``tid + j * BLOCK``, j unrolled), the leading axes in a loop. Loads
+        that depend only on the last axis and on step variables (layer-norm
+        gains) may be issued early, at the barrier before, into registers
+        shared by all leading points."""
+        name, axes, e = s[1], list(s[2]), s[3]
+        lead, last = axes[:-1], axes[-1]
+        nl = self.static[last]
+        NCT = (NWAVE - 1) * WAVE           # compute threads: the polling wave takes no points
+        TJ = -(-nl // NCT)
+        nlead = self.size(lead)
+        sid = self.fresh('p')
+        unsafe = self.unsafe_early()
+        lead_vars = [f'i_{a}' for a in lead] + ['pl_']
+
+        def body_env():
+            env = {last: (f'i_{last}', 'int')}
+            if lead:
+                env.update(self.decode('pl_', lead, [], ''))
+            return env
+
+        def frame(jl, inner, with_lead):
+            lines = [f'{{ const int i_{last} = tid + {jl * NCT};', f'  if (tid < {NCT} && i_{last} < {nl}) {{']
+            if with_lead and lead:
+                lines.append(f'    for (int pl_ = 0; pl_ < {nlead}; ++pl_) {{')
+                lines += ['      ' + x for x in self.decode_lines('pl_', lead)]
+                lines += ['      ' + x for x in inner]
+                lines.append('    }')
+            else:
+                lines += ['    ' + x for x in inner]
+            return lines + ['  }', '}']
+
+        regs = []
+
+        def make(step_override):
+            saved = dict(self.step_env)
+            if step_override is not None and self.loops:
+                self.step_env[self.loops[-1]['var']] = step_override
+            lines = []
+            try:
+                for jl in range(TJ):
+                    self.capture = {'prefix': f'pp_{sid}_{jl}_', 'loads': [], 'unsafe': unsafe, 'dedupe': {},
+                                    'forbid': lead_vars}
+                    self.expr(e, body_env(), [], '')
+                    got = self.capture['loads']
+                    self.capture = None
+                    if step_override is None or step_override[0] == '0':
+                        regs.extend((n, k) for n, _, k in got)
+                    if got:
+                        lines += frame(jl, [f'{n} = {t};' for n, t, _ in got], False)
+            finally:
+                self.capture = None
+                self.step_env.clear()
+                self.step_env.update(saved)
+            return lines
+        self.place_prefetch(make, o, ind)
+        seen = set()
+        for n, k in regs:
+            if n not in seen:
+                seen.add(n)
+                self.decls.append(f'{self.cap_ctype(k)} {n};')
+        o.append(f'{ind}// private {name}')
+        for jl in range(TJ):
+            self.capture = {'prefix': f'pp_{sid}_{jl}_', 'loads': [], 'unsafe': unsafe, 'dedupe': {},
+                            'forbid': lead_vars}
+            try:
+                env = body_env()
+                pre = []
+                v, t = self.expr(e, env, pre, '')
+                inner = pre + [self.store(name, [env[a][0] for a in axes], v, t)]
+                o += [ind + x for x in frame(jl, inner, True)]
+            finally:
+                self.capture = None
+
+    @staticmethod
+    def cap_ctype(kind):
+        return {'int': 'int', 'float': 'float'}.get(kind, kind)
+
+    def decode_lines(self, var, axes):
+        lines = []
+        self.decode(var, axes, lines, '')
+        return lines
+
+    def private_fold(self, name, axes, e, npts, o, ind):
+        """A fold into a few points, every wave of the block working: each
+        point's fold is split over G waves (lanes strided along the fold),
+        wave partials combined in a fixed order through LDS."""
+        op, ax, body = e[1], e[2], e[3]
+        K = self.static[ax]
+        if npts >= NWAVE:
+            G = 1
+        else:
+            G = 1
+            while G * 2 * npts <= NWAVE:
+                G *= 2
+        per = G * WAVE
+        T = -(-K // per)
+        self.red_floats = max(getattr(self, 'red_floats', 4), min(npts, NWAVE) * G)
+        o.append(f'{ind}for (int w_ = wave; w_ < {npts * G}; w_ += {NWAVE}) {{  // private {name}')
+        I = ind + '  '
+        o.append(f'{I}const int p_ = w_ / {G}, q_ = w_ % {G};')
+        env = self.decode('p_', axes, o, I)
+        o.append(f'{I}float a_ = {FOLD_INIT[op]};')
+        o.append(f'{I}#pragma unroll' + ('' if T <= 16 else ' 8'))
+        o.append(f'{I}for (int it_ = 0; it_ < {T}; ++it_) {{')
+        o.append(f'{I}  const int k_ = q_ * {WAVE} + lane + it_ * {per};')
+        o.append(f'{I}  if (k_ < {self.ext_c(ax)}) {{')
+        pre = []
+        v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '    ')
+        o += pre
+        o.append(f'{I}    a_ = {FOLD_OP[op]}(a_, {self.as_float(v, t)});')
+        o.append(f'{I}  }}')
+        o.append(f'{I}}}')
+        o.append(f'{I}a_ = wave_red_{op}(a_);')
+        if G == 1:
+            o.append(f'{I}if (lane == 0) {self.store(name, [env[a][0] for a in axes], "a_", "float")}')
+            o.append(f'{ind}}}')
+            return
+        o.append(f'{I}if (lane == 0) red_sh[w_] = a_;')
+        o.append(f'{ind}}}')
+        o.append(f'{ind}__syncthreads();')
+        o.append(f'{ind}if (tid < {npts}) {{')
+        I = ind + '  '
+        o.append(f'{I}const int p_ = tid;')
+        env = self.decode('p_', axes, o, I)
+        o.append(f'{I}float a_ = red_sh[p_ * {G}];')
+        o.append(f'{I}#pragma unroll')
+        o.append(f'{I}for (int q_ = 1; q_ < {G}; ++q_) a_ = {FOLD_OP[op]}(a_, red_sh[p_ * {G} + q_]);')
+        o.append(f'{I}{self.store(name, [env[a][0] for a in axes], "a_", "float")}')
+        o.append(f'{ind}}}')
 
     # -- group
     def gen_group(self, lead, members, out, ind):
@@ -2153,6 +2357,18 @@ class Lowering:
         out.append(f'{ind}}}')
         self.note(reads, writes)
 
+    def writes_of(self, ss):
+        """Storage roots and residues the statements write."""
+        out = set()
+        for t in ss:
+            if t[0] in ('let', 'step'):
+                out.add(self.root(t[1]))
+            if t[0] == 'emit':
+                out.add(t[1])
+            if t[0] == 'step':
+                out |= self.writes_of(t[6])
+        return out
+
     # -- the layer loop
     def gen_step(self, s, out, ind):
         _, name, axes, var, init, carry, blk = s
@@ -2166,15 +2382,21 @@ class Lowering:
         n = self.static[var]
         lv = f'l_{var}'
         out.append(f'{ind}for (int {lv} = 0; {lv} < {self.ext_c(var)}; ++{lv}) {{  // fold step {var}')
+        out.append(f'{ind}  const int tid = vh_opaque(tid_k_), lane = tid & 63, wave = tid >> 6;')
         saved = self.step_env.get(var)
         self.step_env[var] = (lv, 'int')
         self.mult *= n
+        self.loops.append({'id': self.fresh('loop'), 'var': var, 'lv': lv, 'n': self.ext_c(var),
+                           'pf_before': self.last_pf, 'body_barrier': False, 'end_prefetch': [],
+                           'end_dirty': self.writes_of(blk)})
         body = [b for b in blk if b[0] != 'ret']
         ret = [b for b in blk if b[0] == 'ret'][0][1]
         self.gen(body, out, ind + '  ')
         if not (ret[0] == 'idx' and self.alias.get(ret[1]) == carry):
             self.gen_copy(carry, ret, axes, out, ind + '  ', f'{carry} <- ret')
-        self.barrier(out, ind + '  ', f'next {var}')
+        lp = self.loops[-1]
+        self.barrier(out, ind + '  ', f'next {var}', pre_wait=lp['end_prefetch'])
+        self.loops.pop()
         self.mult //= n
         out.append(f'{ind}}}')
         if saved is None:
@@ -2231,7 +2453,7 @@ class Lowering:
 
 
 def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None, timing=False,
-          kernel_name='vesta_step'):
+          kernel_name='vesta_step', grid=None):
     """Program text -> Lowered: HIP source of one persistent kernel.
 
     Kernel ABI: ``<kernel_name>(R_<residue>... in spec order, float* S,
@@ -2245,7 +2467,7 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
     the first launch and is left consistent by every launch.
     """
     stmts = batch_lift(parse(text), batch, set(per_token))
-    low = Lowering(stmts, res, axis_max, outputs, batch, timing)
+    low = Lowering(stmts, res, axis_max, outputs, batch, timing, grid)
     for o in outputs:
         if o not in low.axes_of:
             raise NameError(f'output {o} is not a value of the program')
@@ -2253,6 +2475,16 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
             raise LowerError(f'output {o} was placed in LDS')
     low.fb_targets = set(feedback or {})
     body = low.kernel(feedback)
+    # prefetch code goes where each barrier left room for it
+    filled = []
+    for line in body:
+        t = line.strip()
+        if t.startswith('/*@PF') and t.endswith('@*/'):
+            slot = low.pf_slots[int(t[5:-3])]
+            filled += [slot['ind'] + x for x in slot['lines']]
+        else:
+            filled.append(line)
+    body = filled
     written = set(low.emitted) | low.fb_targets
     params, args = [], []
     for name, (shape, dt) in low.res.items():
@@ -2261,7 +2493,7 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
         args.append(f'{"" if w else "const "}{CTYPE[dt]}* __restrict__ R_{name}')
     args += ['float* __restrict__ S', 'unsigned* __restrict__ bar', 'unsigned long long* __restrict__ TS',
              'const int nsteps', 'int* __restrict__ tok_out', 'const int* __restrict__ tok_in']
-    pre = []
+    pre = [f'  const vh_rsrc rb_S = mk_rsrc(S, {max(1, low.goff) * 4}u);']
     for name in sorted(written):
         shape, dt = low.res[name]
         if dt == 'f16':
@@ -2287,23 +2519,33 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
         head.append(f'    if (E_{a} > {low.static[a]} || E_{a} < 1) break;  // beyond its bound: stop')
     red = max(low.red_floats, 4)
     prelude = PRELUDE_PATH.read_text()
-    src = (prelude + '\n'
-           + f'extern "C" __global__ void __launch_bounds__({BLOCK}) {kernel_name}(' + ', '.join(args) + ') {\n'
-           + '  extern __shared__ float sh_f[];\n'
+    src = (f'#define VBLOCK {BLOCK}\n' + prelude + '\n'
+           + f'extern "C" __global__ void __launch_bounds__({BLOCK}, 1) {kernel_name}(' + ', '.join(args) + ') {\n'
+           + '  extern __shared__ __attribute__((aligned(16))) float sh_f[];  // 16-byte vector reads\n'
            + f'  __shared__ float red_sh[{red}];\n'
            + '  __shared__ int flag_sh;\n'
-           + '  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;\n'
+           + '  const int tid_k_ = threadIdx.x;\n'
+           + '  const int tid = tid_k_, lane = tid & 63, wave = tid >> 6;\n'
            + f'  const int gtid = blockIdx.x * {BLOCK} + tid;\n'
-           + f'  const int nthr = gridDim.x * {BLOCK};\n'
-           + '  const unsigned nblk = gridDim.x;\n'
-           + '  unsigned bgen_ = tid == 0 ? ldc_u(bar) : 0u;\n'
-           + ('  unsigned long long tlast_ = vh_clock();\n' if timing else '')
+           + f'  const int nthr = {low.grid} * {BLOCK};\n'
+           + f'  const unsigned nblk = {low.grid}u;  // the launch grid (checked at launch)\n'
+           + '  unsigned bk_ = 0u;  // grid barriers passed in this launch\n'
+           + ''.join(f'  {d}\n' for d in low.decls)
+           + (f'  __shared__ unsigned long long ts_sh[{max(1, len(low.sites))}];\n'
+              f'  for (int i_ = tid; i_ < {max(1, len(low.sites))}; i_ += {BLOCK}) ts_sh[i_] = 0ull;\n'
+              '  __syncthreads();\n'
+              '  unsigned long long tlast_ = vh_clock();\n' if timing else '')
            + '\n'.join(pre) + '\n'
            + '  for (int st_ = 0; st_ < nsteps; ++st_) {\n'
+           + '    const int tid = vh_opaque(tid_k_), lane = tid & 63, wave = tid >> 6;\n'
            + '\n'.join(head) + '\n'
            + '\n'.join(body) + '\n'
-           + '    if (st_ + 1 < nsteps) grid_sync(bar, nblk, bgen_);  // feedback visible to the next step\n'
-           + '  }\n}\n')
+           + '    if (st_ + 1 < nsteps) grid_sync(bar, nblk, bk_);  // feedback visible to the next step\n'
+           + '  }\n'
+           + ('  if (blockIdx.x == 0) { __syncthreads(); '
+              f'for (int i_ = tid; i_ < {len(low.sites)}; i_ += {BLOCK}) TS[i_] += ts_sh[i_]; }}\n'
+              if timing else '')
+           + '  grid_exit(bar, nblk);\n}\n')
     scratch = {}
     for n in low.axes_of:
         r = low.root(n)
@@ -2311,5 +2553,5 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
             axes = low.axes_of[n]
             scratch[n] = (low.g[r], axes, tuple(low.static[a] for a in axes))
     return Lowered(src, params, scratch, low.goff, (low.lds_floats + low.stage_floats) * 4, low.barriers,
-                   low.plan, low.sites, low.counters, BLOCK, GRID_MAX, {n: shp for n, (shp, _) in low.res.items()},
-                   kernel_name)
+                   low.plan, low.sites, low.counters, BLOCK, low.grid, {n: shp for n, (shp, _) in low.res.items()},
+                   kernel_name, 1, dict(low.packs))

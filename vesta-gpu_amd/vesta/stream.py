@@ -1,0 +1,502 @@
+"""Streamed contractions: one weight row per output point, read along the fold.
+
+A sum contraction ``y[.., p] = fold sum k: A[r, k] * W[.., k-or-p ..]`` whose
+weight is a read-only residue is lowered so that every output point reads
+one contiguous row of K weights:
+
+  * ``lane`` pattern (the fold indexes W's last axis, e.g. the LM head
+    ``wte[n, d]``): rows are W's own rows;
+  * ``tile`` pattern (the output axis indexes W's last axis, e.g.
+    ``qkvw[l, d, j]``): the kernel reads a copy of W transposed in its last
+    two axes (``<W>__t``), made once when the residues are bound, so column
+    ``j`` of W becomes a contiguous row.
+
+Points are split into equal contiguous ranges, one per block (no split-K, so
+no partial sums cross blocks); inside a block each wave takes ``64 / lpp``
+points at a time, ``lpp`` lanes per point, 16-byte loads along the fold and a
+butterfly reduction. The other factor is read from LDS (in place when it is a
+block-private value laid out [rows, fold], otherwise staged there first).
+
+When a block's share of the weights fits in a few registers, its loads are
+issued ahead of time: at the grid barrier before the site, between
+``grid_arrive`` and ``grid_wait`` (or, for the first site of a layer loop,
+at the end of the previous iteration), so the weights are in flight while
+the block waits for the values they multiply.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+PREFETCH_VGPRS = 64          # registers per lane one site may hold prefetched weights in
+PI_STREAM = 4                # slots whose loads are issued together when not prefetched
+
+
+@dataclass
+class Stream:
+    pack: str | None          # name of the transposed copy, or None (rows are W's own)
+    src: str                  # the residue read (W or its copy)
+    K: int                    # fold length (flattened fold axes)
+    c0: int                   # first fold element within a row
+    rowlen: int               # row length of the array read
+    prefix_idx: list          # index expressions of the leading axes, the point's own axis last (tile)
+    pts: list                 # point axes (row-major)
+    vec: int                  # elements per load
+
+
+class StreamMixin:
+    # ------------------------------------------------------------ eligibility
+    def stream_of(self, c):
+        """Stream description of contraction c, or None when it cannot stream."""
+        W = c.W
+        shape, dt = self.res[W]
+        if W in self.emitted or W in self.fb_targets or dt not in ('f16', 'f32'):
+            return None
+        if any(a in self.dynamic for a in c.fold_axes) or any(a in self.dynamic for a in c.pt_axes):
+            return None
+        K = math.prod(self.static[a] for a in c.fold_axes)
+        if c.kind == 'lane':
+            if len(c.fold_axes) != 1 or c.widx[-1] != ('name', c.fold_axes[0]):
+                return None
+            rowlen, c0, pack = shape[-1], 0, None
+            prefix = list(c.widx[:-1])
+            pts = list(c.pt_axes)
+        else:
+            if len(shape) < 2 or c.contig in self.dynamic:
+                return None
+            aff = self.affine(c.widx[-2])
+            if aff is None:
+                return None
+            const, coefs = aff
+            stride = 1
+            for a in reversed(c.fold_axes):
+                if coefs.get(a) != stride:
+                    return None
+                stride *= self.static[a]
+            if set(coefs) != set(c.fold_axes) or const < 0 or const + K > shape[-2]:
+                return None
+            for x in c.widx[:-2]:
+                if self.free_axes(x) & (set(c.fold_axes) | {c.contig}):
+                    return None
+            rowlen, c0 = shape[-2], const
+            pack = f'{W}__t'
+            prefix = list(c.widx[:-2]) + [('name', c.contig)]
+            pts = list(c.pt_axes) + [c.contig]
+        esz = 2 if dt == 'f16' else 4
+        vec = next(v for v in ((8, 4, 2, 1) if esz == 2 else (4, 2, 1))
+                   if K % v == 0 and rowlen % v == 0 and c0 % v == 0)
+        if pack is not None and pack not in self.res:
+            self.res[pack] = (tuple(shape[:-2]) + (shape[-1], shape[-2]), dt)
+            self.packs[pack] = W
+        return Stream(pack, pack or W, K, c0, rowlen, prefix, pts, vec)
+
+    # ------------------------------------------------------------ prefetch slots
+    def pf_open(self, out, ind, dirty=()):
+        """A place for prefetch code between grid_arrive and grid_wait.
+        ``dirty``: values written since the previous barrier (other blocks'
+        writes of them are not yet visible there)."""
+        k = len(self.pf_slots)
+        self.pf_slots.append({'lines': [], 'loop': self.loop_id(), 'ind': ind, 'dirty': set(dirty)})
+        out.append(f'/*@PF{k}@*/')
+        self.last_pf = k
+
+    def loop_id(self):
+        return self.loops[-1]['id'] if self.loops else None
+
+    def prefetch_target(self):
+        """Where code issued early for the next site goes: ('slot', k) for the
+        latest barrier of this loop body, ('loop', k) for the barrier before
+        the loop (plus the end of the previous iteration), or None (in place)."""
+        k = self.last_pf
+        if k is not None and self.pf_slots[k]['loop'] == self.loop_id():
+            return 'slot', k
+        lp = self.loops[-1] if self.loops else None
+        if lp is not None and k is not None and k == lp['pf_before'] and not lp['body_barrier']:
+            return 'loop', k
+        return None
+
+    def unsafe_early(self):
+        """Values that early loads must not read: written after the barrier
+        before the one the loads go to."""
+        tgt = self.prefetch_target()
+        bad = set(self.dirty)
+        if tgt is not None:
+            bad |= self.pf_slots[tgt[1]]['dirty']
+            if tgt[0] == 'loop':
+                bad |= self.loops[-1]['end_dirty']
+        return bad
+
+    def place_prefetch(self, make, out, ind):
+        """Put the prefetch code ``make(step_override)`` (a list of lines) at the
+        latest barrier of this loop body, or before the loop and at the end of
+        the previous iteration; with no barrier to use, in place."""
+        tgt = self.prefetch_target()
+        if tgt is None:
+            out += [ind + x for x in make(None)]
+            return
+        kind, k = tgt
+        if kind == 'slot':
+            self.pf_slots[k]['lines'] += make(None)
+            return
+        lp = self.loops[-1]
+        self.pf_slots[k]['lines'] += make(('0', 'int'))
+        lv, n = lp['lv'], lp['n']
+        nxt = make((f'({lv} + 1)', 'int'))
+        lp['end_prefetch'] += [f'if ({lv} + 1 < {n}) {{'] + ['  ' + x for x in nxt] + ['}']
+
+    # ------------------------------------------------------------ codegen
+    def gen_stream(self, s, c, st, fused, out, ind):
+        name = s[1]
+        reads, writes = self.site_io(s, c, fused)
+        self.sync(reads, writes, out, ind, name)
+        self.plan.append((self.show_stmt(s), 'stream' + (' (transposed copy)' if st.pack else '')
+                          + (f' +{len(fused)} fused' if fused else '')))
+        for _, t, _ in fused:
+            self.plan.append((self.show_stmt(t), f'epilogue of {name}'))
+        dt = self.res[st.src][1]
+        esz = 2 if dt == 'f16' else 4
+        vec, K = st.vec, st.K
+        nv = K // vec
+        lpp = 64
+        while lpp > 1 and (nv % lpp != 0 or nv < lpp):
+            lpp //= 2
+        if lpp < 8 and nv >= 64:
+            lpp = 64
+        pl = -(-nv // lpp)
+        exact = nv % lpp == 0
+        ppw = 64 // lpp
+        NW = self.NWAVE - 1          # compute waves; the last wave polls barriers and holds no early loads
+        P = self.size(st.pts)
+        NB = self.grid
+        PPB = -(-P // NB)
+        NQ = -(-PPB // (NW * ppw))
+        reg = c.reg_axes
+        R = self.size(reg)
+        rch = min(R, self.REG_MAX)
+        nrch = -(-R // rch)
+        ltype = self.load_type(dt, vec)
+        vregs = NQ * pl * max(1, vec * esz // 4)
+        prefetch = vregs <= PREFETCH_VGPRS
+        sid = self.fresh('s')
+        wq = f'wq_{sid}'
+        I = ind + '  '
+        o = out
+
+        def load_lines(q_c, dst, step_override):
+            """Lines loading slot q_c's vectors into dst[m] (m < pl)."""
+            lines = []
+            saved = None
+            if step_override is not None:
+                saved = dict(self.step_env)
+                for v in list(self.step_env):
+                    if self.loops and v == self.loops[-1]['var']:
+                        self.step_env[v] = step_override
+            p_c, ok_c = self.slot_point(dict(NW=NW, ppw=ppw, PPB=PPB), q_c)
+            lines.append(f'{{ const int p_ = {p_c};')
+            lines.append(f'  if ({ok_c} && p_ < {P}) {{')
+            env = self.decode('p_', st.pts, lines, '    ', prefix='sp_')
+            pre = []
+            ix = [self.index(x, env, pre, '    ') for x in st.prefix_idx]
+            lines += pre
+            rs = self.res_strides(st.src)
+            base = self.addr(ix, rs[:-1]) if ix else '0'
+            lines.append(f'    const unsigned wr_ = (unsigned)({base}) + {st.c0}u;')
+            lines.append('    #pragma unroll')
+            lines.append(f'    for (int m_ = 0; m_ < {pl}; ++m_) {{')
+            lines.append(f'      const int kv_ = cl_ + m_ * {lpp};')
+            cond = '' if exact else f'if (kv_ < {nv}) '
+            lines.append(f'      {cond}{dst}[m_] = {self.nt_load(dt, vec, self.rsrc(st.src), "wr_ + kv_ * %d" % vec)};')
+            if not exact:
+                lines.append(f'      else {dst}[m_] = {self.vec_zero(dt, vec)};')
+            lines.append('    }')
+            lines.append('  } else {')
+            lines.append('    #pragma unroll')
+            lines.append(f'    for (int m_ = 0; m_ < {pl}; ++m_) {dst}[m_] = {self.vec_zero(dt, vec)};')
+            lines.append('  }')
+            lines.append('}')
+            if saved is not None:
+                self.step_env.clear()
+                self.step_env.update(saved)
+            return lines
+
+        lane_decl = [f'const int sub_ = lane / {lpp}, cl_ = lane % {lpp};']
+        rows_of = [min(rch, R - rc * rch) for rc in range(nrch)]
+        geo = dict(P=P, PPB=PPB, NW=NW, ppw=ppw, lpp=lpp, rch=rch, reg=reg)
+        self.geo_nw = NW
+        if prefetch:
+            self.decls.append(f'{ltype} {wq}[{NQ}][{pl}];')
+            unsafe = self.unsafe_early()
+            caps = {}
+
+            def make(step_override):
+                """Weights of every slot, and the loads of the epilogues that may
+                be issued early, into registers."""
+                lines = [f'if (wave < {NW}) {{'] + ['  ' + x for x in lane_decl]
+                for q in range(NQ):
+                    lines += ['  ' + x for x in load_lines(str(q), f'{wq}[{q}]', step_override)]
+                saved = self.override_step(step_override)
+                for rc in range(nrch):
+                    for q in range(NQ):
+                        for j in range(-(-rows_of[rc] // lpp)):
+                            pre = f'pf_{sid}_{q}_{rc}_{j}_'
+                            loads = self.epi_loads(s, c, st, fused, geo, str(q), rc, j, rows_of[rc], pre, unsafe)
+                            caps[pre] = [(n, k) for n, _, k in loads]
+                            if loads:
+                                lines += ['  ' + x for x in self.epi_context(st, geo, str(q), rc, j, rows_of[rc],
+                                                                               [f'{n} = {t};' for n, t, _ in loads])]
+                self.restore_step(saved)
+                return lines + ['}']
+            self.place_prefetch(make, o, ind)
+            for pre, regs in caps.items():
+                for n, k in regs:
+                    self.decls.append(f'{self.cap_ctype(k)} {n};')
+        o.append(f'{ind}{{  // stream {name}: {P} points x {K} from {st.src}, VEC={vec} lanes/point={lpp} '
+                 f'points/block={PPB} rows={R}{" prefetched" if prefetch else ""}')
+        for x in lane_decl:
+            o.append(f'{I}{x}')
+        # the other factor, as floats in LDS laid out [row, fold]
+        direct = self.direct_lds(c, reg)
+        for rc in range(nrch):
+            if direct is not None:
+                abase = f'{direct} + {rc * rch * K}'
+            else:
+                abase = str(self.lds_floats + self.stage_top)
+                self.stage_floats = max(self.stage_floats, self.stage_top + rch * K)
+                self.stage_A(c, reg, rc, rch, R, K, abase, o, I)
+                self.mark(o, I, f'stream {name}: stage')
+            qs = [str(q) for q in range(NQ)] if prefetch else None
+            self.stream_body(s, c, st, fused, o, I, rc, rch, R, K, abase, dt, vec, nv, lpp, pl, exact,
+                             NQ, qs, wq, ltype, geo, load_lines, sid, unsafe if prefetch else None)
+        o.append(f'{ind}}}')
+        self.note(reads, writes)
+        self.mark(out, ind, f'stream {name}')
+
+    def override_step(self, step_override):
+        saved = dict(self.step_env)
+        if step_override is not None and self.loops:
+            self.step_env[self.loops[-1]['var']] = step_override
+        return saved
+
+    def restore_step(self, saved):
+        self.step_env.clear()
+        self.step_env.update(saved)
+
+    @staticmethod
+    def slot_point(geo, q):
+        NW, ppw, PPB = geo['NW'], geo['ppw'], geo['PPB']
+        return (f'((int)blockIdx.x * {PPB} + ({q} * {NW} + wave) * {ppw} + sub_)',
+                f'(wave < {NW} && ({q} * {NW} + wave) * {ppw} + sub_ < {PPB})')
+
+    def epi_context(self, st, geo, q_c, rc, j, rows, body):
+        """Lines binding the point of slot q_c and the row of lane group member
+        j around ``body`` (lines that may use them)."""
+        p_c, ok_c = self.slot_point(geo, q_c)
+        lines = [f'{{ const int p_ = {p_c};', f'  if ({ok_c} && p_ < {geo["P"]}) {{']
+        self.decode('p_', st.pts, lines, '    ', prefix='ep_')
+        lines.append(f'    const int r_ = cl_ + {j * geo["lpp"]};')
+        lines.append(f'    if (r_ < {rows}) {{')
+        if geo['reg']:
+            self.decode(f'({rc * geo["rch"]} + r_)', geo['reg'], lines, '      ', prefix='er_')
+        lines += ['      ' + x for x in body]
+        lines += ['    }', '  }', '}']
+        return lines
+
+    def epi_env(self, st, geo, rc):
+        env = {a: (f'ep_{a}', 'int') for a in st.pts}
+        for a in geo['reg']:
+            env[a] = (f'er_{a}', 'int')
+        return env
+
+    def epi_loads(self, s, c, st, fused, geo, q_c, rc, j, rows, prefix, unsafe):
+        """The loads the epilogue of (slot, row chunk, lane group member j)
+        would issue that may go early: (register, load expression, kind)."""
+        self.capture = {'prefix': prefix, 'loads': [], 'unsafe': unsafe}
+        try:
+            self.epilogue(s, c, fused, self.epi_env(st, geo, rc), '0.0f', [], '')
+            return self.capture['loads']
+        finally:
+            self.capture = None
+
+    def stream_body(self, s, c, st, fused, o, I, rc, rch, R, K, abase, dt, vec, nv, lpp, pl, exact,
+                    NQ, qs, wq, ltype, geo, load_lines, sid, unsafe):
+        """The dot products of one row chunk, then the epilogues. ``qs``: the
+        slots as compile-time constants when the weights were prefetched (the
+        epilogue then reads early-issued registers), else None (slots are
+        streamed PI_STREAM at a time)."""
+        rows = min(rch, R - rc * rch)
+        rpl = -(-rows // lpp)
+        J2 = I + '  '
+        if qs is None:
+            PI = PI_STREAM
+            o.append(f'{I}for (int q0_ = 0; q0_ < {NQ}; q0_ += {PI}) {{')
+            o.append(f'{J2}{ltype} wl_[{PI}][{pl}];')
+            for qi in range(PI):
+                o.append(f'{J2}if (q0_ + {qi} < {NQ}) {{')
+                o += [J2 + '  ' + x for x in load_lines(f'(q0_ + {qi})', f'wl_[{qi}]', None)]
+                o.append(f'{J2}}}')
+            o.append(f'{J2}#pragma unroll')
+            o.append(f'{J2}for (int qi_ = 0; qi_ < {PI}; ++qi_) {{')
+            K3 = J2 + '  '
+            o.append(f'{K3}const int q_ = q0_ + qi_;')
+            o.append(f'{K3}if (q_ >= {NQ}) break;')
+            self.slot_dot(o, K3, 'q_', 'wl_[qi_]', dt, vec, nv, lpp, pl, exact, rch, K, abase, geo)
+            self.slot_epilogue(s, c, st, fused, o, K3, 'q_', rc, rows, rpl, geo, None)
+            o.append(f'{J2}}}')
+            o.append(f'{I}}}')
+            return
+        for q in qs:
+            o.append(f'{I}{{  // slot {q}')
+            self.slot_dot(o, J2, q, f'{wq}[{q}]', dt, vec, nv, lpp, pl, exact, rch, K, abase, geo)
+            self.mark(o, J2, f'stream {s[1]}: dot')
+            self.slot_epilogue(s, c, st, fused, o, J2, q, rc, rows, rpl, geo,
+                               (lambda j, q=q: f'pf_{sid}_{q}_{rc}_{j}_', unsafe))
+            o.append(f'{I}}}')
+
+    def slot_dot(self, o, K3, q_c, wsrc, dt, vec, nv, lpp, pl, exact, rch, K, abase, geo):
+        p_c, ok_c = self.slot_point(geo, q_c)
+        o.append(f'{K3}const int p_ = {p_c};')
+        o.append(f'{K3}const bool ok_ = {ok_c} && p_ < {geo["P"]};')
+        o.append(f'{K3}float acc_[{rch}];')
+        o.append(f'{K3}#pragma unroll')
+        o.append(f'{K3}for (int r_ = 0; r_ < {rch}; ++r_) acc_[r_] = 0.0f;')
+        self.mark(o, K3, 'stream dot start')
+        o.append(f'{K3}#pragma unroll')
+        o.append(f'{K3}for (int m_ = 0; m_ < {pl}; ++m_) {{')
+        K4 = K3 + '  '
+        o.append(f'{K4}const int kv_ = cl_ + m_ * {lpp};')
+        if not exact:
+            o.append(f'{K4}if (kv_ >= {nv}) break;')
+        o.append(f'{K4}float wf_[{vec}];')
+        o.append(f'{K4}{self.vec_unpack(dt, vec, wsrc + "[m_]", "wf_")}')
+        o.append(f'{K4}#pragma unroll')
+        o.append(f'{K4}for (int r_ = 0; r_ < {rch}; ++r_) {{')
+        o.append(f'{K4}  const float* ar_ = sh_f + {abase} + r_ * {K} + kv_ * {vec};')
+        o.append(f'{K4}  float av_[{vec}];')
+        o.append(f'{K4}  {self.lds_vec_load(vec, "ar_", "av_")}')
+        o.append(f'{K4}  #pragma unroll')
+        o.append(f'{K4}  for (int v_ = 0; v_ < {vec}; ++v_) acc_[r_] = fmaf(av_[v_], wf_[v_], acc_[r_]);')
+        o.append(f'{K4}}}')
+        o.append(f'{K3}}}')
+        if lpp > 1:
+            o.append(f'{K3}#pragma unroll')
+            o.append(f'{K3}for (int r_ = 0; r_ < {rch}; ++r_) acc_[r_] = group_red_sum(acc_[r_], {lpp});')
+
+    def slot_epilogue(self, s, c, st, fused, o, K3, q_c, rc, rows, rpl, geo, early):
+        """After the butterfly every lane of a point group holds all rows'
+        sums; lane r of the group finishes row r (rows past the group width go
+        round again). ``early``: (register prefix of member j, unsafe set) when
+        the epilogue's early loads were issued at the barrier."""
+        o.append(f'{K3}if (ok_) {{')
+        K5 = K3 + '  '
+        self.decode('p_', st.pts, o, K5, prefix='ep_')
+        for j in range(rpl):
+            o.append(f'{K5}{{')
+            K6 = K5 + '  '
+            o.append(f'{K6}const int r_ = cl_ + {j * geo["lpp"]};')
+            o.append(f'{K6}if (r_ < {rows}) {{')
+            K7 = K6 + '  '
+            if rows == 1:
+                val = 'acc_[0]'
+            else:
+                o.append(f'{K7}float av_ = acc_[0];')
+                for r in range(1, rows):
+                    o.append(f'{K7}av_ = r_ == {r} ? acc_[{r}] : av_;')
+                val = 'av_'
+            lines = []
+            if geo['reg']:
+                self.decode(f'({rc * geo["rch"]} + r_)', geo['reg'], lines, K7, prefix='er_')
+            if early is not None:
+                self.capture = {'prefix': early[0](j), 'loads': [], 'unsafe': early[1]}
+            try:
+                self.epilogue(s, c, fused, self.epi_env(st, geo, rc), val, lines, K7)
+            finally:
+                self.capture = None
+            o += lines
+            o.append(f'{K6}}}')
+            o.append(f'{K5}}}')
+        o.append(f'{K3}}}')
+
+    # ------------------------------------------------------------ the other factor
+    def direct_lds(self, c, reg):
+        """LDS offset of the other factor when it is a private value laid out
+        [reg axes, fold axes] and read at exactly those axes; else None."""
+        A = c.A
+        if A[0] != 'idx' or A[1] not in self.axes_of:
+            return None
+        r = self.root(A[1])
+        if r not in self.private:
+            return None
+        want = list(reg) + list(c.fold_axes)
+        if list(self.axes_of[r]) != want or list(A[2]) != [('name', a) for a in want]:
+            return None
+        return str(self.lds[r])
+
+    def stage_A(self, c, reg, rc, rch, R, K, abase, o, I):
+        """The other factor at every (row, fold point) of this row chunk into
+        LDS [row, fold] (rows past R are zero). A value of global scratch laid
+        out [reg axes, fold axes] is copied with 16-byte coherent loads;
+        anything else is evaluated point by point, all loads of a thread issued
+        before its LDS stores."""
+        A = c.A
+        o.append(f'{I}__syncthreads();')
+        want = list(reg) + list(c.fold_axes)
+        if (A[0] == 'idx' and A[1] in self.axes_of and self.root(A[1]) in self.g
+                and self.root(A[1]) not in self.private and list(self.axes_of[self.root(A[1])]) == want
+                and list(A[2]) == [('name', a) for a in want] and K % 4 == 0):
+            rows = min(rch, R - rc * rch)
+            off = self.g[self.root(A[1])] + rc * rch * K
+            o.append(f'{I}stage_ldc4(sh_f + {abase}, rb_S, {off}, {rows * K});  // stage {A[1]}')
+            if rows < rch:
+                o.append(f'{I}for (int e_ = tid; e_ < {(rch - rows) * K}; e_ += {self.BLOCK}) '
+                         f'sh_f[{abase} + {rows * K} + e_] = 0.0f;')
+            o.append(f'{I}__syncthreads();')
+            return
+        T = -(-(rch * K) // self.BLOCK)
+        o.append(f'{I}#pragma unroll' + ('' if T <= 16 else ' 8'))
+        o.append(f'{I}for (int it_ = 0; it_ < {T}; ++it_) {{')
+        J2 = I + '  '
+        o.append(f'{J2}const int e_ = tid + it_ * {self.BLOCK};')
+        o.append(f'{J2}if (e_ < {rch * K}) {{')
+        J3 = J2 + '  '
+        o.append(f'{J3}const int ar_ = e_ / {K}, ak_ = e_ % {K};')
+        env = self.decode('ak_', c.fold_axes, o, J3, prefix='fa_')
+        o.append(f'{J3}float v_ = 0.0f;')
+        o.append(f'{J3}if ({rc * rch} + ar_ < {R}) {{')
+        if reg:
+            env.update(self.decode(f'({rc * rch} + ar_)', reg, o, J3 + '  ', prefix='ra_'))
+        pre = []
+        v, t = self.expr(c.A, env, pre, J3 + '  ')
+        o += pre
+        o.append(f'{J3}  v_ = {self.as_float(v, t)};')
+        o.append(f'{J3}}}')
+        o.append(f'{J3}sh_f[{abase} + e_] = v_;')
+        o.append(f'{J2}}}')
+        o.append(f'{I}}}')
+        o.append(f'{I}__syncthreads();')
+
+    # ------------------------------------------------------------ small helpers
+    def load_type(self, dt, vec):
+        if dt == 'f16':
+            return {8: 'vh_u32x4', 4: 'vh_u32x2', 2: 'unsigned', 1: 'vh_half'}[vec]
+        return {4: 'vh_f32x4', 2: 'vh_f32x2', 1: 'float'}[vec]
+
+    def nt_load(self, dt, vec, rr, idx):
+        """Streamed load of ``vec`` elements at element index ``idx`` through descriptor ``rr``."""
+        if dt == 'f16':
+            return {8: f'ldg16_nt({rr}, {idx})', 4: f'ldg8_nt({rr}, {idx})', 2: f'ldg4_nt({rr}, {idx})',
+                    1: f'(vh_half)(ldg4_nt({rr}, {idx}) & 0xffffu)'}[vec]
+        return {4: f'__builtin_bit_cast(vh_f32x4, ldg16_nt({rr}, 2u * ({idx})))',
+                2: f'__builtin_bit_cast(vh_f32x2, ldg8_nt({rr}, 2u * ({idx})))',
+                1: f'ldg_f({rr}, {idx})'}[vec]
+
+    def lds_vec_load(self, vec, ptr, dst):
+        if vec == 8:
+            return (f'{{ const vh_f32x4 x0_ = *(const vh_f32x4*)({ptr}), x1_ = *(const vh_f32x4*)({ptr} + 4); '
+                    f'{dst}[0] = x0_.x; {dst}[1] = x0_.y; {dst}[2] = x0_.z; {dst}[3] = x0_.w; '
+                    f'{dst}[4] = x1_.x; {dst}[5] = x1_.y; {dst}[6] = x1_.z; {dst}[7] = x1_.w; }}')
+        if vec == 4:
+            return (f'{{ const vh_f32x4 x0_ = *(const vh_f32x4*)({ptr}); '
+                    f'{dst}[0] = x0_.x; {dst}[1] = x0_.y; {dst}[2] = x0_.z; {dst}[3] = x0_.w; }}')
+        if vec == 2:
+            return f'{{ const vh_f32x2 x0_ = *(const vh_f32x2*)({ptr}); {dst}[0] = x0_.x; {dst}[1] = x0_.y; }}'
+        return f'{dst}[0] = {ptr}[0];'
