@@ -66,23 +66,24 @@ def test_gpt2_small_b1_plan():
         assert p[name].startswith('stream (transposed copy)'), (name, p[name])
     assert low.packs == {'qkvw__t': 'qkvw', 'ow__t': 'ow', 'fcw__t': 'fcw', 'pw__t': 'pw'}
     # attention: scores, softmax statistics and weighted values in one block per (bt, h)
-    assert p['sc'] == 'group[bt, h] lane (LDS)' and p['o'] == 'group[bt, h] tile'
-    assert p['mx'] == p['_h1'] == 'group[bt, h] (LDS)'
+    assert p['sc'] == p['mx'] == p['_h1'] == p['o'] == 'attention[bt, h]'
     assert p['logit'] == 'stream'
-    assert p['best'] == 'gridred argmax' and p['next'] == 'gridred argmax'
+    # argmax over each block's own logits, combined by every block; embedding in every block
+    assert p['best'] == 'argmax (own points)' and p['next'] == 'argmax'
+    assert p['z0'] == 'replicated'
     assert p['m1'] == p['v1'] == p['a'] == 'private'
     assert p['residue keys'] == 'epilogue of qkv' and p['residue vals'] == 'epilogue of qkv'
     assert p['g'] == 'epilogue of u' and p['z1'] == 'epilogue of oo'
     # softmax denominator hoisted, q / ex / w inlined
     assert '_h1' in p and 'q' not in p and 'w' not in p and 'ex' not in p
-    assert low.barriers_per_launch <= 63
+    assert low.barriers_per_launch == 5 * 12 + 1
     assert set(low.scratch) >= {'logit', 'next'} and low.scratch['logit'][2] == (1, 50257)
 
 
 def test_gpt2_small_b8_plan():
     low = lower_gpt2(8)
     p = placements(low)
-    assert p['mx'].startswith('group') and p['_h1'].startswith('group') and p['o'].startswith('group')
+    assert p['mx'] == p['_h1'] == p['o'] == 'attention[bt, h]'
     assert p['qkv'].startswith('stream') and p['logit'] == 'stream'
     assert low.barriers_per_launch <= 75
     assert low.scratch['logit'][2] == (8, 50257) and low.scratch['next'][2] == (8,)

@@ -1,0 +1,310 @@
+"""Attention groups: scores, softmax statistics and weighted values of one
+leading point (a batch row and head) in one block, K/V rows in registers.
+
+The pattern (what ``gpt2.vst`` Q5-Q7 lower to after hoisting and inlining):
+
+    sc[L.., s] = EPI1(fold sum e: A1[L.., e] * K[.., s, .., e])     lane contraction over a cache
+    mx[L..]    = fold max s: sc[L.., s]
+    hs[L..]    = fold sum s: F(sc[L.., s], mx[L..])
+    o[L.., e]  = EPI4(fold sum s: A4(sc, mx, hs)[L.., s] * V[.., s, .., e])
+
+with ``s`` the dynamic context axis and K, V residues the step emits into.
+Each compute wave lane owns one (position, 8-element chunk of e) pair per
+slot, the same pair for K and for V, so a lane's K and V loads are 16 bytes
+each and a position's score is a butterfly over its lanes. Rows of the
+cache written by earlier steps are loaded at the barrier before the group
+(between grid_arrive and grid_wait) into registers; only the row the step
+itself emits, and the query, are read after the wait. The statistics are
+block reductions; the weighted values are reduced over positions inside a
+wave and then across waves through LDS.
+
+Numerics follow the program statement by statement: the score epilogue,
+``F`` and ``A4`` are evaluated per position exactly as written (so the
+weight is ``exp(sc - mx) / hs`` per position, as in the program); only the
+order of the sums over ``s`` and ``e`` differs from a sequential sum.
+"""
+from __future__ import annotations
+
+import math
+
+from .stream import PREFETCH_VGPRS
+
+ATTN_PREFETCH_SLOTS = 8      # cache rows per lane issued early (K and V each)
+
+
+class AttnMixin:
+    def attn_of(self, lead, members):
+        """Pattern description of an attention group, or None."""
+        if len(members) != 4:
+            return None
+        t1, t2, t3, t4 = members
+        local = set(self.group_local.get(id(t1), []))
+        if local != {t1[1], t2[1], t3[1]}:
+            return None
+        c1, c4 = self.contraction(t1), self.contraction(t4)
+        if c1 is None or c4 is None or c1.kind != 'lane' or c4.kind != 'tile':
+            return None
+        if c1.W not in self.emitted or c4.W not in self.emitted or c1.reg_axes or c4.reg_axes:
+            return None
+        if self.res[c1.W][1] != 'f16' or self.res[c4.W][1] != 'f16':
+            return None
+        plen = len(lead)
+        if list(t1[2][:plen]) != list(lead) or len(t1[2]) != plen + 1:
+            return None
+        S = t1[2][-1]
+        if S not in self.dynamic or len(c1.fold_axes) != 1:
+            return None
+        E1 = c1.fold_axes[0]
+        same = [('name', a) for a in list(lead) + [S]]
+        at_lead = [('name', a) for a in lead]
+        e2 = t2[3]
+        if list(t2[2]) != list(lead) or e2 != ('fold', 'max', S, ('idx', t1[1], same)):
+            return None
+        e3 = t3[3]
+        if list(t3[2]) != list(lead) or e3[0] != 'fold' or e3[1] != 'sum' or e3[2] != S:
+            return None
+        if not self._reads_at(e3[3], {t1[1]: same, t2[1]: at_lead}):
+            return None
+        if list(t4[2]) != list(lead) + [c4.contig] or c4.fold_axes != [S]:
+            return None
+        if not self._reads_at(c4.A, {t1[1]: same, t2[1]: at_lead, t3[1]: at_lead}):
+            return None
+        E4 = c4.contig
+        nE1, nE4 = self.static[E1], self.static[E4]
+        if nE1 % 8 or nE4 % 8 or 64 % (nE1 // 8) or 64 % (nE4 // 8) or nE1 != nE4:
+            return None
+        # both caches read as W[.., s, .., e] with e their last axis; the step's own row
+        # is the one its emits write
+        rows = []
+        for W in (c1.W, c4.W):
+            emits = [x for x in self.emit_stmts if x[1] == W]
+            if len(emits) != 1:
+                return None
+            widx = c1.widx if W == c1.W else c4.widx
+            pos = [i for i, x in enumerate(widx) if x == ('name', S)]
+            if len(pos) != 1:
+                return None
+            erow = emits[0][2][pos[0]]
+            if self.free_axes(erow) - set(lead) - self.steps:
+                return None
+            rows.append(erow)
+        if rows[0] != rows[1]:
+            return None
+        return dict(t=members, c1=c1, c4=c4, S=S, E=E1, E4=E4, nE=nE1, erow=rows[0], lead=list(lead))
+
+    def _reads_at(self, e, allowed):
+        """Does e read group values only at the given index lists (and no folds)?"""
+        for n in self.nodes_of(e):
+            if n[0] == 'fold':
+                return False
+            if n[0] == 'idx' and n[1] in allowed and list(n[2]) != allowed[n[1]]:
+                return False
+            if n[0] == 'name' and n[1] in allowed:
+                return False
+        return True
+
+    # ------------------------------------------------------------ codegen
+    def gen_attn(self, at, out, ind):
+        t1, t2, t3, t4 = at['t']
+        c1, c4, S, lead = at['c1'], at['c4'], at['S'], at['lead']
+        names = {t[1] for t in at['t']}
+        local = self.group_local.get(id(t1), [])
+        reads = self.root_reads([t[3] for t in at['t']], exclude=names)
+        writes = {self.root(t[1]) for t in at['t'] if t[1] not in local}
+        self.sync(reads, writes, out, ind, t1[1])
+        for t in at['t']:
+            self.plan.append((self.show_stmt(t), f'attention[{", ".join(lead)}]'))
+        nE = at['nE']
+        LPE = nE // 8                      # lanes per position (16-byte chunks of e)
+        PPW = 64 // LPE                    # positions per wave per slot
+        NW = self.NWAVE - 1                # compute waves (the last wave polls barriers)
+        PPP = NW * PPW                     # positions per block per slot
+        smax = self.static[S]
+        NPS = -(-smax // PPP)
+        NPF = min(NPS, ATTN_PREFETCH_SLOTS, PREFETCH_VGPRS // 8)
+        G = self.size(lead)
+        sid = self.fresh('a')
+        kq, vq = f'kq_{sid}', f'vq_{sid}'
+        T = self.ext_c(S)
+        rbK, rbV = f'rb_{c1.W}', f'rb_{c4.W}'
+        self.red_floats = max(getattr(self, 'red_floats', 4), 2 * self.NWAVE)
+        red_o = self.lds_floats + self.stage_top
+        self.stage_floats = max(self.stage_floats, self.stage_top + NW * nE)
+
+        def row_index(W, c, env):
+            """Element index of (s, e-chunk start) in cache W: lines, expression."""
+            lines = []
+            ix = [self.index(x, env, lines, '') for x in c.widx]
+            return lines, self.addr(ix, self.res_strides(W))
+
+        def slot_env(k, lead_env):
+            env = dict(lead_env)
+            env[S] = (f's{k}_', 'int')
+            return env
+
+        def erow_c(lead_env):
+            lines = []
+            v = self.index(at['erow'], lead_env, lines, '')
+            return lines, v
+
+        def load_kv(k, lead_env, early):
+            """Lines loading K and V of slot k into kq[k], vq[k] (zeros where the
+            position is out of range; early: only rows other than the step's own)."""
+            lines = [f'{{ const int s{k}_ = {k * PPP} + wave * {PPW} + sub_;']
+            el, ev = erow_c(lead_env)
+            lines += el
+            cond = f'wave < {NW} && s{k}_ < {T}' + (f' && s{k}_ != ({ev})' if early else '')
+            env = slot_env(k, lead_env)
+            env[at['E']] = ('(cl_ * 8)', 'int')
+            l1, a1 = row_index(c1.W, c1, env)
+            env4 = slot_env(k, lead_env)
+            env4[at['E4']] = ('(cl_ * 8)', 'int')
+            l4, a4 = row_index(c4.W, c4, env4)
+            lines.append(f'  if ({cond}) {{')
+            lines += ['    ' + x for x in l1 + l4]
+            lines.append(f'    {kq}[{k}] = ldc16_h({rbK}, {a1});')
+            lines.append(f'    {vq}[{k}] = ldc16_h({rbV}, {a4});')
+            lines.append('  }' + ('' if early else ' else { ' + f'{kq}[{k}] = vh_u32x4{{0u, 0u, 0u, 0u}}; '
+                                                     f'{vq}[{k}] = vh_u32x4{{0u, 0u, 0u, 0u}}; }}'))
+            lines.append('}')
+            return lines
+
+        lane_decl = f'const int sub_ = lane / {LPE}, cl_ = lane % {LPE};'
+        self.decls.append(f'vh_u32x4 {kq}[{NPS}];')
+        self.decls.append(f'vh_u32x4 {vq}[{NPS}];')
+
+        def lead_lines(gp):
+            lines = []
+            env = self.decode(gp, lead, lines, '', prefix='al_')
+            return lines, env
+
+        def make(step_override):
+            saved = self.override_step(step_override)
+            try:
+                ll, lenv = lead_lines('(int)blockIdx.x')
+                lines = [f'if ((int)blockIdx.x < {G}) {{', '  ' + lane_decl] + ['  ' + x for x in ll]
+                for k in range(NPF):
+                    lines += ['  ' + x for x in load_kv(k, lenv, True)]
+                return lines + ['}']
+            finally:
+                self.restore_step(saved)
+        self.place_prefetch(make, out, ind)
+
+        o = out
+        I = ind + '  '
+        o.append(f'{ind}for (int gp_ = blockIdx.x; gp_ < {G}; gp_ += nblk) {{  // attention {t1[1]}..{t4[1]}: '
+                 f'{LPE} lanes/position, {PPP} positions/slot, {NPS} slots, {NPF} loaded early')
+        o.append(f'{I}{lane_decl}')
+        ll, lenv = lead_lines('gp_')
+        o += [I + x for x in ll]
+        o.append(f'{I}const bool first_ = gp_ == (int)blockIdx.x;')
+        # the step's own row (and every row when this is not the block's first point)
+        el, ev = erow_c(lenv)
+        o += [I + x for x in el]
+        for k in range(NPS):
+            o.append(f'{I}{{ const int s{k}_ = {k * PPP} + wave * {PPW} + sub_;')
+            if k < NPF:
+                o.append(f'{I}  if (!first_ || s{k}_ == ({ev}) || s{k}_ >= {T}) {{')
+            else:
+                o.append(f'{I}  {{')
+            o += [I + '    ' + x for x in load_kv(k, lenv, False)]
+            o.append(f'{I}  }}')
+            o.append(f'{I}}}')
+        self.mark(o, I, 'attention: rows')
+        # the query chunk of this lane
+        o.append(f'{I}float qv_[8];')
+        o.append(f'{I}#pragma unroll')
+        o.append(f'{I}for (int v_ = 0; v_ < 8; ++v_) {{')
+        qenv = dict(lenv)
+        qenv[at['E']] = ('(cl_ * 8 + v_)', 'int')
+        pre = []
+        qv, qt = self.expr(c1.A, qenv, pre, I + '  ')
+        o += pre
+        o.append(f'{I}  qv_[v_] = {self.as_float(qv, qt)};')
+        o.append(f'{I}}}')
+        # scores
+        o.append(f'{I}float sk_[{NPS}];')
+        o.append(f'{I}float mloc_ = -INFINITY;')
+        for k in range(NPS):
+            o.append(f'{I}{{ const int s{k}_ = {k * PPP} + wave * {PPW} + sub_;')
+            o.append(f'{I}  float wf_[8];')
+            o.append(f'{I}  unpack8({kq}[{k}], wf_);')
+            o.append(f'{I}  float d_ = 0.0f;')
+            o.append(f'{I}  #pragma unroll')
+            o.append(f'{I}  for (int v_ = 0; v_ < 8; ++v_) d_ = fmaf(qv_[v_], wf_[v_], d_);')
+            o.append(f'{I}  d_ = group_red_sum(d_, {LPE});')
+            venv = dict(slot_env(k, lenv))
+            venv['__acc'] = ('d_', 'float')
+            pre = []
+            sv, st_ = self.expr(c1.epi, venv, pre, I + '  ')
+            o += pre
+            o.append(f'{I}  sk_[{k}] = (wave < {NW} && s{k}_ < {T}) ? {self.as_float(sv, st_)} : -INFINITY;')
+            o.append(f'{I}  mloc_ = fmaxf(mloc_, sk_[{k}]);')
+            o.append(f'{I}}}')
+        self.mark(o, I, 'attention: scores')
+        o.append(f'{I}const float mx_ = block_red_max(mloc_, red_sh);')
+        self.mark(o, I, 'attention: max')
+        # the softmax denominator: each position once (its lane group's first lane)
+        o.append(f'{I}float hloc_ = 0.0f;')
+        for k in range(NPS):
+            o.append(f'{I}{{ const int s{k}_ = {k * PPP} + wave * {PPW} + sub_;')
+            fe, fx = self._subst(t3[3][3], {t1[1]: f'sk_[{k}]', t2[1]: 'mx_'})
+            pre = []
+            fv, ft = self.expr(fe, {**slot_env(k, lenv), **fx}, pre, I + '  ')
+            o += pre
+            o.append(f'{I}  if (cl_ == 0 && wave < {NW} && s{k}_ < {T}) hloc_ += {self.as_float(fv, ft)};')
+            o.append(f'{I}}}')
+        o.append(f'{I}const float hs_ = block_red_sum(hloc_, red_sh);')
+        self.mark(o, I, 'attention: sum')
+        # weighted values
+        o.append(f'{I}float ov_[8];')
+        o.append(f'{I}#pragma unroll')
+        o.append(f'{I}for (int v_ = 0; v_ < 8; ++v_) ov_[v_] = 0.0f;')
+        for k in range(NPS):
+            o.append(f'{I}{{ const int s{k}_ = {k * PPP} + wave * {PPW} + sub_;')
+            o.append(f'{I}  if (wave < {NW} && s{k}_ < {T}) {{')
+            ae, ax = self._subst(c4.A, {t1[1]: f'sk_[{k}]', t2[1]: 'mx_', t3[1]: 'hs_'})
+            pre = []
+            av, aty = self.expr(ae, {**slot_env(k, lenv), **ax}, pre, I + '    ')
+            o += pre
+            o.append(f'{I}    const float w_ = {self.as_float(av, aty)};')
+            o.append(f'{I}    float wf_[8];')
+            o.append(f'{I}    unpack8({vq}[{k}], wf_);')
+            o.append(f'{I}    #pragma unroll')
+            o.append(f'{I}    for (int v_ = 0; v_ < 8; ++v_) ov_[v_] = fmaf(w_, wf_[v_], ov_[v_]);')
+            o.append(f'{I}  }}')
+            o.append(f'{I}}}')
+        self.mark(o, I, 'attention: pv')
+        if PPW > 1:
+            o.append(f'{I}#pragma unroll')
+            o.append(f'{I}for (int v_ = 0; v_ < 8; ++v_) ov_[v_] = wave_red_sum_hi(ov_[v_], {LPE});')
+        o.append(f'{I}if (wave < {NW} && sub_ == 0) {{')
+        o.append(f'{I}  #pragma unroll')
+        o.append(f'{I}  for (int v_ = 0; v_ < 8; ++v_) sh_f[{red_o} + wave * {nE} + cl_ * 8 + v_] = ov_[v_];')
+        o.append(f'{I}}}')
+        o.append(f'{I}vh_lds_sync();')
+        o.append(f'{I}if (tid < {nE}) {{')
+        o.append(f'{I}  float a_ = sh_f[{red_o} + tid];')
+        o.append(f'{I}  #pragma unroll')
+        o.append(f'{I}  for (int w_ = 1; w_ < {NW}; ++w_) a_ += sh_f[{red_o} + w_ * {nE} + tid];')
+        fenv = dict(lenv)
+        fenv[at['E4']] = ('tid', 'int')
+        fenv['__acc'] = ('a_', 'float')
+        pre = []
+        ov, ot = self.expr(c4.epi, fenv, pre, I + '  ')
+        o += pre
+        o.append(f'{I}  {self.store(t4[1], [fenv[a][0] for a in t4[2]], ov, ot)}')
+        o.append(f'{I}}}')
+        o.append(f'{I}vh_lds_sync();')
+        o.append(f'{ind}}}')
+        self.note(reads, writes)
+        self.mark(out, ind, f'attention {t1[1]}..{t4[1]}')
+
+    def _subst(self, e, repl):
+        """e with reads of the named group values replaced by C variables:
+        (expression, the environment entries binding them)."""
+        def f(n):
+            if n[0] == 'idx' and n[1] in repl:
+                return ('name', '__v_' + n[1])
+            return n
+        return self.rebuild_expr(e, f), {('__v_' + k): (v, 'float') for k, v in repl.items()}

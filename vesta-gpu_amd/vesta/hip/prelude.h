@@ -54,39 +54,73 @@ __device__ __forceinline__ float op_sum(float a, float b) { return a + b; }
 __device__ __forceinline__ float op_max(float a, float b) { return fmaxf(a, b); }
 __device__ __forceinline__ float op_min(float a, float b) { return fminf(a, b); }
 
-// Butterfly over lane bits [lo, 64): afterwards every lane of each group of
-// lanes that differ only in those bits holds the group's combined value.
-#define VH_WAVE_RED(NAME, OP)                                              \
-  __device__ __forceinline__ float NAME(float v, int lo) {                 \
-    for (int o = 32; o >= lo; o >>= 1) v = OP(v, __shfl_xor(v, o, 64));    \
-    return v;                                                              \
-  }
-VH_WAVE_RED(wave_red_sum_hi, op_sum)
-VH_WAVE_RED(wave_red_max_hi, op_max)
-VH_WAVE_RED(wave_red_min_hi, op_min)
+// Lane exchanges. Partners within a row of 16 lanes move through DPP (a
+// lane-permute of the source operand, no memory); across rows through
+// ds_bpermute. DPP controls: quad_perm [1,0,3,2] swaps lanes 2k, 2k+1
+// (partner i^1), quad_perm [2,3,0,1] partner i^2, row_ror:8 partner i^8
+// within the row; row_half_mirror (i <-> 7-i) and row_mirror (i <-> 15-i)
+// are used once every lane of a quad / half-row already holds the same value.
+#define VH_DPP_XOR1 0xB1
+#define VH_DPP_XOR2 0x4E
+#define VH_DPP_ROR8 0x128
+#define VH_DPP_HALF_MIRROR 0x141
+#define VH_DPP_MIRROR 0x140
+template <int CTRL>
+__device__ __forceinline__ float vh_dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
 
-// Butterfly over lane bits [0, width): groups of `width` consecutive lanes.
+// Combine over groups of `width` consecutive lanes (width a power of two
+// <= 64): afterwards every lane of a group holds the group's value.
 #define VH_GROUP_RED(NAME, OP)                                             \
   __device__ __forceinline__ float NAME(float v, int width) {              \
-    for (int o = width >> 1; o > 0; o >>= 1) v = OP(v, __shfl_xor(v, o, 64)); \
+    if (width >= 2) v = OP(v, vh_dpp<VH_DPP_XOR1>(v));                     \
+    if (width >= 4) v = OP(v, vh_dpp<VH_DPP_XOR2>(v));                     \
+    if (width >= 8) v = OP(v, vh_dpp<VH_DPP_HALF_MIRROR>(v));              \
+    if (width >= 16) v = OP(v, vh_dpp<VH_DPP_MIRROR>(v));                  \
+    if (width >= 32) v = OP(v, __shfl_xor(v, 16, 64));                     \
+    if (width >= 64) v = OP(v, __shfl_xor(v, 32, 64));                     \
     return v;                                                              \
   }
 VH_GROUP_RED(group_red_sum, op_sum)
 VH_GROUP_RED(group_red_max, op_max)
 VH_GROUP_RED(group_red_min, op_min)
 
+// Combine over lane bits [lo, 64) (lo a power of two): lanes that differ only
+// in those bits end with the same value, each group of lo consecutive lanes
+// keeping its own position.
+#define VH_WAVE_RED(NAME, OP)                                              \
+  __device__ __forceinline__ float NAME(float v, int lo) {                 \
+    if (lo <= 1) v = OP(v, vh_dpp<VH_DPP_XOR1>(v));                        \
+    if (lo <= 2) v = OP(v, vh_dpp<VH_DPP_XOR2>(v));                        \
+    if (lo <= 4) v = OP(v, __shfl_xor(v, 4, 64));                          \
+    if (lo <= 8) v = OP(v, vh_dpp<VH_DPP_ROR8>(v));                        \
+    if (lo <= 16) v = OP(v, __shfl_xor(v, 16, 64));                        \
+    if (lo <= 32) v = OP(v, __shfl_xor(v, 32, 64));                        \
+    return v;                                                              \
+  }
+VH_WAVE_RED(wave_red_sum_hi, op_sum)
+VH_WAVE_RED(wave_red_max_hi, op_max)
+VH_WAVE_RED(wave_red_min_hi, op_min)
+
 __device__ __forceinline__ float wave_red_sum(float v) { return group_red_sum(v, 64); }
 __device__ __forceinline__ float wave_red_max(float v) { return group_red_max(v, 64); }
 __device__ __forceinline__ float wave_red_min(float v) { return group_red_min(v, 64); }
+
+// Block barrier for LDS traffic only: waits for this wave's LDS operations,
+// not for its global loads (loads issued ahead of time stay in flight).
+__device__ __forceinline__ void vh_lds_sync() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
 
 // Whole-block reduction; every thread gets the result. `red` is VNWAVE
 // floats of LDS. Ends with the block synchronised.
 #define VH_BLOCK_RED(NAME, WRED, OP)                                       \
   __device__ __forceinline__ float NAME(float v, float* red) {             \
     v = WRED(v);                                                           \
-    __syncthreads();                                                       \
+    vh_lds_sync();                                                         \
     if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = v;                \
-    __syncthreads();                                                       \
+    vh_lds_sync();                                                         \
     float r = red[0];                                                      \
     for (int w = 1; w < VNWAVE; ++w) r = OP(r, red[w]);                    \
     return r;                                                              \
@@ -102,9 +136,9 @@ __device__ __forceinline__ void argmax_pair(float& v, int& i, float ov, int oi) 
 }
 __device__ __forceinline__ void block_argmax(float& v, int& i, float* rv, int* ri) {
   for (int o = 32; o > 0; o >>= 1) argmax_pair(v, i, __shfl_xor(v, o, 64), __shfl_xor(i, o, 64));
-  __syncthreads();
+  vh_lds_sync();
   if ((threadIdx.x & 63) == 0) { rv[threadIdx.x >> 6] = v; ri[threadIdx.x >> 6] = i; }
-  __syncthreads();
+  vh_lds_sync();
   v = rv[0]; i = ri[0];
   for (int w = 1; w < VNWAVE; ++w) argmax_pair(v, i, rv[w], ri[w]);
 }
@@ -201,7 +235,7 @@ __device__ __forceinline__ void drain() {
 // is visible to every thread of the block.
 __device__ __forceinline__ void block_sync() {
   drain();
-  __syncthreads();
+  vh_lds_sync();
 }
 
 // Four floats of global scratch at float index i (a multiple of 4), coherent.
@@ -260,7 +294,7 @@ __device__ __forceinline__ void stage_ldc(float* dst, const float* src, int n) {
 #define VH_SPIN_LIMIT (1u << 24)
 __device__ __forceinline__ void grid_arrive(unsigned* bar) {
   drain();
-  __syncthreads();
+  vh_lds_sync();
   if (threadIdx.x == 0)
     __hip_atomic_fetch_add(bar + VH_BAR_LINE * (blockIdx.x % VH_BAR_GROUPS), 1u, __ATOMIC_RELAXED,
                            __HIP_MEMORY_SCOPE_AGENT);
@@ -291,7 +325,7 @@ __device__ __forceinline__ void grid_wait(unsigned* bar, unsigned nblk, unsigned
       }
     }
   }
-  __syncthreads();
+  vh_lds_sync();
 }
 __device__ __forceinline__ void grid_sync(unsigned* bar, unsigned nblk, unsigned& k) {
   k += 1u;

@@ -179,7 +179,8 @@ class Kernel:
         self.lowered = lowered
         self.S = torch.zeros(max(1, lowered.scratch_floats), dtype=torch.float32, device='cuda')
         self.bar = torch.zeros(lowered.counters, dtype=torch.int32, device='cuda')
-        self.TS = torch.zeros(1024, dtype=torch.int64, device='cuda')
+        # timing: clock ticks per (site, block), site-major
+        self.TS = torch.zeros(max(1024, len(lowered.sites) * self.grid), dtype=torch.int64, device='cuda')
         self.args = None
 
     def view(self, name):

@@ -63,6 +63,7 @@ from pathlib import Path
 import numpy as np
 
 from .interp import parse
+from .attn import AttnMixin
 from .stream import StreamMixin
 
 PRELUDE_PATH = Path(__file__).resolve().parent / 'hip' / 'prelude.h'
@@ -83,6 +84,7 @@ BIG = 1 << 16                 # a residue this large is streamed, never recomput
 LANE_MIN = 32                 # lane-split a fold only if it is at least this long
 GRIDRED_MIN = 1 << 14         # grid reduction for a fold at least this long into few points
 GRIDRED_POINTS = 8
+REPL_MAX = 1 << 14            # points a replicated (every-block) statement may have
 UNROLL = 8                    # rows (tile) / vectors (lane) whose loads are issued together
 TILE_LANES = 8                # tile: lanes per row (8 x 16 bytes = one 128-byte line of a weight row)
 LINE_WORDS = 32               # one 128-byte line per counter
@@ -104,7 +106,7 @@ class Lowered:
     shared_bytes: int             # dynamic LDS per block
     barriers_per_launch: int
     plan: list = field(default_factory=list)      # (statement, placement) for reading
-    sites: list = field(default_factory=list)     # timing: label of each timed site
+    sites: list = field(default_factory=list)     # timing: label of each timed site (TS is [site][block])
     counters: int = 2                             # length of the bar array
     block: int = BLOCK
     grid_max: int = GRID_MAX
@@ -315,9 +317,11 @@ class LowerError(ValueError):
     pass
 
 
-class Lowering(StreamMixin):
+class Lowering(StreamMixin, AttnMixin):
     NWAVE, BLOCK, REG_MAX = NWAVE, BLOCK, REG_MAX
     show_stmt = staticmethod(show_stmt)
+    nodes_of = staticmethod(nodes)
+    rebuild_expr = staticmethod(rebuild)
 
     def __init__(self, stmts, res, axis_max, outputs, batch, timing=False, grid=None):
         self.res = {n: (tuple(int(x) for x in shp), dt) for n, (shp, dt) in res.items()}
@@ -331,6 +335,7 @@ class Lowering(StreamMixin):
         self.step_ext = {}        # step variable -> loop count
         self.axes_of = {}         # local -> axes
         self.emitted = set()
+        self.emit_stmts = []
         self.alias = {}
         self.tmp = 0
         self.plan = []
@@ -349,6 +354,11 @@ class Lowering(StreamMixin):
         self.loops = []
         self.stage_top = 0
         self.capture = None
+        self.in_fold = False          # generating the body of a fold
+        self.stream_part = {}         # value -> how a stream site split its points over blocks
+        self.local_fb = {}            # feedback target -> ('tok', source) | ('inc', k) kept block-local
+        self.local_vals = {}          # value -> LDS array every block holds it in (redundant combine)
+        self.shared_decls = []        # kernel-scope __shared__ arrays
         self.scan(stmts)
         stmts = self.normalise(stmts)
         stmts = self.hoist(stmts)
@@ -378,6 +388,7 @@ class Lowering(StreamMixin):
                 if s[1] not in self.res:
                     raise NameError(f'residue {s[1]} not supplied')
                 self.emitted.add(s[1])
+                self.emit_stmts.append(s)
             elif k == 'let':
                 self.axes_of[s[1]] = tuple(s[2])
             elif k == 'step':
@@ -688,8 +699,19 @@ class Lowering(StreamMixin):
                 self.in_group.add(id(s))
                 i += 1
                 continue
-            self.place[id(s)] = 'thread'
+            self.place[id(s)] = 'repl' if self.repl_ok(s) else 'thread'
             i += 1
+
+    def repl_ok(self, s):
+        """A small statement that reads only residues is computed by every
+        block for every point (so no block waits for another to read it)."""
+        if s[0] != 'let' or top_folds(s[3]) or s[1] in self.outputs:
+            return False
+        if any(a in self.dynamic for a in s[2]) or self.size(s[2]) > REPL_MAX:
+            return False
+        if self.reads(s[3]) - set(self.res):
+            return False
+        return not any(n[1] in self.emitted for n in self.res_reads(s[3]))
 
     def epilogue_ok(self, s, made, axes):
         if list(s[2]) != axes or top_folds(s[3]) or s[1] in self.alias or s[1] in set(self.alias.values()):
@@ -985,6 +1007,11 @@ class Lowering(StreamMixin):
                     return f'({a} {op} {b})', 'bool'
                 return f'({self.as_float(a, ta)} {op} {self.as_float(b, tb)})', 'bool'
             if op == '/':
+                if self.in_fold and e[3][0] == 'num' and float(e[3][1]) != 0.0:
+                    # a term of a fold (whose summation order is not NumPy's
+                    # anyway): divide by a constant as a multiply by its
+                    # correctly rounded reciprocal (within 1.5 ulp of the quotient)
+                    return f'({self.as_float(a, ta)} * {c_float(np.float32(1.0) / np.float32(e[3][1]))})', 'float'
                 return f'({self.as_float(a, ta)} / {self.as_float(b, tb)})', 'float'
             if ta == 'int' and tb == 'int':
                 return f'({a} {op} {b})', 'int'
@@ -1088,6 +1115,9 @@ class Lowering(StreamMixin):
 
     def res_value(self, n, addr):
         dt = self.res[n][1]
+        if n in self.local_fb:
+            kind = self.local_fb[n][0]
+            return (f'xfb_{n}[{addr}]' if kind == 'tok' else f'tlv_{n}'), 'int'
         if self.coherent(n):
             if dt == 'f16':
                 return f'ldc_h(rb_{n}, {addr})', 'float'
@@ -1199,6 +1229,9 @@ class Lowering(StreamMixin):
         gl_writes = {n for n in writes if n not in self.private}
         if (gl_reads & self.dirty) or (gl_writes & self.readers) or (gl_writes & self.dirty):
             self.barrier(out, ind, what)
+        if not getattr(self, 'first_barrier', True):
+            self.head_io[0] |= gl_reads
+            self.head_io[1] |= gl_writes
         self.readers |= gl_reads
 
     def barrier(self, out, ind, what='', pre_wait=()):
@@ -1208,6 +1241,7 @@ class Lowering(StreamMixin):
         out.append(f'{ind}grid_wait(bar, nblk, bk_);')
         if self.loops:
             self.loops[-1]['body_barrier'] = True
+        self.first_barrier = True
         self.barriers += self.mult
         self.dirty, self.readers = set(), set()
         self.mark(out, ind, f'barrier before {what}')
@@ -1222,7 +1256,7 @@ class Lowering(StreamMixin):
         if k >= 1024:
             return
         self.sites.append(label)
-        out.append(f'{ind}if (gtid == 0) {{ unsigned long long tn_ = vh_clock(); ts_sh[{k}] += tn_ - tlast_; '
+        out.append(f'{ind}if (tid == 0) {{ unsigned long long tn_ = vh_clock(); ts_sh[{k}] += tn_ - tlast_; '
                    f'tlast_ = tn_; }}')
 
     # ------------------------------------------------------------ statements
@@ -1244,7 +1278,11 @@ class Lowering(StreamMixin):
                 continue
             if id(s) in self.groups:
                 lead, members = self.groups[id(s)]
-                self.gen_group(lead, members, out, ind)
+                at = self.attn_of(lead, members)
+                if at is not None:
+                    self.gen_attn(at, out, ind)
+                else:
+                    self.gen_group(lead, members, out, ind)
                 i += len(members)
                 continue
             p = self.place[id(s)]
@@ -1273,6 +1311,8 @@ class Lowering(StreamMixin):
                 continue
             if p == 'gridred':
                 self.gen_gridred(s, out, ind)
+            elif p == 'repl':
+                self.gen_repl(s, out, ind)
             else:                   # thread, or an epilogue statement its contraction could not take
                 self.gen_thread(s, out, ind)
             i += 1
@@ -1593,7 +1633,7 @@ class Lowering(StreamMixin):
         o.append(f'{J2}    for (int v_ = 0; v_ < {vec}; ++v_) red_sh[(wave * {rch} + r_) * {tj} + cl_ * {vec} + v_] = '
                  f'acc_[r_][v_];')
         o.append(f'{J2}}}')
-        o.append(f'{J2}__syncthreads();')
+        o.append(f'{J2}vh_lds_sync();')
         q = rch * tj
 
         def finish(val, lines, ind2):
@@ -1634,7 +1674,7 @@ class Lowering(StreamMixin):
         o.append(f'{J2}    }}')
         o.append(f'{J2}  }}')
         o.append(f'{J2}}}')
-        o.append(f'{J2}__syncthreads();')
+        o.append(f'{J2}vh_lds_sync();')
         o.append(f'{I}}}')
         o.append(f'{ind}}}')
         self.note(reads, writes)
@@ -1867,7 +1907,7 @@ class Lowering(StreamMixin):
     def gen_private(self, run, out, ind):
         reads = self.root_reads([t[3] for t in run], exclude={t[1] for t in run})
         self.sync(reads, set(), out, ind, run[0][1])
-        out.append(f'{ind}__syncthreads();')
+        out.append(f'{ind}vh_lds_sync();')
         # global values the run reads are staged into LDS once (coherent loads)
         base = off = self.lds_floats
         staged = {}
@@ -1880,15 +1920,32 @@ class Lowering(StreamMixin):
                     off += -(-size // 4) * 4
         self.stage_floats = max(self.stage_floats, off - base)
         if staged:
-            out.append(f'{ind}__syncthreads();')
+            out.append(f'{ind}vh_lds_sync();')
             self.mark(out, ind, f'stage {",".join(staged)}')
         self.staged = staged
+        # which waves wrote each value of the run: 'all' (every wave holds every
+        # point), 'wave' (point p in wave p % NWAVE) or 'thread' (any thread);
+        # a statement waits for the block only when it may read another wave's writes
+        wmap = {}
         for s in run:
             self.plan.append((show_stmt(s), 'private'))
             name, axes, e = s[1], list(s[2]), s[3]
             npts = self.size(axes)
             o = out
-            if e[0] == 'fold' and npts <= 64 and self.static[e[2]] >= 64:
+            is_fold = e[0] == 'fold' and npts <= 64 and self.static[e[2]] >= 64
+            mine = ('all' if npts == 1 else 'wave') if is_fold else 'thread'
+            same = [('name', a) for a in axes]
+            need = False
+            for n in nodes(e):
+                if n[0] in ('idx', 'name') and n[1] in wmap:
+                    m = wmap[n[1]]
+                    if m == 'thread' or (m[0] == 'wave' and not (mine == 'wave' and m[1] == axes
+                                                                  and list(n[2]) == same)):
+                        need = True
+            if need:
+                o.append(f'{ind}vh_lds_sync();')
+            wmap[name] = ('wave', axes) if mine == 'wave' else mine
+            if is_fold:
                 self.private_fold(name, axes, e, npts, o, ind)
             elif axes and -(-self.static[axes[-1]] // ((NWAVE - 1) * WAVE)) <= 8:
                 self.private_points(s, npts, o, ind)
@@ -1907,8 +1964,8 @@ class Lowering(StreamMixin):
                 o.append(f'{I2}{self.store(name, [env[a][0] for a in axes], v, t)}')
                 o.append(f'{I}}}')
                 o.append(f'{ind}}}')
-            out.append(f'{ind}__syncthreads();')
             self.mark(out, ind, f'private {name}')
+        out.append(f'{ind}vh_lds_sync();')
         self.staged = {}
 
     def private_points(self, s, npts, o, ind):
@@ -1996,51 +2053,34 @@ class Lowering(StreamMixin):
         return lines
 
     def private_fold(self, name, axes, e, npts, o, ind):
-        """A fold into a few points, every wave of the block working: each
-        point's fold is split over G waves (lanes strided along the fold),
-        wave partials combined in a fixed order through LDS."""
+        """A fold into a few points: a single point is folded by every wave
+        (each wave ends holding it, so readers need no block barrier); several
+        points go one per wave (point p in wave p % NWAVE), lanes strided
+        along the fold, wave butterfly."""
         op, ax, body = e[1], e[2], e[3]
         K = self.static[ax]
-        if npts >= NWAVE:
-            G = 1
-        else:
-            G = 1
-            while G * 2 * npts <= NWAVE:
-                G *= 2
-        per = G * WAVE
-        T = -(-K // per)
-        self.red_floats = max(getattr(self, 'red_floats', 4), min(npts, NWAVE) * G)
-        o.append(f'{ind}for (int w_ = wave; w_ < {npts * G}; w_ += {NWAVE}) {{  // private {name}')
+        T = -(-K // WAVE)
+        first = 'wave' if npts > 1 else '0'
+        o.append(f'{ind}for (int p_ = {first}; p_ < {npts}; p_ += {NWAVE if npts > 1 else 1}) {{  // private {name}')
         I = ind + '  '
-        o.append(f'{I}const int p_ = w_ / {G}, q_ = w_ % {G};')
         env = self.decode('p_', axes, o, I)
         o.append(f'{I}float a_ = {FOLD_INIT[op]};')
         o.append(f'{I}#pragma unroll' + ('' if T <= 16 else ' 8'))
         o.append(f'{I}for (int it_ = 0; it_ < {T}; ++it_) {{')
-        o.append(f'{I}  const int k_ = q_ * {WAVE} + lane + it_ * {per};')
+        o.append(f'{I}  const int k_ = lane + it_ * {WAVE};')
         o.append(f'{I}  if (k_ < {self.ext_c(ax)}) {{')
         pre = []
-        v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '    ')
+        self.in_fold = True
+        try:
+            v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '    ')
+        finally:
+            self.in_fold = False
         o += pre
         o.append(f'{I}    a_ = {FOLD_OP[op]}(a_, {self.as_float(v, t)});')
         o.append(f'{I}  }}')
         o.append(f'{I}}}')
         o.append(f'{I}a_ = wave_red_{op}(a_);')
-        if G == 1:
-            o.append(f'{I}if (lane == 0) {self.store(name, [env[a][0] for a in axes], "a_", "float")}')
-            o.append(f'{ind}}}')
-            return
-        o.append(f'{I}if (lane == 0) red_sh[w_] = a_;')
-        o.append(f'{ind}}}')
-        o.append(f'{ind}__syncthreads();')
-        o.append(f'{ind}if (tid < {npts}) {{')
-        I = ind + '  '
-        o.append(f'{I}const int p_ = tid;')
-        env = self.decode('p_', axes, o, I)
-        o.append(f'{I}float a_ = red_sh[p_ * {G}];')
-        o.append(f'{I}#pragma unroll')
-        o.append(f'{I}for (int q_ = 1; q_ < {G}; ++q_) a_ = {FOLD_OP[op]}(a_, red_sh[p_ * {G} + q_]);')
-        o.append(f'{I}{self.store(name, [env[a][0] for a in axes], "a_", "float")}')
+        o.append(f'{I}if (lane == 0) {self.store(name, [env[a][0] for a in axes], "a_", "float")}')
         o.append(f'{ind}}}')
 
     # -- group
@@ -2175,7 +2215,7 @@ class Lowering(StreamMixin):
         o.append(f'{J2}  #pragma unroll')
         o.append(f'{J2}  for (int v_ = 0; v_ < {vec}; ++v_) red_sh[wave * {tj} + cl_ * {vec} + v_] = acc_[v_];')
         o.append(f'{J2}}}')
-        o.append(f'{J2}__syncthreads();')
+        o.append(f'{J2}vh_lds_sync();')
         o.append(f'{J2}if (tid < {tj}) {{')
         K3 = J2 + '  '
         o.append(f'{K3}const float s_ = ' + ' + '.join(f'red_sh[{w * tj} + tid]' for w in range(NWAVE)) + ';')
@@ -2188,7 +2228,7 @@ class Lowering(StreamMixin):
         o += pre
         o.append(f'{K3}{self.store(name, [fenv[a][0] for a in t[2]], v, ty)}')
         o.append(f'{J2}}}')
-        o.append(f'{J2}__syncthreads();')
+        o.append(f'{J2}vh_lds_sync();')
         o.append(f'{I}}}')
         o.append(f'{ind}}}')
 
@@ -2244,21 +2284,35 @@ class Lowering(StreamMixin):
 
     def gen_argmax(self, s1, s2, out, ind):
         """best = fold max n: E[n]; next = lowest n with E[n] == best: one pass
-        over E keeping (value, index) pairs, ties to the lower index; per-block
-        pairs combined in block order by the last block."""
+        over E keeping (value, index) pairs, ties to the lower index. Each
+        block reduces the points it made itself when E is a streamed value
+        (no grid barrier before), else a grid-strided share; after one grid
+        barrier every block combines the per-block pairs in block order, so
+        every block holds the result (kept in LDS for block-local feedback)."""
         name, axes, e = s1[1], list(s1[2]), s1[3]
         ax, body = e[2], e[3]
         reads = self.root_reads([e])
         writes = {self.root(name), self.root(s2[1])}
-        self.sync(reads, writes, out, ind, name)
-        self.plan.append((show_stmt(s1), 'gridred argmax'))
-        self.plan.append((show_stmt(s2), 'gridred argmax'))
+        part, src = None, None
+        if body[0] == 'idx' and body[1] in self.axes_of:
+            src = self.root(body[1])
+            pp = self.stream_part.get(src)
+            if (pp and pp['pts'] == [ax] and pp['reg'] == axes and src in self.dirty
+                    and list(body[2]) == [('name', a) for a in axes + [ax]]):
+                part = pp
+        if part:
+            self.sync(reads - {src}, writes, out, ind, name)
+            self.readers.add(src)
+            out.append(f'{ind}block_sync();  // this block\'s own points of {body[1]}')
+        else:
+            self.sync(reads, writes, out, ind, name)
+        self.plan.append((show_stmt(s1), 'argmax' + (' (own points)' if part else ' (grid-strided)')))
+        self.plan.append((show_stmt(s2), 'argmax'))
         npts = self.size(axes)
         poff = self.alloc_scratch(2 * npts * GRID_MAX)
-        coff = self.alloc_counters(1)
         o = out
         I = ind + '  '
-        o.append(f'{ind}{{  // argmax {name}, {s2[1]}')
+        o.append(f'{ind}{{  // argmax {name}, {s2[1]}: per-block pairs')
         envs = []
         for p in range(npts):
             lines = []
@@ -2267,7 +2321,12 @@ class Lowering(StreamMixin):
             o += lines
             o.append(f'{I}{{')
             o.append(f'{I}  float bv_ = -INFINITY; int bi_ = 0x7fffffff;')
-            o.append(f'{I}  for (int k_ = gtid; k_ < {self.static[ax]}; k_ += nthr) {{')
+            if part:
+                o.append(f'{I}  const int k0_ = (int)blockIdx.x * {part["PPB"]};')
+                o.append(f'{I}  const int k1_ = k0_ + {part["PPB"]} < {part["P"]} ? k0_ + {part["PPB"]} : {part["P"]};')
+                o.append(f'{I}  for (int k_ = k0_ + tid; k_ < k1_; k_ += {BLOCK}) {{')
+            else:
+                o.append(f'{I}  for (int k_ = gtid; k_ < {self.static[ax]}; k_ += nthr) {{')
             pre = []
             v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '    ')
             o += pre
@@ -2275,33 +2334,64 @@ class Lowering(StreamMixin):
             o.append(f'{I}    if (v_ > bv_ || (v_ == bv_ && k_ < bi_)) {{ bv_ = v_; bi_ = k_; }}')
             o.append(f'{I}  }}')
             o.append(f'{I}  block_argmax(bv_, bi_, red_sh, (int*)(red_sh + {NWAVE}));')
-            o.append(f'{I}  if (tid == 0) {{ stc(S + {poff + p * GRID_MAX} + blockIdx.x, bv_); '
-                     f'stc(S + {poff + (npts + p) * GRID_MAX} + blockIdx.x, (float)bi_); }}')
+            o.append(f'{I}  if (tid == 0) {{ stcs(rb_S, {poff + p * GRID_MAX} + blockIdx.x, bv_); '
+                     f'stcs(rb_S, {poff + (npts + p) * GRID_MAX} + blockIdx.x, (float)bi_); }}')
             o.append(f'{I}}}')
-        o.append(f'{I}if (last_arrival(bar + {coff}, nblk, &flag_sh)) {{')
+        o.append(f'{ind}}}')
+        self.barrier(out, ind, f'combine {name}')
         cval = s2[3][3][3][1]
+        o.append(f'{ind}{{  // argmax {name}, {s2[1]}: every block combines the pairs in block order')
         for p in range(npts):
-            env = envs[p]
-            o.append(f'{I}  {{')
-            o.append(f'{I}    float bv_ = -INFINITY; int bi_ = 0x7fffffff;')
-            o.append(f'{I}    for (int b_ = tid; b_ < (int)nblk; b_ += {BLOCK}) {{')
-            o.append(f'{I}      const float v_ = ldc(S + {poff + p * GRID_MAX} + b_);')
-            o.append(f'{I}      const int i_ = (int)ldc(S + {poff + (npts + p) * GRID_MAX} + b_);')
-            o.append(f'{I}      if (v_ > bv_ || (v_ == bv_ && i_ < bi_)) {{ bv_ = v_; bi_ = i_; }}')
-            o.append(f'{I}    }}')
-            o.append(f'{I}    block_argmax(bv_, bi_, red_sh, (int*)(red_sh + {NWAVE}));')
-            o.append(f'{I}    if (tid == 0) {{')
+            lines = []
+            env = self.decode_const(str(p), axes, lines, I) if axes else {}
+            o += lines
+            o.append(f'{I}{{')
+            o.append(f'{I}  float bv_ = -INFINITY; int bi_ = 0x7fffffff;')
+            o.append(f'{I}  for (int b_ = tid; b_ < (int)nblk; b_ += {BLOCK}) {{')
+            o.append(f'{I}    const float v_ = ldcs(rb_S, {poff + p * GRID_MAX} + b_);')
+            o.append(f'{I}    const int i_ = (int)ldcs(rb_S, {poff + (npts + p) * GRID_MAX} + b_);')
+            o.append(f'{I}    if (v_ > bv_ || (v_ == bv_ && i_ < bi_)) {{ bv_ = v_; bi_ = i_; }}')
+            o.append(f'{I}  }}')
+            o.append(f'{I}  block_argmax(bv_, bi_, red_sh, (int*)(red_sh + {NWAVE}));')
+            o.append(f'{I}  const float nv_ = bi_ == 0x7fffffff ? {c_float(cval)} : (float)bi_;')
+            o.append(f'{I}  if (tid == 0) {{')
+            o.append(f'{I}    amx_[{p}] = nv_;')
+            o.append(f'{I}    if (blockIdx.x == 0) {{')
             o.append(f'{I}      {self.store(name, [env[a][0] for a in axes], "bv_", "float")}')
-            o.append(f'{I}      {self.store(s2[1], [env[a][0] for a in axes], f"(bi_ == 0x7fffffff ? {c_float(cval)} : (float)bi_)", "float")}')
+            o.append(f'{I}      {self.store(s2[1], [env[a][0] for a in axes], "nv_", "float")}')
             o.append(f'{I}    }}')
             o.append(f'{I}  }}')
-        o.append(f'{I}}}')
+            o.append(f'{I}}}')
+        o.append(f'{I}vh_lds_sync();')
         o.append(f'{ind}}}')
+        self.local_vals[s2[1]] = ('amx_', npts)
+        self.shared_decls.append(f'__shared__ float amx_[{npts}];')
         self.note(reads, writes)
         self.red_floats = max(getattr(self, 'red_floats', 4), 2 * NWAVE)
         self.mark(out, ind, f'argmax {name}')
 
     # -- one thread per point
+    def gen_repl(self, s, out, ind):
+        """Every block computes every point and stores it (identical values),
+        then reads only its own stores: no grid barrier is needed before its
+        readers, only the block's own drain."""
+        name, axes, e = s[1], list(s[2]), s[3]
+        reads = self.root_reads([e])
+        writes = {self.root(name)}
+        self.sync(reads, writes, out, ind, name)
+        self.plan.append((show_stmt(s), 'replicated'))
+        I = ind + '  '
+        out.append(f'{ind}for (int p_ = tid; p_ < {self.count_c(axes)}; p_ += {BLOCK}) {{  // replicated {name}')
+        env = self.decode('p_', axes, out, I)
+        pre = []
+        v, t = self.expr(e, env, pre, I)
+        out += pre
+        out.append(f'{I}{self.store(name, [env[a][0] for a in axes], v, t)}')
+        out.append(f'{ind}}}')
+        out.append(f'{ind}block_sync();')
+        self.readers |= {n for n in reads if n not in self.private}
+        self.mark(out, ind, f'replicated {name}')
+
     def gen_thread(self, s, out, ind):
         name, axes, e = s[1], list(s[2]), s[3]
         reads = self.root_reads([e])
@@ -2405,19 +2495,68 @@ class Lowering(StreamMixin):
             self.step_env[var] = saved
 
     # ------------------------------------------------------------ the kernel
+    def plan_feedback(self, feedback):
+        """Feedback every block can keep to itself: a token chosen by an
+        argmax every block combines, and a step counter. Then no grid barrier
+        is needed between steps for it; block 0 alone writes the residues back
+        for the host."""
+        self.local_fb = {}
+        if not feedback:
+            return
+        tok_srcs = {t[1] for t in self.argmax.values()}
+        plan = {}
+        for dst, src in feedback.items():
+            if dst not in self.res:
+                raise NameError(f'feedback target {dst} not supplied')
+            shape, dt = self.res[dst]
+            if dt != 'i32' or dst in self.emitted:
+                return
+            if isinstance(src, int):
+                if math.prod(shape) != 1:
+                    return
+                plan[dst] = ('inc', src)
+            elif src in tok_srcs and src in self.axes_of and math.prod(shape) == self.size(self.axes_of[src]):
+                plan[dst] = ('tok', src)
+            else:
+                return
+        self.local_fb = plan
+
     def kernel(self, feedback):
         """Body of one step, the feedback stores, and the history of chosen tokens."""
         self.dirty, self.readers = set(), set()
         self.red_floats = 4
+        self.plan_feedback(feedback)
+        self.head_io = [set(), set()]
+        self.first_barrier = False
         body = []
         ind = '    '
         self.gen(self.stmts, body, ind)
         self.history = None
-        if feedback:
+        self.wrap_barrier = True
+        if feedback and self.local_fb:
+            for dst, (kind, src) in self.local_fb.items():
+                if kind == 'inc':
+                    body.append(f'{ind}tlv_{dst} += {src};')
+                    body.append(f'{ind}if (blockIdx.x == 0 && tid == 0) stc_i(R_{dst}, tlv_{dst});')
+                    continue
+                arr, n = self.local_vals[src]
+                self.history = n
+                body.append(f'{ind}if (tid < {n}) {{  // {dst} <- {src}, in every block')
+                body.append(f'{ind}  const int nx_ = (int){arr}[tid];')
+                body.append(f'{ind}  if (blockIdx.x == 0 && tok_out != nullptr) tok_out[st_ * {n} + tid] = nx_;')
+                body.append(f'{ind}  const int xi_ = (tok_in != nullptr && st_ + 1 < nsteps) ? '
+                            f'tok_in[(st_ + 1) * {n} + tid] : nx_;')
+                body.append(f'{ind}  xfb_{dst}[tid] = xi_;')
+                body.append(f'{ind}  if (blockIdx.x == 0) stc_i(R_{dst} + tid, xi_);')
+                body.append(f'{ind}}}')
+            body.append(f'{ind}vh_lds_sync();')
+            # a barrier between steps only if the next step's first phase touches
+            # what this step's last phase wrote or read
+            hr, hw = self.head_io
+            self.wrap_barrier = bool(hr & self.dirty or hw & (self.readers | self.dirty))
+        elif feedback:
             self.barrier(body, ind, 'feedback')
             for dst, src in feedback.items():
-                if dst not in self.res:
-                    raise NameError(f'feedback target {dst} not supplied')
                 dt = self.res[dst][1]
                 if isinstance(src, int):
                     if dt == 'i32':
@@ -2506,7 +2645,9 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
     for name, (shape, dt) in low.res.items():
         if math.prod(shape) == 1 and len(shape) <= 1 and name not in low.emitted:
             cty = {'i32': 'int', 'f32': 'float', 'f16': 'float'}[dt]
-            if low.coherent(name):
+            if name in low.local_fb:
+                val = f'xfb_{name}[0]' if low.local_fb[name][0] == 'tok' else f'tlv_{name}'
+            elif low.coherent(name):
                 val = {'i32': f'ldc_i(R_{name})', 'f32': f'ldc(R_{name})', 'f16': f'ldc_h(rb_{name}, 0)'}[dt]
             else:
                 val = f'h2f(R_{name}[0])' if dt == 'f16' else f'R_{name}[0]'
@@ -2517,6 +2658,17 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
         head += lines
         head.append(f'    const int E_{a} = {v};')
         head.append(f'    if (E_{a} > {low.static[a]} || E_{a} < 1) break;  // beyond its bound: stop')
+    # block-local feedback state: the chosen tokens in LDS, step counters in registers
+    fb_init = []
+    for name, (kind, _) in low.local_fb.items():
+        n = math.prod(low.res[name][0])
+        if kind == 'tok':
+            fb_init += [f'  __shared__ int xfb_{name}[{n}];\n',
+                        f'  for (int i_ = tid; i_ < {n}; i_ += {BLOCK}) xfb_{name}[i_] = ldc_i(R_{name} + i_);\n']
+        else:
+            fb_init.append(f'  int tlv_{name} = ldc_i(R_{name});\n')
+    if fb_init:
+        fb_init.append('  vh_lds_sync();\n')
     red = max(low.red_floats, 4)
     prelude = PRELUDE_PATH.read_text()
     src = (f'#define VBLOCK {BLOCK}\n' + prelude + '\n'
@@ -2536,14 +2688,17 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
               '  __syncthreads();\n'
               '  unsigned long long tlast_ = vh_clock();\n' if timing else '')
            + '\n'.join(pre) + '\n'
+           + ''.join(f'  {d}\n' for d in low.shared_decls)
+           + ''.join(fb_init)
            + '  for (int st_ = 0; st_ < nsteps; ++st_) {\n'
            + '    const int tid = vh_opaque(tid_k_), lane = tid & 63, wave = tid >> 6;\n'
            + '\n'.join(head) + '\n'
            + '\n'.join(body) + '\n'
-           + '    if (st_ + 1 < nsteps) grid_sync(bar, nblk, bk_);  // feedback visible to the next step\n'
+           + ('    if (st_ + 1 < nsteps) grid_sync(bar, nblk, bk_);  // feedback visible to the next step\n'
+              if low.wrap_barrier else '')
            + '  }\n'
-           + ('  if (blockIdx.x == 0) { __syncthreads(); '
-              f'for (int i_ = tid; i_ < {len(low.sites)}; i_ += {BLOCK}) TS[i_] += ts_sh[i_]; }}\n'
+           + ('  __syncthreads();\n'
+              f'  for (int i_ = tid; i_ < {len(low.sites)}; i_ += {BLOCK}) TS[i_ * nblk + blockIdx.x] += ts_sh[i_];\n'
               if timing else '')
            + '  grid_exit(bar, nblk);\n}\n')
     scratch = {}

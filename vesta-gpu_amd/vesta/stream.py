@@ -254,6 +254,8 @@ class StreamMixin:
                  f'points/block={PPB} rows={R}{" prefetched" if prefetch else ""}')
         for x in lane_decl:
             o.append(f'{I}{x}')
+        # which block made which points (an argmax over them can stay in the block)
+        self.stream_part[self.root(name)] = dict(pts=list(st.pts), PPB=PPB, P=P, reg=list(reg))
         # the other factor, as floats in LDS laid out [row, fold]
         direct = self.direct_lds(c, reg)
         for rc in range(nrch):
@@ -438,7 +440,7 @@ class StreamMixin:
         anything else is evaluated point by point, all loads of a thread issued
         before its LDS stores."""
         A = c.A
-        o.append(f'{I}__syncthreads();')
+        o.append(f'{I}vh_lds_sync();')
         want = list(reg) + list(c.fold_axes)
         if (A[0] == 'idx' and A[1] in self.axes_of and self.root(A[1]) in self.g
                 and self.root(A[1]) not in self.private and list(self.axes_of[self.root(A[1])]) == want
@@ -449,7 +451,7 @@ class StreamMixin:
             if rows < rch:
                 o.append(f'{I}for (int e_ = tid; e_ < {(rch - rows) * K}; e_ += {self.BLOCK}) '
                          f'sh_f[{abase} + {rows * K} + e_] = 0.0f;')
-            o.append(f'{I}__syncthreads();')
+            o.append(f'{I}vh_lds_sync();')
             return
         T = -(-(rch * K) // self.BLOCK)
         o.append(f'{I}#pragma unroll' + ('' if T <= 16 else ' 8'))
@@ -472,7 +474,7 @@ class StreamMixin:
         o.append(f'{J3}sh_f[{abase} + e_] = v_;')
         o.append(f'{J2}}}')
         o.append(f'{I}}}')
-        o.append(f'{I}__syncthreads();')
+        o.append(f'{I}vh_lds_sync();')
 
     # ------------------------------------------------------------ small helpers
     def load_type(self, dt, vec):
