@@ -224,6 +224,42 @@ __device__ __forceinline__ unsigned ldg4_nt(vh_rsrc r, unsigned i) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, i * 2u, 0, VH_NT);
 }
 
+// Fixed-point accumulators: fp32 values summed exactly as 64-bit integers in
+// units of 2^-32 (any order of atomic adds gives the same bits), read back as
+// fp32. Element i of such a buffer is the 8 bytes at float index i of global
+// scratch (i even).
+#define VH_FX_SCALE 4294967296.0
+__device__ __forceinline__ long long vh_f2fx(float v) { return (long long)rint((double)v * VH_FX_SCALE); }
+__device__ __forceinline__ float vh_fx2f(long long q) { return (float)((double)q * (1.0 / VH_FX_SCALE)); }
+__device__ __forceinline__ float fxld(vh_rsrc r, unsigned i) {
+  return vh_fx2f(__builtin_bit_cast(long long, __builtin_amdgcn_raw_buffer_load_b64(r, i * 4u, 0, VH_SC1)));
+}
+__device__ __forceinline__ void fxst(vh_rsrc r, unsigned i, float v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(vh_u32x2, vh_f2fx(v)), r, i * 4u, 0, VH_SC1);
+}
+__device__ __forceinline__ void fxadd(float* S, unsigned i, float v) {
+  __hip_atomic_fetch_add((unsigned long long*)(S + i), (unsigned long long)vh_f2fx(v), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+}
+// n fixed-point values at float index off into LDS floats (16-byte loads).
+__device__ __forceinline__ void stage_fx(float* dst, vh_rsrc S, unsigned off, int n) {
+  const int nv = (n + 1) >> 1;
+  for (int base = threadIdx.x; base < nv; base += VBLOCK * 8) {
+    vh_u32x4 v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      v[u] = base + u * VBLOCK < nv ? __builtin_amdgcn_raw_buffer_load_b128(S, (off + 4u * (unsigned)(base + u * VBLOCK)) * 4u, 0, VH_SC1)
+                                    : vh_u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+      if (base + u * VBLOCK < nv) {
+        const int j = 2 * (base + u * VBLOCK);
+        dst[j] = vh_fx2f(__builtin_bit_cast(long long, vh_u32x2{v[u].x, v[u].y}));
+        if (j + 1 < n) dst[j + 1] = vh_fx2f(__builtin_bit_cast(long long, vh_u32x2{v[u].z, v[u].w}));
+      }
+  }
+}
+
 // Wait until every memory operation this wave issued has completed. The
 // signal fences keep the compiler from moving memory operations across it.
 __device__ __forceinline__ void drain() {
@@ -305,18 +341,19 @@ __device__ __forceinline__ void grid_arrive(unsigned* bar) {
 // VH_SPIN_LIMIT polls (seconds) gives up and raises the error word
 // bar[VH_BAR_LINE * 9 + 1] (only a broken launch configuration can get there).
 #define VH_POLL_WAVE (VNWAVE - 1)
-__device__ __forceinline__ unsigned ldc_ub(vh_rsrc r, unsigned i) {
-  return __builtin_amdgcn_raw_buffer_load_b32(r, i * 4u, 0, VH_SC1);
-}
+
 __device__ __forceinline__ void grid_wait(unsigned* bar, unsigned nblk, unsigned k) {
   if ((int)(threadIdx.x >> 6) == VH_POLL_WAVE) {
-    const vh_rsrc rb = mk_rsrc(bar, VH_BAR_WORDS * 4u);
     const unsigned g = threadIdx.x & 63u;
     bool done = g >= VH_BAR_GROUPS || g >= nblk;
     const unsigned target = done ? 0u : k * ((nblk - g + VH_BAR_GROUPS - 1u) / VH_BAR_GROUPS);
+    // one poll in flight per lane (each counter line is read by every block, so
+    // more polls only queue at its memory channel); polls are atomic loads, so
+    // the compiler neither merges nor hoists them
+    const unsigned* cp = bar + VH_BAR_LINE * (done ? 0u : g);
     unsigned n = 0;
     while (true) {
-      if (!done) done = ldc_ub(rb, VH_BAR_LINE * g) >= target;
+      if (!done) done = ldc_u(cp) >= target;
       if (__all(done)) break;
       __builtin_amdgcn_s_sleep(1);
       if (++n > VH_SPIN_LIMIT) {

@@ -180,7 +180,10 @@ class Kernel:
         self.S = torch.zeros(max(1, lowered.scratch_floats), dtype=torch.float32, device='cuda')
         self.bar = torch.zeros(lowered.counters, dtype=torch.int32, device='cuda')
         # timing: clock ticks per (site, block), site-major
-        self.TS = torch.zeros(max(1024, len(lowered.sites) * self.grid), dtype=torch.int64, device='cuda')
+        # and, after it, each block's arrival / release time at the barriers of a launch's last step
+        from .lower import BTRACE
+        self.TS = torch.zeros(max(1024, (len(lowered.sites) + 2 * BTRACE) * self.grid), dtype=torch.int64,
+                              device='cuda')
         self.args = None
 
     def view(self, name):

@@ -85,6 +85,7 @@ LANE_MIN = 32                 # lane-split a fold only if it is at least this lo
 GRIDRED_MIN = 1 << 14         # grid reduction for a fold at least this long into few points
 GRIDRED_POINTS = 8
 REPL_MAX = 1 << 14            # points a replicated (every-block) statement may have
+BTRACE = 96                   # timing: barriers of the last step traced per block
 UNROLL = 8                    # rows (tile) / vectors (lane) whose loads are issued together
 TILE_LANES = 8                # tile: lanes per row (8 x 16 bytes = one 128-byte line of a weight row)
 LINE_WORDS = 32               # one 128-byte line per counter
@@ -1236,9 +1237,17 @@ class Lowering(StreamMixin, AttnMixin):
 
     def barrier(self, out, ind, what='', pre_wait=()):
         out.append(f'{ind}bk_ += 1u; grid_arrive(bar);' + (f'  // before {what}' if what else ''))
+        self.mark(out, ind, f'arrive before {what}')
+        if self.timing:
+            # the launch's last step: each block's arrival and release time at every barrier
+            out.append(f'{ind}if (tid == 0 && st_ + 1 == nsteps && bk_ - bk0_ <= {BTRACE}u) '
+                       f'TS[TSB_ + (bk_ - bk0_ - 1u) * 2u * nblk + blockIdx.x] = vh_clock();')
         out += [ind + x for x in pre_wait]
         self.pf_open(out, ind, self.dirty)
         out.append(f'{ind}grid_wait(bar, nblk, bk_);')
+        if self.timing:
+            out.append(f'{ind}if (tid == 0 && st_ + 1 == nsteps && bk_ - bk0_ <= {BTRACE}u) '
+                       f'TS[TSB_ + ((bk_ - bk0_ - 1u) * 2u + 1u) * nblk + blockIdx.x] = vh_clock();')
         if self.loops:
             self.loops[-1]['body_barrier'] = True
         self.first_barrier = True
@@ -2690,8 +2699,11 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
            + '\n'.join(pre) + '\n'
            + ''.join(f'  {d}\n' for d in low.shared_decls)
            + ''.join(fb_init)
+           + (f'  const unsigned TSB_ = {len(low.sites)}u * nblk;  // barrier trace after the site table\n'
+              if timing else '')
            + '  for (int st_ = 0; st_ < nsteps; ++st_) {\n'
            + '    const int tid = vh_opaque(tid_k_), lane = tid & 63, wave = tid >> 6;\n'
+           + ('    const unsigned bk0_ = bk_;\n' if timing else '')
            + '\n'.join(head) + '\n'
            + '\n'.join(body) + '\n'
            + ('    if (st_ + 1 < nsteps) grid_sync(bar, nblk, bk_);  // feedback visible to the next step\n'
