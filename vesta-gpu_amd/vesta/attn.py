@@ -30,6 +30,8 @@ import math
 from .stream import PREFETCH_VGPRS
 
 ATTN_PREFETCH_SLOTS = 8      # cache rows per lane issued early (K and V each)
+PROJ_MIN_REPLICAS = 2        # fuse the out-projection only if every leading point gets this many blocks
+PROJ_EARLY_SLOTS = 4         # projection weights issued at the barrier when a lane needs at most this many loads
 
 
 class AttnMixin:
@@ -92,6 +94,140 @@ class AttnMixin:
             return None
         return dict(t=members, c1=c1, c4=c4, S=S, E=E1, E4=E4, nE=nE1, erow=rows[0], lead=list(lead))
 
+    # ------------------------------------------------------------ projection
+    def find_projections(self, ss):
+        """Attention groups that also do the contraction reading their output
+        (the out-projection): see ``proj_of``. The contraction and the
+        statement adding it to a residual are then made by the group's blocks."""
+        for i, s in enumerate(ss):
+            if s[0] == 'step':
+                self.find_projections(s[6])
+                continue
+            if id(s) not in self.groups:
+                continue
+            lead, members = self.groups[id(s)]
+            at = self.attn_of(lead, members)
+            j = i + len(members)
+            if at is None or j + 1 >= len(ss):
+                continue
+            pj = self.proj_of(at, ss[j], ss[j + 1])
+            if pj is None:
+                continue
+            self.proj[id(s)] = pj
+            self.elided |= {id(ss[j]), id(ss[j + 1])}
+            self.elided_vals |= {ss[j][1], members[3][1]}
+            self.fx.add(ss[j + 1][1])
+
+    def proj_of(self, at, so, sz):
+        """The pattern
+
+            oo[P.., d] = fold sum F..: fold sum e: o[L.., e] * W[.., F.. e .., d]
+            z1[P.., d] = BASE + oo[P.., d]          (oo added, nothing else done to it)
+
+        right after attention group ``at`` (output o[L.., e]), where each
+        leading axis of o is a point axis P or a fold axis F of oo, W is an
+        fp16 residue streamed through its transposed copy, and o and oo have no
+        other readers. The blocks of a leading point then multiply its 64-ish
+        outputs by their slice of W (rows of the transposed copy, split over
+        ``R`` replica blocks that each redo the point's attention) and add the
+        products into z1, kept as a 64-bit fixed-point sum (exact, so the order
+        of the adds does not change the result); BASE is stored into z1 in the
+        phase before the attention. Returns the description, or None."""
+        t4 = at['t'][3]
+        o, lead = t4[1], at['lead']
+        if so[0] != 'let' or sz[0] != 'let' or self.place.get(id(so)) != 'tile':
+            return None
+        c = self.info[id(so)]
+        oo, z1 = so[1], sz[1]
+        if c.epi != ('name', '__acc') or c.pt_axes or self.res[c.W][1] != 'f16':
+            return None
+        carries = set(self.alias) | set(self.alias.values())
+        for n in (o, oo, z1):
+            if n in self.outputs or n in carries or self.root(n) != n:
+                return None
+        if self.readers_of.get(o, set()) != {id(so)} or self.readers_of.get(oo, set()) != {id(sz)}:
+            return None
+        A = c.A
+        if A[0] != 'idx' or A[1] != o or any(x[0] != 'name' for x in A[2]):
+            return None
+        names = [x[1] for x in A[2]]
+        fold = list(c.fold_axes)
+        plen = len(lead)
+        if len(names) != plen + 1 or names[-1] != fold[-1] or len(set(names)) != len(names):
+            return None
+        if set(fold) - set(names) or self.static[names[-1]] != at['nE']:
+            return None
+        pmap, fmap = {}, {}
+        for k in range(plen):
+            n = names[k]
+            if self.static.get(n) != self.static[lead[k]]:
+                return None
+            if n in fold:
+                fmap[n] = k
+            elif n in so[2] and n != c.contig:
+                pmap[n] = k
+            else:
+                return None
+        if set(so[2]) != set(pmap) | {c.contig} or list(sz[2]) != list(so[2]):
+            return None
+        target = ('idx', oo, [('name', a) for a in so[2]])
+        if not self._additive(sz[3], target, oo):
+            return None
+        base = self.rebuild_expr(sz[3], lambda n: ('num', 0.0) if n == target else n)
+        if self.reads(base) & {t[1] for t in at['t']}:
+            return None
+        st = self.stream_of(c)
+        if st is None or st.pack is None or st.vec != 8:
+            return None
+        G = self.size(lead)
+        R = self.grid // G
+        if R < PROJ_MIN_REPLICAS:
+            return None
+        # fold position of (F.., e): the flat index over the fold axes, last fastest
+        strides, acc = {}, 1
+        for a in reversed(fold):
+            strides[a] = acc
+            acc *= self.static[a]
+        D = self.static[c.contig]
+        return dict(so=so, sz=sz, c=c, st=st, base=base, pmap=pmap, fmap=fmap, strides=strides,
+                    R=R, D=D, DPR=-(-D // R))
+
+    def _additive(self, e, target, name):
+        """Is e = (something) + target, target read once and only through + and
+        the left side of -?"""
+        hits = [n for n in self.nodes_of(e) if n[0] in ('idx', 'name') and n[1] == name]
+        if hits != [target]:
+            return False
+
+        def walk(x):
+            if x == target:
+                return True
+            if x[0] == 'bin' and x[1] == '+':
+                return walk(x[2]) or walk(x[3])
+            if x[0] == 'bin' and x[1] == '-':
+                return walk(x[2])
+            return False
+        return walk(e)
+
+    def gen_proj_base(self, pj, out, ind):
+        """z1 = BASE at every point, spread over all blocks (a few threads each)."""
+        sz, base = pj['sz'], pj['base']
+        z1, axes = sz[1], list(sz[2])
+        reads = self.root_reads([base])
+        self.sync(reads, {z1}, out, ind, f'{z1} base')
+        self.plan.append((self.show_stmt(sz), 'fixed-point sum: base here, projection adds'))
+        I = ind + '  '
+        out.append(f'{ind}for (int p_ = (int)blockIdx.x + (int)nblk * tid; p_ < {self.count_c(axes)}; '
+                   f'p_ += nthr) {{  // {z1} base')
+        env = self.decode('p_', axes, out, I)
+        pre = []
+        v, t = self.expr(base, env, pre, I)
+        out += pre
+        out.append(f'{I}{self.store(z1, [env[a][0] for a in axes], v, t)}')
+        out.append(f'{ind}}}')
+        self.note(reads, {z1})
+        self.mark(out, ind, f'{z1} base')
+
     def _reads_at(self, e, allowed):
         """Does e read group values only at the given index lists (and no folds)?"""
         for n in self.nodes_of(e):
@@ -104,16 +240,24 @@ class AttnMixin:
         return True
 
     # ------------------------------------------------------------ codegen
-    def gen_attn(self, at, out, ind):
+    def gen_attn(self, at, out, ind, pj=None):
+        """The group's code; with ``pj`` (see ``proj_of``) also the projection
+        of its output, added into a fixed-point sum."""
         t1, t2, t3, t4 = at['t']
         c1, c4, S, lead = at['c1'], at['c4'], at['S'], at['lead']
+        if pj is not None:
+            self.gen_proj_base(pj, out, ind)
         names = {t[1] for t in at['t']}
         local = self.group_local.get(id(t1), [])
         reads = self.root_reads([t[3] for t in at['t']], exclude=names)
         writes = {self.root(t[1]) for t in at['t'] if t[1] not in local}
+        if pj is not None:
+            writes = (writes - {t4[1]}) | {pj['sz'][1]}
         self.sync(reads, writes, out, ind, t1[1])
         for t in at['t']:
             self.plan.append((self.show_stmt(t), f'attention[{", ".join(lead)}]'))
+        if pj is not None:
+            self.plan.append((self.show_stmt(pj['so']), f'attention[{", ".join(lead)}] projection x{pj["R"]}'))
         nE = at['nE']
         LPE = nE // 8                      # lanes per position (16-byte chunks of e)
         PPW = 64 // LPE                    # positions per wave per slot
@@ -123,6 +267,8 @@ class AttnMixin:
         NPS = -(-smax // PPP)
         NPF = min(NPS, ATTN_PREFETCH_SLOTS, PREFETCH_VGPRS // 8)
         G = self.size(lead)
+        R = pj['R'] if pj is not None else 1      # blocks per leading point (each redoes its attention)
+        GR = G * R
         sid = self.fresh('a')
         kq, vq = f'kq_{sid}', f'vq_{sid}'
         T = self.ext_c(S)
@@ -178,13 +324,42 @@ class AttnMixin:
             env = self.decode(gp, lead, lines, '', prefix='al_')
             return lines, env
 
+        if pj is not None:
+            c5, st5 = pj['c'], pj['st']
+            DPR, D = pj['DPR'], pj['D']
+            NQP = -(-DPR // (NW * PPW))               # projection rounds: PPW rows per wave each
+            early = NQP <= PROJ_EARLY_SLOTS
+            wp = f'wp_{sid}'
+            if early:
+                self.decls.append(f'vh_u32x4 {wp}[{NQP}];')
+
+        def proj_loads(lenv, rp):
+            """Lines loading this lane's 8 weights of each projection round
+            (row d of the transposed copy, the point's fold positions)."""
+            lines = []
+            foff = ' + '.join(f'{pj["strides"][a]} * {lenv[lead[k]][0]}' for a, k in pj['fmap'].items()) or '0'
+            rs = self.res_strides(st5.src)
+            for q in range(NQP):
+                lines.append(f'{{ const int dl_ = {q * NW * PPW} + wave * {PPW} + sub_, d_ = {rp} * {DPR} + dl_;')
+                lines.append(f'  if (wave < {NW} && dl_ < {DPR} && d_ < {D}) {{')
+                pre = []
+                ix = [self.index(x, {c5.contig: ('d_', 'int')}, pre, '    ') for x in st5.prefix_idx]
+                lines += pre
+                lines.append(f'    {wp}[{q}] = ldg16_nt({self.rsrc(st5.src)}, (unsigned)({self.addr(ix, rs[:-1])}) + '
+                             f'{st5.c0}u + (unsigned)({foff}) + (unsigned)cl_ * 8u);')
+                lines.append(f'  }} else {wp}[{q}] = vh_u32x4{{0u, 0u, 0u, 0u}};')
+                lines.append('}')
+            return lines
+
         def make(step_override):
             saved = self.override_step(step_override)
             try:
-                ll, lenv = lead_lines('(int)blockIdx.x')
-                lines = [f'if ((int)blockIdx.x < {G}) {{', '  ' + lane_decl] + ['  ' + x for x in ll]
+                ll, lenv = lead_lines(f'((int)blockIdx.x % {G})' if R > 1 else '(int)blockIdx.x')
+                lines = [f'if ((int)blockIdx.x < {GR}) {{', '  ' + lane_decl] + ['  ' + x for x in ll]
                 for k in range(NPF):
                     lines += ['  ' + x for x in load_kv(k, lenv, True)]
+                if pj is not None and early:
+                    lines += ['  ' + x for x in proj_loads(lenv, f'((int)blockIdx.x / {G})')]
                 return lines + ['}']
             finally:
                 self.restore_step(saved)
@@ -192,12 +367,14 @@ class AttnMixin:
 
         o = out
         I = ind + '  '
-        o.append(f'{ind}for (int gp_ = blockIdx.x; gp_ < {G}; gp_ += nblk) {{  // attention {t1[1]}..{t4[1]}: '
-                 f'{LPE} lanes/position, {PPP} positions/slot, {NPS} slots, {NPF} loaded early')
+        o.append(f'{ind}for (int gi_ = blockIdx.x; gi_ < {GR}; gi_ += nblk) {{  // attention {t1[1]}..{t4[1]}: '
+                 f'{LPE} lanes/position, {PPP} positions/slot, {NPS} slots, {NPF} loaded early'
+                 + (f', {R} blocks per point' if R > 1 else ''))
         o.append(f'{I}{lane_decl}')
+        o.append(f'{I}const int gp_ = gi_ % {G}, rp_ = gi_ / {G};' if R > 1 else f'{I}const int gp_ = gi_;')
         ll, lenv = lead_lines('gp_')
         o += [I + x for x in ll]
-        o.append(f'{I}const bool first_ = gp_ == (int)blockIdx.x;')
+        o.append(f'{I}const bool first_ = gi_ == (int)blockIdx.x;')
         # the step's own row (and every row when this is not the block's first point)
         el, ev = erow_c(lenv)
         o += [I + x for x in el]
@@ -209,6 +386,13 @@ class AttnMixin:
                 o.append(f'{I}  {{')
             o += [I + '    ' + x for x in load_kv(k, lenv, False)]
             o.append(f'{I}  }}')
+            o.append(f'{I}}}')
+        if pj is not None and not early:
+            o.append(f'{I}vh_u32x4 {wp}[{NQP}];')
+        elif pj is not None:
+            # a block's later points (none when every point has its own blocks) load here
+            o.append(f'{I}if (!first_) {{')
+            o += [I + '  ' + x for x in proj_loads(lenv, 'rp_')]
             o.append(f'{I}}}')
         self.mark(o, I, 'attention: rows')
         # the query chunk of this lane
@@ -242,6 +426,10 @@ class AttnMixin:
             o.append(f'{I}  mloc_ = fmaxf(mloc_, sk_[{k}]);')
             o.append(f'{I}}}')
         self.mark(o, I, 'attention: scores')
+        if pj is not None and not early:
+            # issued once the keys are dead (their registers take these) and after
+            # the cache rows, so waiting for the values does not wait for these
+            o += [I + x for x in proj_loads(lenv, 'rp_')]
         o.append(f'{I}const float mx_ = block_red_max(mloc_, red_sh);')
         self.mark(o, I, 'attention: max')
         # the softmax denominator: each position once (its lane group's first lane)
@@ -293,12 +481,46 @@ class AttnMixin:
         pre = []
         ov, ot = self.expr(c4.epi, fenv, pre, I + '  ')
         o += pre
-        o.append(f'{I}  {self.store(t4[1], [fenv[a][0] for a in t4[2]], ov, ot)}')
+        po = red_o + NW * nE                       # the point's output, when the projection reads it
+        if pj is None:
+            o.append(f'{I}  {self.store(t4[1], [fenv[a][0] for a in t4[2]], ov, ot)}')
+        else:
+            self.stage_floats = max(self.stage_floats, self.stage_top + NW * nE + nE)
+            o.append(f'{I}  sh_f[{po} + tid] = {self.as_float(ov, ot)};')
         o.append(f'{I}}}')
         o.append(f'{I}vh_lds_sync();')
+        if pj is not None:
+            self.gen_proj_tail(pj, lenv, lead, po, wp, NQP, NW, PPW, LPE, o, I)
         o.append(f'{ind}}}')
         self.note(reads, writes)
         self.mark(out, ind, f'attention {t1[1]}..{t4[1]}')
+
+    def gen_proj_tail(self, pj, lenv, lead, po, wp, NQP, NW, PPW, LPE, o, I):
+        """Each lane group (LPE lanes, 8 outputs each) dots the point's output
+        with one weight row; the group's first lane adds the sum into z1."""
+        so, sz = pj['so'], pj['sz']
+        z1, c5 = sz[1], pj['c']
+        DPR, D = pj['DPR'], pj['D']
+        o.append(f'{I}{{  // {so[1]}: rows [rp_ * {DPR}, +{DPR}) of {pj["st"].src}, added into {z1}')
+        J = I + '  '
+        o.append(f'{J}float ol_[8];')
+        o.append(f'{J}{self.lds_vec_load(8, f"(sh_f + {po} + cl_ * 8)", "ol_")}')
+        zenv = {a: lenv[lead[k]] for a, k in pj['pmap'].items()}
+        zenv[c5.contig] = ('d_', 'int')
+        za = self.addr([zenv[a][0] for a in sz[2]], self.strides(self.axes_of[z1]))
+        for q in range(NQP):
+            o.append(f'{J}{{ const int dl_ = {q * NW * PPW} + wave * {PPW} + sub_, d_ = rp_ * {DPR} + dl_;')
+            o.append(f'{J}  float wf_[8];')
+            o.append(f'{J}  unpack8({wp}[{q}], wf_);')
+            o.append(f'{J}  float a_ = 0.0f;')
+            o.append(f'{J}  #pragma unroll')
+            o.append(f'{J}  for (int v_ = 0; v_ < 8; ++v_) a_ = fmaf(ol_[v_], wf_[v_], a_);')
+            o.append(f'{J}  a_ = group_red_sum(a_, {LPE});')
+            o.append(f'{J}  if (wave < {NW} && cl_ == 0 && dl_ < {DPR} && d_ < {D}) '
+                     f'fxadd(S, {self.g[z1]}u + 2u * (unsigned)({za}), a_);')
+            o.append(f'{J}}}')
+        o.append(f'{I}}}')
+        self.mark(o, I, 'attention: projection')
 
     def _subst(self, e, repl):
         """e with reads of the named group values replaced by C variables:

@@ -231,9 +231,10 @@ __device__ __forceinline__ unsigned ldg4_nt(vh_rsrc r, unsigned i) {
 #define VH_FX_SCALE 4294967296.0
 __device__ __forceinline__ long long vh_f2fx(float v) { return (long long)rint((double)v * VH_FX_SCALE); }
 __device__ __forceinline__ float vh_fx2f(long long q) { return (float)((double)q * (1.0 / VH_FX_SCALE)); }
-__device__ __forceinline__ float fxld(vh_rsrc r, unsigned i) {
-  return vh_fx2f(__builtin_bit_cast(long long, __builtin_amdgcn_raw_buffer_load_b64(r, i * 4u, 0, VH_SC1)));
+__device__ __forceinline__ long long ldfx_raw(vh_rsrc r, unsigned i) {
+  return __builtin_bit_cast(long long, __builtin_amdgcn_raw_buffer_load_b64(r, i * 4u, 0, VH_SC1));
 }
+__device__ __forceinline__ float fxld(vh_rsrc r, unsigned i) { return vh_fx2f(ldfx_raw(r, i)); }
 __device__ __forceinline__ void fxst(vh_rsrc r, unsigned i, float v) {
   __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(vh_u32x2, vh_f2fx(v)), r, i * 4u, 0, VH_SC1);
 }

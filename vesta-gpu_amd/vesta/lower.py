@@ -360,6 +360,10 @@ class Lowering(StreamMixin, AttnMixin):
         self.local_fb = {}            # feedback target -> ('tok', source) | ('inc', k) kept block-local
         self.local_vals = {}          # value -> LDS array every block holds it in (redundant combine)
         self.shared_decls = []        # kernel-scope __shared__ arrays
+        self.proj = {}                # id(first attention statement) -> projection it also does
+        self.fx = set()               # values kept as 64-bit fixed-point sums in global scratch
+        self.elided = set()           # ids of statements another site computes
+        self.elided_vals = set()      # values no site stores
         self.scan(stmts)
         stmts = self.normalise(stmts)
         stmts = self.hoist(stmts)
@@ -367,6 +371,7 @@ class Lowering(StreamMixin, AttnMixin):
         stmts = self.inline(stmts)
         self.stmts = stmts
         self.place_all(stmts)
+        self.find_projections(stmts)
         self.layout(stmts)
 
     # ------------------------------------------------------------ program facts
@@ -932,10 +937,11 @@ class Lowering(StreamMixin, AttnMixin):
         self.g, self.goff = {}, 0
         for n in self.axes_of:
             r = self.root(n)
-            if r in self.private or r in self.g or n in self.inlined:
+            if r in self.private or r in self.g or n in self.inlined or r in self.elided_vals:
                 continue
             self.g[r] = self.goff
-            self.goff += -(-max(1, self.size(self.axes_of[r])) // LINE_WORDS) * LINE_WORDS
+            words = max(1, self.size(self.axes_of[r])) * (2 if r in self.fx else 1)
+            self.goff += -(-words // LINE_WORDS) * LINE_WORDS
         self.counters = BAR_WORDS
         self.staged = {}
         self.glocal = {}
@@ -1177,6 +1183,9 @@ class Lowering(StreamMixin, AttnMixin):
         if r in self.glocal:
             off, plen = self.glocal[r]
             return f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}]'
+        if r in self.fx:
+            i = f'{self.g[r]} + 2u * ({a})'
+            return self.captured(f'fxld(rb_S, {i})', 'float', r, raw=(f'ldfx_raw(rb_S, {i})', 'long long', 'vh_fx2f'))
         return self.captured(f'ldcs(rb_S, {self.g[r]} + {a})', 'float', r)
 
     def store(self, n, ix, v, t):
@@ -1187,6 +1196,8 @@ class Lowering(StreamMixin, AttnMixin):
         if r in self.glocal:
             off, plen = self.glocal[r]
             return f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}] = {self.as_float(v, t)};'
+        if r in self.fx:
+            return f'fxst(rb_S, {self.g[r]} + 2u * ({a}), {self.as_float(v, t)});'
         return f'stcs(rb_S, {self.g[r]} + {a}, {self.as_float(v, t)});'
 
     def decode(self, var, axes, out, ind, prefix='i_'):
@@ -1285,11 +1296,14 @@ class Lowering(StreamMixin, AttnMixin):
                 self.gen_emit(s, out, ind)
                 i += 1
                 continue
+            if id(s) in self.elided:
+                i += 1
+                continue
             if id(s) in self.groups:
                 lead, members = self.groups[id(s)]
                 at = self.attn_of(lead, members)
                 if at is not None:
-                    self.gen_attn(at, out, ind)
+                    self.gen_attn(at, out, ind, self.proj.get(id(s)))
                 else:
                     self.gen_group(lead, members, out, ind)
                 i += len(members)
@@ -1925,7 +1939,8 @@ class Lowering(StreamMixin, AttnMixin):
                 size = self.size(self.axes_of[r])
                 if off - base + size <= STAGE_MAX:
                     staged[r] = off
-                    out.append(f'{ind}stage_ldc4(sh_f + {off}, rb_S, {self.g[r]}, {size});  // stage {r}')
+                    fn = 'stage_fx' if r in self.fx else 'stage_ldc4'
+                    out.append(f'{ind}{fn}(sh_f + {off}, rb_S, {self.g[r]}, {size});  // stage {r}')
                     off += -(-size // 4) * 4
         self.stage_floats = max(self.stage_floats, off - base)
         if staged:
@@ -2578,6 +2593,8 @@ class Lowering(StreamMixin, AttnMixin):
                 if src not in self.axes_of:
                     raise NameError(f'feedback source {src} is not a value of the program')
                 r = self.root(src)
+                if r in self.fx:
+                    raise LowerError(f'feedback source {src} is a fixed-point sum')
                 n = self.size(self.axes_of[r])
                 if math.prod(self.res[dst][0]) != n:
                     raise LowerError(f'feedback {dst} <- {src}: {math.prod(self.res[dst][0])} vs {n} elements')
@@ -2716,7 +2733,7 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
     scratch = {}
     for n in low.axes_of:
         r = low.root(n)
-        if r in low.g:
+        if r in low.g and r not in low.fx:
             axes = low.axes_of[n]
             scratch[n] = (low.g[r], axes, tuple(low.static[a] for a in axes))
     return Lowered(src, params, scratch, low.goff, (low.lds_floats + low.stage_floats) * 4, low.barriers,

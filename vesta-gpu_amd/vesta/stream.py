@@ -443,7 +443,8 @@ class StreamMixin:
         o.append(f'{I}vh_lds_sync();')
         want = list(reg) + list(c.fold_axes)
         if (A[0] == 'idx' and A[1] in self.axes_of and self.root(A[1]) in self.g
-                and self.root(A[1]) not in self.private and list(self.axes_of[self.root(A[1])]) == want
+                and self.root(A[1]) not in self.private and self.root(A[1]) not in self.fx
+                and list(self.axes_of[self.root(A[1])]) == want
                 and list(A[2]) == [('name', a) for a in want] and K % 4 == 0):
             rows = min(rch, R - rc * rch)
             off = self.g[self.root(A[1])] + rc * rch * K
