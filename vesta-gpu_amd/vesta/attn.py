@@ -367,14 +367,19 @@ class AttnMixin:
 
         o = out
         I = ind + '  '
-        o.append(f'{ind}for (int gi_ = blockIdx.x; gi_ < {GR}; gi_ += nblk) {{  // attention {t1[1]}..{t4[1]}: '
+        # one point per block when there are blocks enough: then every block's
+        # point is its first, whose rows were loaded early
+        once = GR <= self.grid
+        head = (f'{{ const int gi_ = blockIdx.x; if (gi_ < {GR}) {{' if once else
+                f'for (int gi_ = blockIdx.x; gi_ < {GR}; gi_ += nblk) {{')
+        o.append(f'{ind}{head}  // attention {t1[1]}..{t4[1]}: '
                  f'{LPE} lanes/position, {PPP} positions/slot, {NPS} slots, {NPF} loaded early'
                  + (f', {R} blocks per point' if R > 1 else ''))
         o.append(f'{I}{lane_decl}')
         o.append(f'{I}const int gp_ = gi_ % {G}, rp_ = gi_ / {G};' if R > 1 else f'{I}const int gp_ = gi_;')
         ll, lenv = lead_lines('gp_')
         o += [I + x for x in ll]
-        o.append(f'{I}const bool first_ = gi_ == (int)blockIdx.x;')
+        o.append(f'{I}const bool first_ = ' + ('true;' if once else 'gi_ == (int)blockIdx.x;'))
         # the step's own row (and every row when this is not the block's first point)
         el, ev = erow_c(lenv)
         o += [I + x for x in el]
@@ -491,7 +496,7 @@ class AttnMixin:
         o.append(f'{I}vh_lds_sync();')
         if pj is not None:
             self.gen_proj_tail(pj, lenv, lead, po, wp, NQP, NW, PPW, LPE, o, I)
-        o.append(f'{ind}}}')
+        o.append(f'{ind}}}' + ('}' if once else ''))
         self.note(reads, writes)
         self.mark(out, ind, f'attention {t1[1]}..{t4[1]}')
 

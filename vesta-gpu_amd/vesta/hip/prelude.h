@@ -224,6 +224,15 @@ __device__ __forceinline__ unsigned ldg4_nt(vh_rsrc r, unsigned i) {
   return __builtin_amdgcn_raw_buffer_load_b32(r, i * 2u, 0, VH_NT);
 }
 
+// x / d from r = 1 / d (both correctly rounded): q = x * r is within an ulp
+// of the quotient, and one residual step (exact through the fma) rounds it
+// correctly (Markstein), so the result is the IEEE quotient for finite
+// nonzero d and a quotient that neither overflows nor underflows.
+__device__ __forceinline__ float vh_divr(float x, float d, float r) {
+  const float q = x * r;
+  return fmaf(fmaf(-q, d, x), r, q);
+}
+
 // Fixed-point accumulators: fp32 values summed exactly as 64-bit integers in
 // units of 2^-32 (any order of atomic adds gives the same bits), read back as
 // fp32. Element i of such a buffer is the 8 bytes at float index i of global

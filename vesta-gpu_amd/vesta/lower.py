@@ -85,6 +85,7 @@ LANE_MIN = 32                 # lane-split a fold only if it is at least this lo
 GRIDRED_MIN = 1 << 14         # grid reduction for a fold at least this long into few points
 GRIDRED_POINTS = 8
 REPL_MAX = 1 << 14            # points a replicated (every-block) statement may have
+PRIV_GROUP = 8                # elementwise private: leading points whose reads are issued together
 BTRACE = 96                   # timing: barriers of the last step traced per block
 UNROLL = 8                    # rows (tile) / vectors (lane) whose loads are issued together
 TILE_LANES = 8                # tile: lanes per row (8 x 16 bytes = one 128-byte line of a weight row)
@@ -356,6 +357,9 @@ class Lowering(StreamMixin, AttnMixin):
         self.stage_top = 0
         self.capture = None
         self.in_fold = False          # generating the body of a fold
+        self.divr = {}                # shown divisor -> (value, reciprocal) C expressions
+        self.invs = {}                # shown subexpression -> C expression of its value
+        self.lcap = None              # LDS reads being collected into registers
         self.stream_part = {}         # value -> how a stream site split its points over blocks
         self.local_fb = {}            # feedback target -> ('tok', source) | ('inc', k) kept block-local
         self.local_vals = {}          # value -> LDS array every block holds it in (redundant combine)
@@ -974,6 +978,10 @@ class Lowering(StreamMixin, AttnMixin):
         """C code of e as (text, type); type is 'int', 'float' or 'bool'.
         Folds inside e become serial loops appended to ``out``."""
         k = e[0]
+        if self.invs and k in ('call', 'bin'):
+            got = self.invs.get(show(e))
+            if got is not None:
+                return got, 'float'
         if k == 'num':
             v = e[1]
             if isinstance(v, int) and not isinstance(v, bool):
@@ -1008,17 +1016,24 @@ class Lowering(StreamMixin, AttnMixin):
         if k == 'bin':
             op = e[1]
             a, ta = self.expr(e[2], env, out, ind)
+            if op == '/' and self.divr and show(e[3]) in self.divr:
+                # a divisor that does not vary over the points being made:
+                # its value and reciprocal were computed once
+                dv, rv = self.divr[show(e[3])]
+                return f'vh_divr({self.as_float(a, ta)}, {dv}, {rv})', 'float'
             b, tb = self.expr(e[3], env, out, ind)
             if op in ('==', '<', '>', '<=', '>='):
                 if ta == 'int' and tb == 'int':
                     return f'({a} {op} {b})', 'bool'
                 return f'({self.as_float(a, ta)} {op} {self.as_float(b, tb)})', 'bool'
             if op == '/':
-                if self.in_fold and e[3][0] == 'num' and float(e[3][1]) != 0.0:
-                    # a term of a fold (whose summation order is not NumPy's
-                    # anyway): divide by a constant as a multiply by its
-                    # correctly rounded reciprocal (within 1.5 ulp of the quotient)
-                    return f'({self.as_float(a, ta)} * {c_float(np.float32(1.0) / np.float32(e[3][1]))})', 'float'
+                if e[3][0] == 'num' and np.isfinite(np.float32(e[3][1])) and np.float32(e[3][1]) != 0:
+                    c = np.float32(e[3][1])
+                    r = np.float32(1.0) / c
+                    if np.frexp(c)[0] in (0.5, -0.5):
+                        # a power of two: the reciprocal is exact
+                        return f'({self.as_float(a, ta)} * {c_float(r)})', 'float'
+                    return f'vh_divr({self.as_float(a, ta)}, {c_float(c)}, {c_float(r)})', 'float'
                 return f'({self.as_float(a, ta)} / {self.as_float(b, tb)})', 'float'
             if ta == 'int' and tb == 'int':
                 return f'({a} {op} {b})', 'int'
@@ -1065,7 +1080,11 @@ class Lowering(StreamMixin, AttnMixin):
             out.append(f'{ind}#pragma unroll 8')
             out.append(f'{ind}for (int {kv} = 0; {kv} < {self.ext_c(ax)}; ++{kv}) {{')
             inner = []
-            v, t = self.expr(body, {**env, ax: (kv, 'int')}, inner, ind + '  ')
+            saved, self.lcap = self.lcap, None       # reads in the loop stay in the loop
+            try:
+                v, t = self.expr(body, {**env, ax: (kv, 'int')}, inner, ind + '  ')
+            finally:
+                self.lcap = saved
             out += inner
             out.append(f'{ind}  {acc} = {FOLD_OP[op]}({acc}, {self.as_float(v, t)});')
             out.append(f'{ind}}}')
@@ -1177,12 +1196,12 @@ class Lowering(StreamMixin, AttnMixin):
         r = self.root(n)
         a = self.addr(ix, self.strides(self.axes_of[r]))
         if r in self.private:
-            return f'sh_f[{self.lds[r]} + {a}]'
+            return self.lds_read(f'sh_f[{self.lds[r]} + {a}]')
         if r in self.staged:
-            return f'sh_f[{self.staged[r]} + {a}]'
+            return self.lds_read(f'sh_f[{self.staged[r]} + {a}]')
         if r in self.glocal:
             off, plen = self.glocal[r]
-            return f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}]'
+            return self.lds_read(f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}]')
         if r in self.fx:
             i = f'{self.g[r]} + 2u * ({a})'
             return self.captured(f'fxld(rb_S, {i})', 'float', r, raw=(f'ldfx_raw(rb_S, {i})', 'long long', 'vh_fx2f'))
@@ -1943,6 +1962,7 @@ class Lowering(StreamMixin, AttnMixin):
                     out.append(f'{ind}{fn}(sh_f + {off}, rb_S, {self.g[r]}, {size});  // stage {r}')
                     off += -(-size // 4) * 4
         self.stage_floats = max(self.stage_floats, off - base)
+        self.priv_stage_end = off - base
         if staged:
             out.append(f'{ind}vh_lds_sync();')
             self.mark(out, ind, f'stage {",".join(staged)}')
@@ -2006,7 +2026,10 @@ class Lowering(StreamMixin, AttnMixin):
         nlead = self.size(lead)
         sid = self.fresh('p')
         unsafe = self.unsafe_early()
-        lead_vars = [f'i_{a}' for a in lead] + ['pl_']
+        # leading points made together: all their LDS reads are issued before
+        # any of their stores (a store to LDS keeps later reads behind it)
+        LG = max(g for g in range(1, min(nlead, PRIV_GROUP) + 1) if nlead % g == 0)
+        lead_vars = [f'i_{a}' for a in lead] + ['pl_', 'pg_'] + [f'i{u}_{a}' for u in range(LG) for a in lead]
 
         def body_env():
             env = {last: (f'i_{last}', 'int')}
@@ -2055,17 +2078,122 @@ class Lowering(StreamMixin, AttnMixin):
                 seen.add(n)
                 self.decls.append(f'{self.cap_ctype(k)} {n};')
         o.append(f'{ind}// private {name}')
+        hv = self.hoist_invariants(e, lead, nlead, o, ind)
         for jl in range(TJ):
             self.capture = {'prefix': f'pp_{sid}_{jl}_', 'loads': [], 'unsafe': unsafe, 'dedupe': {},
                             'forbid': lead_vars}
             try:
-                env = body_env()
-                pre = []
-                v, t = self.expr(e, env, pre, '')
-                inner = pre + [self.store(name, [env[a][0] for a in axes], v, t)]
-                o += [ind + x for x in frame(jl, inner, True)]
+                decl, loads, comp = [], [], []
+                for u in range(LG):
+                    pl = f'(pg_ + {u})' if lead else '0'
+                    env = {last: (f'i_{last}', 'int')}
+                    if lead:
+                        env.update(self.decode(pl, lead, decl, '', prefix=f'i{u}_'))
+                    self.lcap = {'prefix': f'lv{u}_', 'loads': [], 'dedupe': {}}
+                    self.bind_invariants(hv, pl)
+                    pre = []
+                    v, t = self.expr(e, env, pre, '')
+                    loads += [f'const float {n} = {x};' for n, x in self.lcap['loads']]
+                    self.lcap = None
+                    comp += pre + [self.store(name, [env[a][0] for a in axes], v, t)]
+                inner = decl + loads + comp
+                if lead and LG < nlead:
+                    inner = ([f'for (int pg_ = 0; pg_ < {nlead}; pg_ += {LG}) {{']
+                             + ['  ' + x for x in inner] + ['}'])
+                elif lead:
+                    inner = ['{ const int pg_ = 0;'] + ['  ' + x for x in inner] + ['}']
+                o += [ind + x for x in frame(jl, inner, False)]
             finally:
                 self.capture = None
+                self.lcap = None
+        self.invs, self.divr = {}, {}
+
+    def lead_invariants(self, e, lead):
+        """Subexpressions of e (outside folds) that depend on no axis but the
+        leading ones (and step variables) and cost a call or a division:
+        [(node, is a divisor)], each once."""
+        allowed = set(lead) | self.steps
+        found, seen = [], set()
+
+        def inv(n):
+            return (n[0] != 'num' and self.free_axes(n) <= allowed
+                    and not any(x[0] == 'fold' for x in nodes(n)))
+
+        def walk(n):
+            if not is_node(n) or n[0] == 'fold':
+                return
+            if n[0] == 'bin' and n[1] == '/' and n[3][0] != 'num' and inv(n[3]):
+                if show(n[3]) not in seen:
+                    seen.add(show(n[3]))
+                    found.append((n[3], True))
+                walk(n[2])
+                return
+            if n[0] == 'call' and inv(n):
+                if show(n) not in seen:
+                    seen.add(show(n))
+                    found.append((n, False))
+                return
+            for x in n[1:]:
+                for y in (x if isinstance(x, list) else [x]):
+                    walk(y)
+        walk(e)
+        return found
+
+    def hoist_invariants(self, e, lead, nlead, o, ind):
+        """Values of e's lead-invariant calls and divisors, once per leading
+        point (thread p makes point p) into LDS: [(node, LDS offset, offset of
+        the reciprocal or None)]; ``bind_invariants`` then makes the code for
+        e's points read them, and divide by such a divisor through its
+        reciprocal with the exact residual step."""
+        invs = self.lead_invariants(e, lead) if nlead <= self.BLOCK else []
+        if not invs:
+            return []
+        base = self.lds_floats + self.priv_stage_end
+        I = ind + '  '
+        o.append(f'{ind}if (tid < {nlead}) {{  // once per leading point')
+        env = self.decode('tid', lead, o, I, prefix='ip_')
+        k, hv = 0, []
+        for node, is_div in invs:
+            pre = []
+            v, t = self.expr(node, env, pre, I)
+            o += pre
+            o.append(f'{I}{{ const float iv_ = {self.as_float(v, t)};')
+            o.append(f'{I}  sh_f[{base + k * nlead} + tid] = iv_;')
+            if is_div:
+                o.append(f'{I}  sh_f[{base + (k + 1) * nlead} + tid] = 1.0f / iv_;')
+                hv.append((node, base + k * nlead, base + (k + 1) * nlead))
+                k += 2
+            else:
+                hv.append((node, base + k * nlead, None))
+                k += 1
+            o.append(f'{I}}}')
+        o.append(f'{ind}}}')
+        o.append(f'{ind}vh_lds_sync();')
+        self.stage_floats = max(self.stage_floats, self.priv_stage_end + k * nlead)
+        return hv
+
+    def bind_invariants(self, hv, pl):
+        """The hoisted values of leading point ``pl`` (a C expression)."""
+        self.invs, self.divr = {}, {}
+        for node, off, roff in hv:
+            val = self.lds_read(f'sh_f[{off} + {pl}]')
+            if roff is None:
+                self.invs[show(node)] = val
+            else:
+                self.divr[show(node)] = (val, self.lds_read(f'sh_f[{roff} + {pl}]'))
+
+    def lds_read(self, text):
+        """An LDS read; while ``self.lcap`` collects them, a register it names
+        (loaded before the statements that use it)."""
+        cap = self.lcap
+        if cap is None:
+            return text
+        got = cap['dedupe'].get(text)
+        if got is None:
+            got = f"{cap['prefix']}{len(cap['loads'])}"
+            cap['loads'].append((got, text))
+            cap['dedupe'][text] = got
+        return got
 
     @staticmethod
     def cap_ctype(kind):

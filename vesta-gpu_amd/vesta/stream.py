@@ -106,13 +106,15 @@ class StreamMixin:
     def prefetch_target(self):
         """Where code issued early for the next site goes: ('slot', k) for the
         latest barrier of this loop body, ('loop', k) for the barrier before
-        the loop (plus the end of the previous iteration), or None (in place)."""
+        the loop (plus the end of the previous iteration), ('top', None) when
+        the loop has no barrier before it (in place in the first iteration,
+        plus the end of the previous one), or None (in place)."""
         k = self.last_pf
         if k is not None and self.pf_slots[k]['loop'] == self.loop_id():
             return 'slot', k
         lp = self.loops[-1] if self.loops else None
-        if lp is not None and k is not None and k == lp['pf_before'] and not lp['body_barrier']:
-            return 'loop', k
+        if lp is not None and k == lp['pf_before'] and not lp['body_barrier']:
+            return ('loop', k) if k is not None else ('top', None)
         return None
 
     def unsafe_early(self):
@@ -121,8 +123,9 @@ class StreamMixin:
         tgt = self.prefetch_target()
         bad = set(self.dirty)
         if tgt is not None:
-            bad |= self.pf_slots[tgt[1]]['dirty']
-            if tgt[0] == 'loop':
+            if tgt[1] is not None:
+                bad |= self.pf_slots[tgt[1]]['dirty']
+            if tgt[0] in ('loop', 'top'):
                 bad |= self.loops[-1]['end_dirty']
         return bad
 
@@ -139,8 +142,13 @@ class StreamMixin:
             self.pf_slots[k]['lines'] += make(None)
             return
         lp = self.loops[-1]
-        self.pf_slots[k]['lines'] += make(('0', 'int'))
         lv, n = lp['lv'], lp['n']
+        if kind == 'loop':
+            self.pf_slots[k]['lines'] += make(('0', 'int'))
+        else:
+            out.append(f'{ind}if ({lv} == 0) {{')
+            out += [ind + '  ' + x for x in make(('0', 'int'))]
+            out.append(f'{ind}}}')
         nxt = make((f'({lv} + 1)', 'int'))
         lp['end_prefetch'] += [f'if ({lv} + 1 < {n}) {{'] + ['  ' + x for x in nxt] + ['}']
 
