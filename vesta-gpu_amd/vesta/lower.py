@@ -360,6 +360,9 @@ class Lowering(StreamMixin, AttnMixin):
         self.divr = {}                # shown divisor -> (value, reciprocal) C expressions
         self.invs = {}                # shown subexpression -> C expression of its value
         self.lcap = None              # LDS reads being collected into registers
+        self.skip_store = set()       # epilogue values no other statement reads
+        self.out_stage = {}           # epilogue value -> (LDS base, points/block, reg axes, point axes)
+        self.stream_lds = {}          # value -> (LDS base, points/block, rows) of the site just made
         self.stream_part = {}         # value -> how a stream site split its points over blocks
         self.local_fb = {}            # feedback target -> ('tok', source) | ('inc', k) kept block-local
         self.local_vals = {}          # value -> LDS array every block holds it in (redundant combine)
@@ -1307,6 +1310,8 @@ class Lowering(StreamMixin, AttnMixin):
             if k in ('axis', 'recv', 'ret'):
                 i += 1
                 continue
+            if self.place.get(id(s)) != 'argmax':
+                self.stream_lds = {}      # the LDS copy of a stream's values lasts until its next site
             if k == 'step':
                 self.gen_step(s, out, ind)
                 i += 1
@@ -1475,8 +1480,9 @@ class Lowering(StreamMixin, AttnMixin):
         v, t = self.expr(c.epi, venv, out, ind)
         cur = self.fresh('v')
         out.append(f'{ind}const float {cur} = {self.as_float(v, t)};')
-        ix = [env[a][0] for a in axes]
-        out.append(f'{ind}{self.store(name, ix, cur, "float")}')
+        st_line = self.epi_store(name, axes, env, cur)
+        if st_line:
+            out.append(f'{ind}{st_line}')
         made = {name: cur}
         for kind, t_, inv in fused:
             if kind == 'let':
@@ -1491,12 +1497,28 @@ class Lowering(StreamMixin, AttnMixin):
                 v2, t2 = self.expr(e2, fenv, out, ind)
                 nv = self.fresh('v')
                 out.append(f'{ind}const float {nv} = {self.as_float(v2, t2)};')
-                out.append(f'{ind}{self.store(t_[1], [env[a][0] for a in t_[2]], nv, "float")}')
+                st_line = self.epi_store(t_[1], list(t_[2]), env, nv)
+                if st_line:
+                    out.append(f'{ind}{st_line}')
                 made[t_[1]] = nv
             else:
                 saved_cap, self.capture = self.capture, None
                 self.epilogue_emit(t_, inv, env, made, out, ind)
                 self.capture = saved_cap
+
+    def epi_store(self, name, axes, env, cur):
+        """The store of an epilogue value at the point bound in env: none when
+        only statements of the same epilogue read it; into the block's LDS
+        copy when its site writes it out afterwards (``out_stage``)."""
+        if name in self.skip_store:
+            return None
+        os_ = self.out_stage.get(name)
+        if os_ is not None:
+            base, PPB, reg, pts = os_
+            row = self.addr([env[a][0] for a in reg], self.strides(reg)) if reg else '0'
+            pt = self.addr([env[a][0] for a in pts], self.strides(pts))
+            return f'sh_f[{base} + ({row}) * {PPB} + ({pt}) - (int)blockIdx.x * {PPB}] = {cur};'
+        return self.store(name, [env[a][0] for a in axes], cur, 'float')
 
     def epilogue_emit(self, t_, inv, env, made, out, ind):
         if True:
@@ -2452,10 +2474,12 @@ class Lowering(StreamMixin, AttnMixin):
             if (pp and pp['pts'] == [ax] and pp['reg'] == axes and src in self.dirty
                     and list(body[2]) == [('name', a) for a in axes + [ax]]):
                 part = pp
+        in_lds = self.stream_lds.get(src) if part else None
         if part:
             self.sync(reads - {src}, writes, out, ind, name)
             self.readers.add(src)
-            out.append(f'{ind}block_sync();  // this block\'s own points of {body[1]}')
+            if in_lds is None:
+                out.append(f'{ind}block_sync();  // this block\'s own points of {body[1]}')
         else:
             self.sync(reads, writes, out, ind, name)
         self.plan.append((show_stmt(s1), 'argmax' + (' (own points)' if part else ' (grid-strided)')))
@@ -2480,7 +2504,11 @@ class Lowering(StreamMixin, AttnMixin):
             else:
                 o.append(f'{I}  for (int k_ = gtid; k_ < {self.static[ax]}; k_ += nthr) {{')
             pre = []
-            v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '    ')
+            if in_lds is not None:
+                # the block's copy in LDS, laid out [row][own point]
+                v, t = f'sh_f[{in_lds[0]} + {p * in_lds[1]} + k_ - k0_]', 'float'
+            else:
+                v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '    ')
             o += pre
             o.append(f'{I}    const float v_ = {self.as_float(v, t)};')
             o.append(f'{I}    if (v_ > bv_ || (v_ == bv_ && k_ < bi_)) {{ bv_ = v_; bi_ = k_; }}')

@@ -30,6 +30,9 @@ from dataclasses import dataclass
 
 PREFETCH_VGPRS = 64          # registers per lane one site may hold prefetched weights in
 PI_STREAM = 4                # slots whose loads are issued together when not prefetched
+PB_MAX = 4                   # points one lane group makes at once (each LDS read of the other factor serves them all)
+PB_ACC = 32                  # ... holding at most this many partial sums per lane
+STAGE_OUT_MAX = 8192         # floats of a stream's values a block collects in LDS before writing them out
 
 
 @dataclass
@@ -177,21 +180,27 @@ class StreamMixin:
         P = self.size(st.pts)
         NB = self.grid
         PPB = -(-P // NB)
-        NQ = -(-PPB // (NW * ppw))
         reg = c.reg_axes
         R = self.size(reg)
         rch = min(R, self.REG_MAX)
         nrch = -(-R // rch)
         ltype = self.load_type(dt, vec)
-        vregs = NQ * pl * max(1, vec * esz // 4)
+        vregs = -(-PPB // (NW * ppw)) * pl * max(1, vec * esz // 4)
         prefetch = vregs <= PREFETCH_VGPRS
+        # a long stream with several rows: a lane group makes PB points at once,
+        # so each value of the other factor read from LDS serves PB weight
+        # vectors (a short one keeps every wave busy instead)
+        PB = 1 if rch < 4 or prefetch else max(1, min(PB_MAX, PPB, PB_ACC // rch))
+        NQ = -(-PPB // (NW * ppw * PB))
         sid = self.fresh('s')
         wq = f'wq_{sid}'
         I = ind + '  '
         o = out
 
+        geo = dict(P=P, PPB=PPB, NW=NW, ppw=ppw, lpp=lpp, rch=rch, reg=reg, PB=PB)
+
         def load_lines(q_c, dst, step_override):
-            """Lines loading slot q_c's vectors into dst[m] (m < pl)."""
+            """Lines loading slot q_c's vectors into dst[j][m] (j < PB, m < pl)."""
             lines = []
             saved = None
             if step_override is not None:
@@ -199,29 +208,31 @@ class StreamMixin:
                 for v in list(self.step_env):
                     if self.loops and v == self.loops[-1]['var']:
                         self.step_env[v] = step_override
-            p_c, ok_c = self.slot_point(dict(NW=NW, ppw=ppw, PPB=PPB), q_c)
-            lines.append(f'{{ const int p_ = {p_c};')
-            lines.append(f'  if ({ok_c} && p_ < {P}) {{')
-            env = self.decode('p_', st.pts, lines, '    ', prefix='sp_')
-            pre = []
-            ix = [self.index(x, env, pre, '    ') for x in st.prefix_idx]
-            lines += pre
-            rs = self.res_strides(st.src)
-            base = self.addr(ix, rs[:-1]) if ix else '0'
-            lines.append(f'    const unsigned wr_ = (unsigned)({base}) + {st.c0}u;')
-            lines.append('    #pragma unroll')
-            lines.append(f'    for (int m_ = 0; m_ < {pl}; ++m_) {{')
-            lines.append(f'      const int kv_ = cl_ + m_ * {lpp};')
-            cond = '' if exact else f'if (kv_ < {nv}) '
-            lines.append(f'      {cond}{dst}[m_] = {self.nt_load(dt, vec, self.rsrc(st.src), "wr_ + kv_ * %d" % vec)};')
-            if not exact:
-                lines.append(f'      else {dst}[m_] = {self.vec_zero(dt, vec)};')
-            lines.append('    }')
-            lines.append('  } else {')
-            lines.append('    #pragma unroll')
-            lines.append(f'    for (int m_ = 0; m_ < {pl}; ++m_) {dst}[m_] = {self.vec_zero(dt, vec)};')
-            lines.append('  }')
-            lines.append('}')
+            for j in range(PB):
+                p_c, ok_c = self.slot_point(geo, q_c, j)
+                lines.append(f'{{ const int p_ = {p_c};')
+                lines.append(f'  if ({ok_c} && p_ < {P}) {{')
+                env = self.decode('p_', st.pts, lines, '    ', prefix='sp_')
+                pre = []
+                ix = [self.index(x, env, pre, '    ') for x in st.prefix_idx]
+                lines += pre
+                rs = self.res_strides(st.src)
+                base = self.addr(ix, rs[:-1]) if ix else '0'
+                lines.append(f'    const unsigned wr_ = (unsigned)({base}) + {st.c0}u;')
+                lines.append('    #pragma unroll')
+                lines.append(f'    for (int m_ = 0; m_ < {pl}; ++m_) {{')
+                lines.append(f'      const int kv_ = cl_ + m_ * {lpp};')
+                cond = '' if exact else f'if (kv_ < {nv}) '
+                lines.append(f'      {cond}{dst}[{j}][m_] = '
+                             f'{self.nt_load(dt, vec, self.rsrc(st.src), "wr_ + kv_ * %d" % vec)};')
+                if not exact:
+                    lines.append(f'      else {dst}[{j}][m_] = {self.vec_zero(dt, vec)};')
+                lines.append('    }')
+                lines.append('  } else {')
+                lines.append('    #pragma unroll')
+                lines.append(f'    for (int m_ = 0; m_ < {pl}; ++m_) {dst}[{j}][m_] = {self.vec_zero(dt, vec)};')
+                lines.append('  }')
+                lines.append('}')
             if saved is not None:
                 self.step_env.clear()
                 self.step_env.update(saved)
@@ -229,10 +240,9 @@ class StreamMixin:
 
         lane_decl = [f'const int sub_ = lane / {lpp}, cl_ = lane % {lpp};']
         rows_of = [min(rch, R - rc * rch) for rc in range(nrch)]
-        geo = dict(P=P, PPB=PPB, NW=NW, ppw=ppw, lpp=lpp, rch=rch, reg=reg)
         self.geo_nw = NW
         if prefetch:
-            self.decls.append(f'{ltype} {wq}[{NQ}][{pl}];')
+            self.decls.append(f'{ltype} {wq}[{NQ}][{PB}][{pl}];')
             unsafe = self.unsafe_early()
             caps = {}
 
@@ -245,7 +255,7 @@ class StreamMixin:
                 saved = self.override_step(step_override)
                 for rc in range(nrch):
                     for q in range(NQ):
-                        for j in range(-(-rows_of[rc] // lpp)):
+                        for j in range(-(-(rows_of[rc] * PB) // lpp)):
                             pre = f'pf_{sid}_{q}_{rc}_{j}_'
                             loads = self.epi_loads(s, c, st, fused, geo, str(q), rc, j, rows_of[rc], pre, unsafe)
                             caps[pre] = [(n, k) for n, _, k in loads]
@@ -259,13 +269,29 @@ class StreamMixin:
                 for n, k in regs:
                     self.decls.append(f'{self.cap_ctype(k)} {n};')
         o.append(f'{ind}{{  // stream {name}: {P} points x {K} from {st.src}, VEC={vec} lanes/point={lpp} '
-                 f'points/block={PPB} rows={R}{" prefetched" if prefetch else ""}')
+                 f'points/block={PPB} rows={R} points/lane group={PB}{" prefetched" if prefetch else ""}')
         for x in lane_decl:
             o.append(f'{I}{x}')
         # which block made which points (an argmax over them can stay in the block)
         self.stream_part[self.root(name)] = dict(pts=list(st.pts), PPB=PPB, P=P, reg=list(reg))
         # the other factor, as floats in LDS laid out [row, fold]
         direct = self.direct_lds(c, reg)
+        # values of the site: not stored when only its own epilogue reads them;
+        # with several rows (or an argmax reading them next), collected in LDS
+        # [row][own point] and written out row by row afterwards
+        fused_ids = {id(t) for _, t, _ in fused}
+        made = [s] + [t for kind, t, _ in fused if kind == 'let']
+        self.skip_store = {t[1] for t in made if self.epi_only(t[1], fused_ids)}
+        self.out_stage = {}
+        obase = self.lds_floats + self.stage_top + (0 if direct is not None else rch * K)
+        otop = obase
+        for t in made:
+            n = t[1]
+            if n in self.skip_store or not self.stage_out_ok(t, reg, st.pts, R, PPB):
+                continue
+            self.out_stage[n] = (otop, PPB, list(reg), list(st.pts))
+            otop += -(-R * PPB // 4) * 4
+        self.stage_floats = max(self.stage_floats, otop - self.lds_floats)
         for rc in range(nrch):
             if direct is not None:
                 abase = f'{direct} + {rc * rch * K}'
@@ -277,9 +303,42 @@ class StreamMixin:
             qs = [str(q) for q in range(NQ)] if prefetch else None
             self.stream_body(s, c, st, fused, o, I, rc, rch, R, K, abase, dt, vec, nv, lpp, pl, exact,
                              NQ, qs, wq, ltype, geo, load_lines, sid, unsafe if prefetch else None)
+        if self.out_stage:
+            o.append(f'{I}vh_lds_sync();')
+            o.append(f'{I}{{ const int p0_ = (int)blockIdx.x * {PPB};')
+            o.append(f'{I}  for (int e_ = tid; e_ < {R * PPB}; e_ += {self.BLOCK}) {{')
+            o.append(f'{I}    const int r_ = e_ / {PPB}, i_ = e_ - r_ * {PPB};')
+            o.append(f'{I}    if (p0_ + i_ < {P}) {{')
+            for n, (base, _, _, _) in self.out_stage.items():
+                o.append(f'{I}      stcs(rb_S, {self.g[self.root(n)]} + r_ * {P} + p0_ + i_, sh_f[{base} + e_]);')
+            o.append(f'{I}    }}')
+            o.append(f'{I}  }}')
+            o.append(f'{I}}}')
+            self.mark(o, I, f'stream {name}: write out')
+        self.stream_lds = {self.root(n): (base, PPB, R) for n, (base, _, _, _) in self.out_stage.items()}
+        self.skip_store, self.out_stage = set(), {}
         o.append(f'{ind}}}')
         self.note(reads, writes)
         self.mark(out, ind, f'stream {name}')
+
+    def epi_only(self, n, fused_ids):
+        """Is value n read only by the statements fused into this epilogue?"""
+        r = self.root(n)
+        carries = set(self.alias) | set(self.alias.values())
+        return (n not in self.outputs and r == n and n not in carries
+                and self.readers_of.get(n, set()) <= fused_ids)
+
+    def stage_out_ok(self, t, reg, pts, R, PPB):
+        """Can value t (made at every point of this stream) go through an LDS
+        copy: laid out [reg axes, point axes] in global scratch, and worth it
+        (several rows per point, or the argmax that reads it next)?"""
+        n = t[1]
+        r = self.root(n)
+        if r in self.private or r in self.fx or r not in self.g or list(self.axes_of[r]) != list(t[2]):
+            return False
+        if list(t[2]) != list(reg) + list(pts) or R * PPB > STAGE_OUT_MAX:
+            return False
+        return R >= 2 or any(i in self.argmax for i in self.readers_of.get(n, ()))
 
     def override_step(self, step_override):
         saved = dict(self.step_env)
@@ -292,23 +351,38 @@ class StreamMixin:
         self.step_env.update(saved)
 
     @staticmethod
-    def slot_point(geo, q):
-        NW, ppw, PPB = geo['NW'], geo['ppw'], geo['PPB']
-        return (f'((int)blockIdx.x * {PPB} + ({q} * {NW} + wave) * {ppw} + sub_)',
-                f'(wave < {NW} && ({q} * {NW} + wave) * {ppw} + sub_ < {PPB})')
+    def slot_point(geo, q, j='0'):
+        """(point, valid) of point j of this lane group in slot q: a lane group
+        makes PB consecutive points of its block's range."""
+        NW, ppw, PPB, PB = geo['NW'], geo['ppw'], geo['PPB'], geo['PB']
+        loc = f'(({q} * {NW} + wave) * {ppw} + sub_) * {PB} + {j}' if PB > 1 else \
+            f'({q} * {NW} + wave) * {ppw} + sub_'
+        return f'((int)blockIdx.x * {PPB} + {loc})', f'(wave < {NW} && {loc} < {PPB})'
+
+    def epi_item(self, geo, q_c, t, rows, lines, ind):
+        """Lines binding item t of this lane: after the butterfly every lane of
+        a group holds all (point, row) sums; item it_ = cl_ + t * lpp of the
+        group's PB * rows is point jj_, row r_. Returns (point, valid)."""
+        PB = geo['PB']
+        lines.append(f'{ind}const int it_ = cl_ + {t * geo["lpp"]};')
+        if PB > 1:
+            lines.append(f'{ind}const int jj_ = it_ / {rows}, r_ = it_ % {rows};')
+        else:
+            lines.append(f'{ind}const int jj_ = 0, r_ = it_;')
+        p_c, ok_c = self.slot_point(geo, q_c, 'jj_')
+        return p_c, f'it_ < {rows * PB} && {ok_c}'
 
     def epi_context(self, st, geo, q_c, rc, j, rows, body):
-        """Lines binding the point of slot q_c and the row of lane group member
-        j around ``body`` (lines that may use them)."""
-        p_c, ok_c = self.slot_point(geo, q_c)
-        lines = [f'{{ const int p_ = {p_c};', f'  if ({ok_c} && p_ < {geo["P"]}) {{']
+        """Lines binding the point and row of this lane's item j of slot q_c
+        around ``body`` (lines that may use them)."""
+        lines = ['{']
+        p_c, ok = self.epi_item(geo, q_c, j, rows, lines, '  ')
+        lines += [f'  const int p_ = {p_c};', f'  if ({ok} && p_ < {geo["P"]}) {{']
         self.decode('p_', st.pts, lines, '    ', prefix='ep_')
-        lines.append(f'    const int r_ = cl_ + {j * geo["lpp"]};')
-        lines.append(f'    if (r_ < {rows}) {{')
         if geo['reg']:
-            self.decode(f'({rc * geo["rch"]} + r_)', geo['reg'], lines, '      ', prefix='er_')
-        lines += ['      ' + x for x in body]
-        lines += ['    }', '  }', '}']
+            self.decode(f'({rc * geo["rch"]} + r_)', geo['reg'], lines, '    ', prefix='er_')
+        lines += ['    ' + x for x in body]
+        lines += ['  }', '}']
         return lines
 
     def epi_env(self, st, geo, rc):
@@ -334,12 +408,13 @@ class StreamMixin:
         epilogue then reads early-issued registers), else None (slots are
         streamed PI_STREAM at a time)."""
         rows = min(rch, R - rc * rch)
-        rpl = -(-rows // lpp)
+        PB = geo['PB']
+        rpl = -(-(rows * PB) // lpp)
         J2 = I + '  '
         if qs is None:
-            PI = PI_STREAM
+            PI = max(1, PI_STREAM // PB)
             o.append(f'{I}for (int q0_ = 0; q0_ < {NQ}; q0_ += {PI}) {{')
-            o.append(f'{J2}{ltype} wl_[{PI}][{pl}];')
+            o.append(f'{J2}{ltype} wl_[{PI}][{PB}][{pl}];')
             for qi in range(PI):
                 o.append(f'{J2}if (q0_ + {qi} < {NQ}) {{')
                 o += [J2 + '  ' + x for x in load_lines(f'(q0_ + {qi})', f'wl_[{qi}]', None)]
@@ -363,12 +438,12 @@ class StreamMixin:
             o.append(f'{I}}}')
 
     def slot_dot(self, o, K3, q_c, wsrc, dt, vec, nv, lpp, pl, exact, rch, K, abase, geo):
-        p_c, ok_c = self.slot_point(geo, q_c)
-        o.append(f'{K3}const int p_ = {p_c};')
-        o.append(f'{K3}const bool ok_ = {ok_c} && p_ < {geo["P"]};')
-        o.append(f'{K3}float acc_[{rch}];')
+        PB = geo['PB']
+        o.append(f'{K3}float acc_[{PB}][{rch}];')
         o.append(f'{K3}#pragma unroll')
-        o.append(f'{K3}for (int r_ = 0; r_ < {rch}; ++r_) acc_[r_] = 0.0f;')
+        o.append(f'{K3}for (int j_ = 0; j_ < {PB}; ++j_)')
+        o.append(f'{K3}  #pragma unroll')
+        o.append(f'{K3}  for (int r_ = 0; r_ < {rch}; ++r_) acc_[j_][r_] = 0.0f;')
         self.mark(o, K3, 'stream dot start')
         o.append(f'{K3}#pragma unroll')
         o.append(f'{K3}for (int m_ = 0; m_ < {pl}; ++m_) {{')
@@ -376,41 +451,47 @@ class StreamMixin:
         o.append(f'{K4}const int kv_ = cl_ + m_ * {lpp};')
         if not exact:
             o.append(f'{K4}if (kv_ >= {nv}) break;')
-        o.append(f'{K4}float wf_[{vec}];')
-        o.append(f'{K4}{self.vec_unpack(dt, vec, wsrc + "[m_]", "wf_")}')
+        o.append(f'{K4}float wf_[{PB}][{vec}];')
+        for j in range(PB):
+            o.append(f'{K4}{self.vec_unpack(dt, vec, wsrc + f"[{j}][m_]", f"wf_[{j}]")}')
         o.append(f'{K4}#pragma unroll')
         o.append(f'{K4}for (int r_ = 0; r_ < {rch}; ++r_) {{')
         o.append(f'{K4}  const float* ar_ = sh_f + {abase} + r_ * {K} + kv_ * {vec};')
         o.append(f'{K4}  float av_[{vec}];')
         o.append(f'{K4}  {self.lds_vec_load(vec, "ar_", "av_")}')
         o.append(f'{K4}  #pragma unroll')
-        o.append(f'{K4}  for (int v_ = 0; v_ < {vec}; ++v_) acc_[r_] = fmaf(av_[v_], wf_[v_], acc_[r_]);')
+        o.append(f'{K4}  for (int j_ = 0; j_ < {PB}; ++j_)')
+        o.append(f'{K4}    #pragma unroll')
+        o.append(f'{K4}    for (int v_ = 0; v_ < {vec}; ++v_) acc_[j_][r_] = fmaf(av_[v_], wf_[j_][v_], acc_[j_][r_]);')
         o.append(f'{K4}}}')
         o.append(f'{K3}}}')
         if lpp > 1:
             o.append(f'{K3}#pragma unroll')
-            o.append(f'{K3}for (int r_ = 0; r_ < {rch}; ++r_) acc_[r_] = group_red_sum(acc_[r_], {lpp});')
+            o.append(f'{K3}for (int j_ = 0; j_ < {PB}; ++j_)')
+            o.append(f'{K3}  #pragma unroll')
+            o.append(f'{K3}  for (int r_ = 0; r_ < {rch}; ++r_) acc_[j_][r_] = group_red_sum(acc_[j_][r_], {lpp});')
 
     def slot_epilogue(self, s, c, st, fused, o, K3, q_c, rc, rows, rpl, geo, early):
-        """After the butterfly every lane of a point group holds all rows'
-        sums; lane r of the group finishes row r (rows past the group width go
-        round again). ``early``: (register prefix of member j, unsafe set) when
-        the epilogue's early loads were issued at the barrier."""
-        o.append(f'{K3}if (ok_) {{')
-        K5 = K3 + '  '
-        self.decode('p_', st.pts, o, K5, prefix='ep_')
+        """After the butterfly every lane of a lane group holds the sums of
+        all its (point, row) items; lane i of the group finishes items i,
+        i + lpp, ... (``epi_item``). ``early``: (register prefix of round j,
+        unsafe set) when the epilogue's early loads were issued at the barrier."""
+        K5 = K3
+        PB = geo['PB']
         for j in range(rpl):
             o.append(f'{K5}{{')
             K6 = K5 + '  '
-            o.append(f'{K6}const int r_ = cl_ + {j * geo["lpp"]};')
-            o.append(f'{K6}if (r_ < {rows}) {{')
+            p_c, ok = self.epi_item(geo, q_c, j, rows, o, K6)
+            o.append(f'{K6}const int p_ = {p_c};')
+            o.append(f'{K6}if ({ok} && p_ < {geo["P"]}) {{')
             K7 = K6 + '  '
-            if rows == 1:
-                val = 'acc_[0]'
+            self.decode('p_', st.pts, o, K7, prefix='ep_')
+            if rows * PB == 1:
+                val = 'acc_[0][0]'
             else:
-                o.append(f'{K7}float av_ = acc_[0];')
-                for r in range(1, rows):
-                    o.append(f'{K7}av_ = r_ == {r} ? acc_[{r}] : av_;')
+                o.append(f'{K7}float av_ = acc_[0][0];')
+                for it in range(1, rows * PB):
+                    o.append(f'{K7}av_ = it_ == {it} ? acc_[{it // rows}][{it % rows}] : av_;')
                 val = 'av_'
             lines = []
             if geo['reg']:
@@ -424,7 +505,6 @@ class StreamMixin:
             o += lines
             o.append(f'{K6}}}')
             o.append(f'{K5}}}')
-        o.append(f'{K3}}}')
 
     # ------------------------------------------------------------ the other factor
     def direct_lds(self, c, reg):
