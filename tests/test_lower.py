@@ -72,9 +72,10 @@ def test_gpt2_small_b1_plan():
     # attention: scores, softmax statistics and weighted values in one block per (bt, h)
     assert p['sc'] == p['mx'] == p['_h1'] == p['o'] == 'attention[bt, h]'
     assert p['logit'] == 'stream'
-    # argmax over each block's own logits, combined by every block; embedding in every block
+    # argmax over each block's own logits, combined by every block; the embedding
+    # (the layer loop's first residual) is evaluated where layer 0 reads it
     assert p['best'] == 'argmax (own points)' and p['next'] == 'argmax'
-    assert p['z0'] == 'replicated'
+    assert p['z0'] == 'first value of z, made where read'
     assert p['m1'] == p['v1'] == p['a'] == 'private'
     assert p['residue keys'] == 'epilogue of qkv' and p['residue vals'] == 'epilogue of qkv'
     assert p['g'] == 'epilogue of u'

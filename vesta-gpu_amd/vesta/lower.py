@@ -379,6 +379,9 @@ class Lowering(StreamMixin, AttnMixin):
         self.stmts = stmts
         self.place_all(stmts)
         self.find_projections(stmts)
+        self.peels = {}               # id(step) -> statement of its carry's first value, made where read
+        self.peel_active = {}         # carry root -> (loop variable, that statement) inside the loop
+        self.find_peels(stmts)
         self.layout(stmts)
 
     # ------------------------------------------------------------ program facts
@@ -548,6 +551,46 @@ class Lowering(StreamMixin, AttnMixin):
                         self.alias[e[1]] = carry
                 self.alias[name] = carry
         walk(ss)
+
+    def find_peels(self, ss):
+        """A step loop whose carry starts from a replicated statement (one
+        reading residues only): in the first iteration, reads of the carry
+        evaluate that statement where they are, so it is never stored (every
+        block would otherwise write the same values to the same addresses)."""
+        for i, s in enumerate(ss):
+            if s[0] != 'step':
+                continue
+            self.find_peels(s[6])
+            _, name, axes, var, init, carry, blk = s
+            if init[0] != 'idx' or self.alias.get(init[1]) != carry or var in self.dynamic:
+                continue
+            if self.static.get(var, 0) < 1:
+                continue
+            defs = [t for t in ss[:i] if t[0] == 'let' and t[1] == init[1]]
+            if len(defs) != 1 or self.place.get(id(defs[0])) != 'repl':
+                continue
+            if self.readers_of.get(init[1], set()) != {id(s)}:
+                continue
+            self.peels[id(s)] = defs[0]
+            self.elided.add(id(defs[0]))
+
+    def peel_value(self, r, ix):
+        """For a carry read in the first iteration of its loop: C text of
+        its first value at the index ix (C expressions), or None."""
+        pk = self.peel_active.get(r)
+        if pk is None:
+            return None
+        lv, zs = pk
+        env = {a: (c, 'int') for a, c in zip(zs[2], ix)}
+        saved, self.capture = self.capture, None
+        try:
+            pre = []
+            v, t = self.expr(zs[3], env, pre, '')
+        finally:
+            self.capture = saved
+        if pre:
+            raise LowerError(f'first value of {r} needs statements of its own')
+        return lv, self.as_float(v, t)
 
     def root(self, n):
         while n in self.alias:
@@ -1208,6 +1251,9 @@ class Lowering(StreamMixin, AttnMixin):
         if r in self.fx:
             i = f'{self.g[r]} + 2u * ({a})'
             return self.captured(f'fxld(rb_S, {i})', 'float', r, raw=(f'ldfx_raw(rb_S, {i})', 'long long', 'vh_fx2f'))
+        pv = self.peel_value(r, ix)
+        if pv is not None:
+            return f'({pv[0]} == 0 ? {pv[1]} : ldcs(rb_S, {self.g[r]} + {a}))'
         return self.captured(f'ldcs(rb_S, {self.g[r]} + {a})', 'float', r)
 
     def store(self, n, ix, v, t):
@@ -1981,7 +2027,21 @@ class Lowering(StreamMixin, AttnMixin):
                 if off - base + size <= STAGE_MAX:
                     staged[r] = off
                     fn = 'stage_fx' if r in self.fx else 'stage_ldc4'
-                    out.append(f'{ind}{fn}(sh_f + {off}, rb_S, {self.g[r]}, {size});  // stage {r}')
+                    if r in self.peel_active:
+                        lv, zs = self.peel_active[r]
+                        out.append(f'{ind}if ({lv} == 0) {{  // {r} starts as {zs[1]}: made here')
+                        # every iteration's loads in flight at once (the token rows are random)
+                        out.append(f'{ind}  #pragma unroll')
+                        out.append(f'{ind}  for (int e_ = tid; e_ < {size}; e_ += {BLOCK}) {{')
+                        env = self.decode('e_', list(zs[2]), out, ind + '    ', prefix='z0_')
+                        lv_, val = self.peel_value(r, [env[a][0] for a in zs[2]])
+                        out.append(f'{ind}    sh_f[{off} + e_] = {val};')
+                        out.append(f'{ind}  }}')
+                        out.append(f'{ind}}} else {{')
+                        out.append(f'{ind}  {fn}(sh_f + {off}, rb_S, {self.g[r]}, {size});  // stage {r}')
+                        out.append(f'{ind}}}')
+                    else:
+                        out.append(f'{ind}{fn}(sh_f + {off}, rb_S, {self.g[r]}, {size});  // stage {r}')
                     off += -(-size // 4) * 4
         self.stage_floats = max(self.stage_floats, off - base)
         self.priv_stage_end = off - base
@@ -2655,6 +2715,10 @@ class Lowering(StreamMixin, AttnMixin):
         out.append(f'{ind}  const int tid = vh_opaque(tid_k_), lane = tid & 63, wave = tid >> 6;')
         saved = self.step_env.get(var)
         self.step_env[var] = (lv, 'int')
+        pe = self.peels.get(id(s))
+        if pe is not None:
+            self.plan.append((show_stmt(pe), f'first value of {carry}, made where read'))
+            self.peel_active[self.root(carry)] = (lv, pe)
         self.mult *= n
         self.loops.append({'id': self.fresh('loop'), 'var': var, 'lv': lv, 'n': self.ext_c(var),
                            'pf_before': self.last_pf, 'body_barrier': False, 'end_prefetch': [],
@@ -2665,6 +2729,7 @@ class Lowering(StreamMixin, AttnMixin):
         if not (ret[0] == 'idx' and self.alias.get(ret[1]) == carry):
             self.gen_copy(carry, ret, axes, out, ind + '  ', f'{carry} <- ret')
         lp = self.loops[-1]
+        self.peel_active.pop(self.root(carry), None)
         self.barrier(out, ind + '  ', f'next {var}', pre_wait=lp['end_prefetch'])
         self.loops.pop()
         self.mult //= n

@@ -532,6 +532,7 @@ class StreamMixin:
         want = list(reg) + list(c.fold_axes)
         if (A[0] == 'idx' and A[1] in self.axes_of and self.root(A[1]) in self.g
                 and self.root(A[1]) not in self.private and self.root(A[1]) not in self.fx
+                and self.root(A[1]) not in self.peel_active
                 and list(self.axes_of[self.root(A[1])]) == want
                 and list(A[2]) == [('name', a) for a in want] and K % 4 == 0):
             rows = min(rch, R - rc * rch)
