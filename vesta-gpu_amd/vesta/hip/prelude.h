@@ -134,6 +134,9 @@ VH_BLOCK_RED(block_red_min, wave_red_min, op_min)
 __device__ __forceinline__ void argmax_pair(float& v, int& i, float ov, int oi) {
   if (ov > v || (ov == v && oi < i)) { v = ov; i = oi; }
 }
+__device__ __forceinline__ void wave_argmax(float& v, int& i) {
+  for (int o = 32; o > 0; o >>= 1) argmax_pair(v, i, __shfl_xor(v, o, 64), __shfl_xor(i, o, 64));
+}
 __device__ __forceinline__ void block_argmax(float& v, int& i, float* rv, int* ri) {
   for (int o = 32; o > 0; o >>= 1) argmax_pair(v, i, __shfl_xor(v, o, 64), __shfl_xor(i, o, 64));
   vh_lds_sync();
@@ -231,6 +234,26 @@ __device__ __forceinline__ unsigned ldg4_nt(vh_rsrc r, unsigned i) {
 __device__ __forceinline__ float vh_divr(float x, float d, float r) {
   const float q = x * r;
   return fmaf(fmaf(-q, d, x), r, q);
+}
+
+// Matrix cores: 16x16 fp32 tile += A (16 x 32 fp16) * B (32 x 16 fp16); lane l
+// holds A[l % 16][8 (l / 16) ..+8], B[8 (l / 16) ..+8][l % 16] and the result
+// rows 4 (l / 16) ..+4 of column l % 16.
+typedef _Float16 vh_h8 __attribute__((ext_vector_type(8)));
+__device__ __forceinline__ vh_f32x4 vh_mfma(vh_u32x4 a, vh_u32x4 b, vh_f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(vh_h8, a), __builtin_bit_cast(vh_h8, b), c, 0, 0, 0);
+}
+// Eight floats as fp16 halves v = hi + lo: hi the nearest fp16, lo the nearest
+// fp16 to the remainder v - hi (exact in fp32).
+__device__ __forceinline__ void vh_split8(const float* v, vh_u32x4& hi, vh_u32x4& lo) {
+  vh_h8 h, l;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    h[j] = (_Float16)v[j];
+    l[j] = (_Float16)(v[j] - (float)h[j]);
+  }
+  hi = __builtin_bit_cast(vh_u32x4, h);
+  lo = __builtin_bit_cast(vh_u32x4, l);
 }
 
 // Fixed-point accumulators: fp32 values summed exactly as 64-bit integers in

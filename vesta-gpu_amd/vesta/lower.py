@@ -65,6 +65,7 @@ import numpy as np
 from .interp import parse
 from .attn import AttnMixin
 from .stream import StreamMixin
+from .mfma import MfmaMixin
 
 PRELUDE_PATH = Path(__file__).resolve().parent / 'hip' / 'prelude.h'
 
@@ -319,7 +320,7 @@ class LowerError(ValueError):
     pass
 
 
-class Lowering(StreamMixin, AttnMixin):
+class Lowering(StreamMixin, MfmaMixin, AttnMixin):
     NWAVE, BLOCK, REG_MAX = NWAVE, BLOCK, REG_MAX
     show_stmt = staticmethod(show_stmt)
     nodes_of = staticmethod(nodes)
@@ -2549,8 +2550,22 @@ class Lowering(StreamMixin, AttnMixin):
         o = out
         I = ind + '  '
         o.append(f'{ind}{{  // argmax {name}, {s2[1]}: per-block pairs')
+        if in_lds is not None and npts <= NWAVE:
+            # wave p reduces row p of the block's LDS copy: no block-wide steps
+            o.append(f'{I}if (wave < {npts}) {{')
+            o.append(f'{I}  float bv_ = -INFINITY; int bi_ = 0x7fffffff;')
+            o.append(f'{I}  const int k0_ = (int)blockIdx.x * {part["PPB"]};')
+            o.append(f'{I}  const int k1_ = k0_ + {part["PPB"]} < {part["P"]} ? k0_ + {part["PPB"]} : {part["P"]};')
+            o.append(f'{I}  for (int k_ = k0_ + lane; k_ < k1_; k_ += 64) {{')
+            o.append(f'{I}    const float v_ = sh_f[{in_lds[0]} + wave * {in_lds[1]} + k_ - k0_];')
+            o.append(f'{I}    if (v_ > bv_ || (v_ == bv_ && k_ < bi_)) {{ bv_ = v_; bi_ = k_; }}')
+            o.append(f'{I}  }}')
+            o.append(f'{I}  wave_argmax(bv_, bi_);')
+            o.append(f'{I}  if (lane == 0) {{ stcs(rb_S, {poff} + wave * {GRID_MAX} + blockIdx.x, bv_); '
+                     f'stcs(rb_S, {poff + npts * GRID_MAX} + wave * {GRID_MAX} + blockIdx.x, (float)bi_); }}')
+            o.append(f'{I}}}')
         envs = []
-        for p in range(npts):
+        for p in (range(npts) if in_lds is None or npts > NWAVE else ()):
             lines = []
             env = self.decode_const(str(p), axes, lines, I) if axes else {}
             envs.append(env)
@@ -2581,7 +2596,27 @@ class Lowering(StreamMixin, AttnMixin):
         self.barrier(out, ind, f'combine {name}')
         cval = s2[3][3][3][1]
         o.append(f'{ind}{{  // argmax {name}, {s2[1]}: every block combines the pairs in block order')
-        for p in range(npts):
+        if npts <= NWAVE:
+            # wave p combines row p
+            o.append(f'{I}if (wave < {npts}) {{')
+            o.append(f'{I}  float bv_ = -INFINITY; int bi_ = 0x7fffffff;')
+            o.append(f'{I}  for (int b_ = lane; b_ < (int)nblk; b_ += 64) {{')
+            o.append(f'{I}    const float v_ = ldcs(rb_S, {poff} + wave * {GRID_MAX} + b_);')
+            o.append(f'{I}    const int i_ = (int)ldcs(rb_S, {poff + npts * GRID_MAX} + wave * {GRID_MAX} + b_);')
+            o.append(f'{I}    if (v_ > bv_ || (v_ == bv_ && i_ < bi_)) {{ bv_ = v_; bi_ = i_; }}')
+            o.append(f'{I}  }}')
+            o.append(f'{I}  wave_argmax(bv_, bi_);')
+            o.append(f'{I}  const float nv_ = bi_ == 0x7fffffff ? {c_float(cval)} : (float)bi_;')
+            o.append(f'{I}  if (lane == 0) {{')
+            o.append(f'{I}    amx_[wave] = nv_;')
+            o.append(f'{I}    if (blockIdx.x == 0) {{')
+            env = self.decode('wave', axes, o, I + '      ', prefix='aw_') if axes else {}
+            o.append(f'{I}      {self.store(name, [env[a][0] for a in axes], "bv_", "float")}')
+            o.append(f'{I}      {self.store(s2[1], [env[a][0] for a in axes], "nv_", "float")}')
+            o.append(f'{I}    }}')
+            o.append(f'{I}  }}')
+            o.append(f'{I}}}')
+        for p in (range(npts) if npts > NWAVE else ()):
             lines = []
             env = self.decode_const(str(p), axes, lines, I) if axes else {}
             o += lines

@@ -1,0 +1,318 @@
+"""Streamed contractions with several rows on the matrix cores.
+
+A stream ``y[r.., p] = EPI(fold sum k: A[r.., k] * W[p, k])`` with 4 to 16
+rows r (the batch) and fp16 weights runs on ``v_mfma_f32_16x16x32_f16``:
+rows are the MFMA's M (padded to 16 with zeros), a tile of 16 consecutive
+output points its N, and the fold its K, 32 at a time. Lane l of a wave holds
+A[l % 16][k0 + 8 (l / 16) ..+8], W[k0 + 8 (l / 16) ..+8][point l % 16] (one
+16-byte load from the point's row of the weight copy) and, after the loop,
+y[4 (l / 16) + v][point l % 16] for v < 4.
+
+The other factor is fp32; it is split into fp16 halves a = hi + lo (hi the
+nearest fp16, lo the nearest fp16 to the exact remainder), both multiplied
+into the same fp32 accumulator, so a keeps 22 significant bits (the weights
+are fp16 already, and every product is exact). Values beyond the fp16 range
+(65504) are not representable on this path.
+
+Work split: a block's points form NT tiles. With at least as many tiles as
+compute waves, wave w makes tiles w, w + NW, .. over the whole fold; with
+fewer, KW waves share a tile, each over its own range of the fold, and the
+partial tiles are added through LDS in wave order (a fixed order, so results
+do not depend on timing). The weights of a wave's share are loaded at the
+barrier before the site when they fit in PREFETCH_VGPRS registers, else
+streamed MFMA_PIPE k-blocks ahead through two register sets.
+"""
+from __future__ import annotations
+
+from .stream import PREFETCH_VGPRS
+
+MFMA_ROWS_MIN = 4            # rows from which a stream runs on the matrix cores
+MFMA_PIPE = 3                # k-blocks of weights in flight per tile when not prefetched
+MFMA_POINTS_MIN = 8          # points a block must make (of a tile's 16 columns)
+
+
+class MfmaMixin:
+    def mfma_ok(self, c, st):
+        """Can stream st (of contraction c) run on the matrix cores, with at
+        least half of a tile's 16 columns holding points of the block?"""
+        R = self.size(c.reg_axes)
+        PPB = -(-self.size(st.pts) // self.grid)
+        return (self.res[st.src][1] == 'f16' and MFMA_ROWS_MIN <= R <= 16 and st.K % 32 == 0
+                and st.c0 % 8 == 0 and st.rowlen % 8 == 0 and PPB >= MFMA_POINTS_MIN)
+
+    def gen_stream_mfma(self, s, c, st, fused, out, ind):
+        name = s[1]
+        reads, writes = self.site_io(s, c, fused)
+        self.sync(reads, writes, out, ind, name)
+        self.plan.append((self.show_stmt(s), 'stream' + (' (transposed copy)' if st.pack else '') + ' mfma'
+                          + (f' +{len(fused)} fused' if fused else '')))
+        for _, t, _ in fused:
+            self.plan.append((self.show_stmt(t), f'epilogue of {name}'))
+        K, NKB = st.K, st.K // 32
+        NW = self.NWAVE - 1
+        P = self.size(st.pts)
+        PPB = -(-P // self.grid)
+        reg = c.reg_axes
+        R = self.size(reg)
+        NT = -(-PPB // 16)
+        if NT >= NW:
+            TPW, KW = -(-NT // NW), 1
+        else:
+            TPW, KW = 1, NW // NT
+        KBW = -(-NKB // KW)
+        prefetch = TPW * KBW * 4 <= PREFETCH_VGPRS
+        sid = self.fresh('m')
+        CT = NW * 64                          # the epilogue: one (row, point) item per compute thread
+        NI = -(-(R * PPB) // CT)
+        geo = dict(P=P, PPB=PPB, NW=NW, NT=NT, TPW=TPW, KW=KW, NKB=NKB, KBW=KBW, R=R, reg=list(reg), CT=CT)
+        rr = self.rsrc(st.src)
+        rs = self.res_strides(st.src)
+        I = ind + '  '
+        o = out
+
+        def wload(i, kb, dst, cond='true'):
+            """Lines loading the weight fragment of slot i, k-block kb (C
+            expressions) into dst (zeros where there is no point)."""
+            lines = [f'{{ const int n_ = ({self.mfma_tile(geo, i)}) * 16 + (lane & 15);',
+                     '  const int p_ = (int)blockIdx.x * %d + n_;' % PPB,
+                     f'  if (mok_ && ({cond}) && ({self.mfma_tile(geo, i)}) < {NT} && n_ < {PPB} && p_ < {P}) {{']
+            env = self.decode('p_', st.pts, lines, '    ', prefix='sp_')
+            pre = []
+            ix = [self.index(x, env, pre, '    ') for x in st.prefix_idx]
+            lines += pre
+            base = self.addr(ix, rs[:-1]) if ix else '0'
+            lines.append(f'    {dst} = ldg16_nt({rr}, (unsigned)({base}) + {st.c0}u + (unsigned)(({kb}) * 32 + (lane >> 4) * 8));')
+            lines.append(f'  }} else {dst} = vh_u32x4{{0u, 0u, 0u, 0u}};')
+            lines.append('}')
+            return lines
+
+        wm = f'wm_{sid}'
+        if prefetch:
+            self.decls.append(f'vh_u32x4 {wm}[{TPW}][{KBW}];')
+            unsafe = self.unsafe_early()
+            caps = {}
+
+            def make(step_override):
+                saved = self.override_step(step_override)
+                try:
+                    lines = [f'if (wave < {NW}) {{'] + ['  ' + x for x in self.mfma_role(geo)]
+                    for i in range(TPW):
+                        for j in range(KBW):
+                            lines += ['  ' + x for x in wload(i, f'mk0_ + {j}', f'{wm}[{i}][{j}]', f'mk0_ + {j} < mk1_')]
+                    for q in range(NI):
+                        pre = f'pf_{sid}_{q}_'
+                        self.capture = {'prefix': pre, 'loads': [], 'unsafe': unsafe}
+                        try:
+                            self.epilogue(s, c, fused, self.mfma_env(st, geo), '0.0f', [], '')
+                            loads = self.capture['loads']
+                        finally:
+                            self.capture = None
+                        caps[pre] = [(n, k) for n, _, k in loads]
+                        if loads:
+                            lines += ['  ' + x for x in self.mfma_item(st, geo, q, [f'{n} = {t};' for n, t, _ in loads])]
+                    return lines + ['}']
+                finally:
+                    self.restore_step(saved)
+            self.place_prefetch(make, o, ind)
+            for regs in caps.values():
+                for n, k in regs:
+                    self.decls.append(f'{self.cap_ctype(k)} {n};')
+        o.append(f'{ind}{{  // stream {name} on the matrix cores: {P} points x {K} from {st.src}, rows={R}, '
+                 f'points/block={PPB}, tiles={NT}, tiles/wave={TPW}, waves/tile={KW}'
+                 + (' prefetched' if prefetch else ''))
+        o += [I + x for x in self.mfma_role(geo)]
+        self.stream_part[self.root(name)] = dict(pts=list(st.pts), PPB=PPB, P=P, reg=list(reg))
+        # LDS: [fp32 copy of the other factor, if it has to be made] [hi] [lo] [partial tiles] [values]
+        top = self.lds_floats + self.stage_top
+        direct = self.direct_lds(c, reg)
+        src = None
+        if direct is None:
+            src = self.mfma_global_src(c, reg, K)
+            if src is None:
+                self.stage_A(c, reg, 0, R, R, K, str(top), o, I)
+                direct, top = str(top), top + R * K
+        SAB = K * 2 + 16                      # bytes per row of a half array (padded against bank conflicts)
+        ah = top * 4
+        al = ah + R * SAB
+        top = (al + R * SAB) // 4
+        red = top
+        if KW > 1:
+            top += NW * 64 * 4
+        accb = top                            # the sums, [row][own point]
+        top += -(-R * PPB // 4) * 4
+        self.mfma_split(direct, src, R, K, SAB, ah, al, o, I)
+        self.mark(o, I, f'stream {name}: halves')
+        # values of the site (as in the other streams)
+        fused_ids = {id(t) for _, t, _ in fused}
+        made = [s] + [t for kind, t, _ in fused if kind == 'let']
+        self.skip_store = {t[1] for t in made if self.epi_only(t[1], fused_ids)}
+        self.out_stage = {}
+        for t in made:
+            n = t[1]
+            if n in self.skip_store or not self.stage_out_ok(t, reg, st.pts, R, PPB):
+                continue
+            self.out_stage[n] = (top, PPB, list(reg), list(st.pts))
+            top += -(-R * PPB // 4) * 4
+        self.stage_floats = max(self.stage_floats, top - self.lds_floats)
+        # the products
+        o.append(f'{I}vh_f32x4 acc_[{TPW}];')
+        o.append(f'{I}#pragma unroll')
+        o.append(f'{I}for (int i_ = 0; i_ < {TPW}; ++i_) acc_[i_] = vh_f32x4{{0.f, 0.f, 0.f, 0.f}};')
+
+        def kstep(kb, wsrc, J):
+            """Lines of one k-block (C expression kb, relative to mk0_) from weight registers wsrc(i)."""
+            lines = [f'{J}{{ const int kb_ = mk0_ + {kb};',
+                     f'{J}  const int ar_ = lane & 15, ak_ = kb_ * 32 + (lane >> 4) * 8;',
+                     f'{J}  const vh_u32x4 ah_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {ah} + ar_ * {SAB} + ak_ * 2) '
+                     f': vh_u32x4{{0u, 0u, 0u, 0u}};',
+                     f'{J}  const vh_u32x4 al_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {al} + ar_ * {SAB} + ak_ * 2) '
+                     f': vh_u32x4{{0u, 0u, 0u, 0u}};']
+            for i in range(TPW):
+                lines.append(f'{J}  acc_[{i}] = vh_mfma(ah_, {wsrc(i)}, acc_[{i}]);')
+                lines.append(f'{J}  acc_[{i}] = vh_mfma(al_, {wsrc(i)}, acc_[{i}]);')
+            lines.append(f'{J}}}')
+            return lines
+
+        o.append(f'{I}if (mok_) {{')
+        J = I + '  '
+        if prefetch:
+            for j in range(KBW):
+                o.append(f'{J}if (mk0_ + {j} < mk1_)')
+                o += kstep(str(j), lambda i, j=j: f'{wm}[{i}][{j}]', J + '  ')
+        else:
+            D = MFMA_PIPE
+            o.append(f'{J}vh_u32x4 wb0_[{TPW}][{D}], wb1_[{TPW}][{D}];')
+            for i in range(TPW):
+                for d in range(D):
+                    o += [J + x for x in wload(i, f'mk0_ + {d}', f'wb0_[{i}][{d}]', f'mk0_ + {d} < mk1_')]
+            o.append(f'{J}for (int c0_ = 0; c0_ < {KBW}; c0_ += {2 * D}) {{')
+            J2 = J + '  '
+            for half, (cur, nxt) in enumerate((('wb0_', 'wb1_'), ('wb1_', 'wb0_'))):
+                ahead = f'c0_ + {(half + 1) * D}'
+                for i in range(TPW):
+                    for d in range(D):
+                        o += [J2 + x for x in wload(i, f'mk0_ + {ahead} + {d}', f'{nxt}[{i}][{d}]',
+                                                    f'mk0_ + {ahead} + {d} < mk1_')]
+                for d in range(D):
+                    kb = f'c0_ + {half * D + d}'
+                    o.append(f'{J2}if (mk0_ + {kb} < mk1_)')
+                    o += kstep(kb, lambda i, cur=cur, d=d: f'{cur}[{i}][{d}]', J2 + '  ')
+            o.append(f'{J}}}')
+        o.append(f'{I}}}')
+        self.mark(o, I, f'stream {name}: products')
+        if KW > 1:
+            # partial tiles of the later parts of the fold, added in part order
+            o.append(f'{I}if (mok_ && mkp_ > 0) *(vh_f32x4*)(sh_f + {red} + (wave * 64 + lane) * 4) = acc_[0];')
+            o.append(f'{I}vh_lds_sync();')
+            o.append(f'{I}if (mok_ && mkp_ == 0) {{')
+            for q in range(1, KW):
+                o.append(f'{I}  acc_[0] += *(const vh_f32x4*)(sh_f + {red} + ((wave + {q * NT}) * 64 + lane) * 4);')
+            o.append(f'{I}}}')
+        # the sums into LDS [row][own point] (lane l holds rows 4 (l / 16) ..+4 of
+        # point l % 16 of each of its tiles); then every compute thread finishes
+        # one (row, point) item at a time, consecutive threads consecutive points
+        o.append(f'{I}if (mok_ && mkp_ == 0) {{')
+        for i in range(TPW):
+            o.append(f'{I}  {{ const int n_ = ({self.mfma_tile(geo, i)}) * 16 + (lane & 15);')
+            o.append(f'{I}    if (({self.mfma_tile(geo, i)}) < {NT} && n_ < {PPB}) {{')
+            o.append(f'{I}      #pragma unroll')
+            o.append(f'{I}      for (int v_ = 0; v_ < 4; ++v_) {{')
+            o.append(f'{I}        const int r_ = (lane >> 4) * 4 + v_;')
+            o.append(f'{I}        if (r_ < {R}) sh_f[{accb} + r_ * {PPB} + n_] = acc_[{i}][v_];')
+            o.append(f'{I}      }}')
+            o.append(f'{I}    }}')
+            o.append(f'{I}  }}')
+        o.append(f'{I}}}')
+        o.append(f'{I}vh_lds_sync();')
+        for q in range(NI):
+            body = []
+            if prefetch:
+                self.capture = {'prefix': f'pf_{sid}_{q}_', 'loads': [], 'unsafe': unsafe}
+            try:
+                self.epilogue(s, c, fused, self.mfma_env(st, geo), f'sh_f[{accb} + e_]', body, '')
+            finally:
+                self.capture = None
+            o += [I + x for x in self.mfma_item(st, geo, q, body)]
+        if self.out_stage:
+            self.write_out(P, PPB, R, o, I)
+            self.mark(o, I, f'stream {name}: write out')
+        self.stream_lds = {self.root(n): (base, PPB, R) for n, (base, _, _, _) in self.out_stage.items()}
+        self.skip_store, self.out_stage = set(), {}
+        o.append(f'{ind}}}')
+        self.note(reads, writes)
+        self.mark(out, ind, f'stream {name}')
+
+    # ------------------------------------------------------------ pieces
+    @staticmethod
+    def mfma_role(geo):
+        """Lines binding this wave's share: mok_ (takes part), mkp_ (its part of
+        the fold), mt_ (its first tile), mk0_ / mk1_ (its k-blocks)."""
+        NW, NT, KW, NKB = geo['NW'], geo['NT'], geo['KW'], geo['NKB']
+        if KW == 1:
+            return [f'const bool mok_ = wave < {NW} && wave < {NT};',
+                    'const int mkp_ = 0, mt_ = wave, mk0_ = 0, mk1_ = %d;' % NKB]
+        return [f'const bool mok_ = wave < {NT * KW};',
+                f'const int mkp_ = wave / {NT}, mt_ = wave % {NT};',
+                f'const int mk0_ = mkp_ * {NKB} / {KW}, mk1_ = (mkp_ + 1) * {NKB} / {KW};']
+
+    @staticmethod
+    def mfma_tile(geo, i):
+        return f'mt_ + {i * geo["NW"]}' if i else 'mt_'
+
+    def mfma_env(self, st, geo):
+        env = {a: (f'ep_{a}', 'int') for a in st.pts}
+        for a in geo['reg']:
+            env[a] = (f'er_{a}', 'int')
+        return env
+
+    def mfma_item(self, st, geo, q, body):
+        """Lines binding row r_ and point p_ of this thread's item q (item
+        e_ = tid + q * CT of the block's rows x points, point fastest) around
+        ``body``."""
+        PPB, CT = geo['PPB'], geo['CT']
+        lines = [f'{{ const int e_ = tid + {q * CT};',
+                 f'  const int r_ = e_ / {PPB}, n_ = e_ - r_ * {PPB};',
+                 f'  const int p_ = (int)blockIdx.x * {PPB} + n_;',
+                 f'  if (tid < {CT} && e_ < {geo["R"] * PPB} && p_ < {geo["P"]}) {{']
+        self.decode('p_', st.pts, lines, '    ', prefix='ep_')
+        if geo['reg']:
+            self.decode('r_', geo['reg'], lines, '    ', prefix='er_')
+        lines += ['    ' + x for x in body]
+        lines += ['  }', '}']
+        return lines
+
+    def mfma_global_src(self, c, reg, K):
+        """Global scratch offset of the other factor when it is a plain fp32
+        value laid out [reg axes, fold axes] (read with 16-byte loads), else None."""
+        A = c.A
+        if A[0] != 'idx' or A[1] not in self.axes_of:
+            return None
+        r = self.root(A[1])
+        want = list(reg) + list(c.fold_axes)
+        if (r in self.private or r in self.fx or r in self.peel_active or r not in self.g
+                or list(self.axes_of[r]) != want or list(A[2]) != [('name', a) for a in want] or K % 8):
+            return None
+        return self.g[r]
+
+    def mfma_split(self, direct, src, R, K, SAB, ah, al, o, I):
+        """The other factor (rows x K fp32, in LDS at float offset ``direct``
+        or in global scratch at ``src``) into fp16 halves in LDS."""
+        K8 = K // 8
+        o.append(f'{I}vh_lds_sync();')
+        o.append(f'{I}for (int e_ = tid; e_ < {R * K8}; e_ += {self.BLOCK}) {{')
+        o.append(f'{I}  const int r_ = e_ / {K8}, k8_ = e_ - r_ * {K8};')
+        o.append(f'{I}  float v_[8];')
+        if direct is not None:
+            o.append(f'{I}  const float* s_ = sh_f + {direct} + r_ * {K} + k8_ * 8;')
+            o.append(f'{I}  {self.lds_vec_load(8, "s_", "v_")}')
+        else:
+            o.append(f'{I}  const vh_f32x4 x0_ = ldc4(rb_S, {src}u + (unsigned)(r_ * {K} + k8_ * 8)), '
+                     f'x1_ = ldc4(rb_S, {src}u + (unsigned)(r_ * {K} + k8_ * 8 + 4));')
+            o.append(f'{I}  v_[0] = x0_.x; v_[1] = x0_.y; v_[2] = x0_.z; v_[3] = x0_.w; '
+                     f'v_[4] = x1_.x; v_[5] = x1_.y; v_[6] = x1_.z; v_[7] = x1_.w;')
+        o.append(f'{I}  vh_u32x4 h_, l_;')
+        o.append(f'{I}  vh_split8(v_, h_, l_);')
+        o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {ah} + r_ * {SAB} + k8_ * 16) = h_;')
+        o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {al} + r_ * {SAB} + k8_ * 16) = l_;')
+        o.append(f'{I}}}')
+        o.append(f'{I}vh_lds_sync();')

@@ -157,6 +157,8 @@ class StreamMixin:
 
     # ------------------------------------------------------------ codegen
     def gen_stream(self, s, c, st, fused, out, ind):
+        if self.mfma_ok(c, st):
+            return self.gen_stream_mfma(s, c, st, fused, out, ind)
         name = s[1]
         reads, writes = self.site_io(s, c, fused)
         self.sync(reads, writes, out, ind, name)
@@ -304,22 +306,27 @@ class StreamMixin:
             self.stream_body(s, c, st, fused, o, I, rc, rch, R, K, abase, dt, vec, nv, lpp, pl, exact,
                              NQ, qs, wq, ltype, geo, load_lines, sid, unsafe if prefetch else None)
         if self.out_stage:
-            o.append(f'{I}vh_lds_sync();')
-            o.append(f'{I}{{ const int p0_ = (int)blockIdx.x * {PPB};')
-            o.append(f'{I}  for (int e_ = tid; e_ < {R * PPB}; e_ += {self.BLOCK}) {{')
-            o.append(f'{I}    const int r_ = e_ / {PPB}, i_ = e_ - r_ * {PPB};')
-            o.append(f'{I}    if (p0_ + i_ < {P}) {{')
-            for n, (base, _, _, _) in self.out_stage.items():
-                o.append(f'{I}      stcs(rb_S, {self.g[self.root(n)]} + r_ * {P} + p0_ + i_, sh_f[{base} + e_]);')
-            o.append(f'{I}    }}')
-            o.append(f'{I}  }}')
-            o.append(f'{I}}}')
+            self.write_out(P, PPB, R, o, I)
             self.mark(o, I, f'stream {name}: write out')
         self.stream_lds = {self.root(n): (base, PPB, R) for n, (base, _, _, _) in self.out_stage.items()}
         self.skip_store, self.out_stage = set(), {}
         o.append(f'{ind}}}')
         self.note(reads, writes)
         self.mark(out, ind, f'stream {name}')
+
+    def write_out(self, P, PPB, R, o, I):
+        """The block's LDS copies of its values ([row][own point]) into global
+        scratch, row by row (consecutive threads, consecutive points)."""
+        o.append(f'{I}vh_lds_sync();')
+        o.append(f'{I}{{ const int p0_ = (int)blockIdx.x * {PPB};')
+        o.append(f'{I}  for (int e_ = tid; e_ < {R * PPB}; e_ += {self.BLOCK}) {{')
+        o.append(f'{I}    const int r_ = e_ / {PPB}, i_ = e_ - r_ * {PPB};')
+        o.append(f'{I}    if (p0_ + i_ < {P}) {{')
+        for n, (base, _, _, _) in self.out_stage.items():
+            o.append(f'{I}      stcs(rb_S, {self.g[self.root(n)]} + r_ * {P} + p0_ + i_, sh_f[{base} + e_]);')
+        o.append(f'{I}    }}')
+        o.append(f'{I}  }}')
+        o.append(f'{I}}}')
 
     def epi_only(self, n, fused_ids):
         """Is value n read only by the statements fused into this epilogue?"""
