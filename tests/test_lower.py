@@ -93,7 +93,10 @@ def test_gpt2_small_b8_plan():
     assert p['mx'] == p['_h1'] == p['o'] == 'attention[bt, h]'
     # several rows: the streams with 8+ points per block run on the matrix cores
     assert p['qkv'] == 'stream (transposed copy) mfma +2 fused' and p['logit'] == 'stream mfma'
-    assert p['u'].endswith('mfma +1 fused') and p['z2'] == 'stream (transposed copy)'
+    assert p['u'].endswith('mfma +1 fused')
+    # few points per block: the fold is split over blocks too, partial tiles added
+    # into a fixed-point residual
+    assert p['z2'].startswith('stream (transposed copy) mfma, fold in 16 slices, fixed-point sum')
     assert low.barriers_per_launch <= 75
     assert low.scratch['logit'][2] == (8, 50257) and low.scratch['next'][2] == (8,)
 

@@ -383,6 +383,8 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
         self.peels = {}               # id(step) -> statement of its carry's first value, made where read
         self.peel_active = {}         # carry root -> (loop variable, that statement) inside the loop
         self.find_peels(stmts)
+        self.splits = {}              # id(stream statement) -> geometry of its fold split over blocks
+        self.find_splits(stmts)
         self.layout(stmts)
 
     # ------------------------------------------------------------ program facts
@@ -1249,10 +1251,12 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
         if r in self.glocal:
             off, plen = self.glocal[r]
             return self.lds_read(f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}]')
+        pv = self.peel_value(r, ix)
         if r in self.fx:
             i = f'{self.g[r]} + 2u * ({a})'
+            if pv is not None:
+                return f'({pv[0]} == 0 ? {pv[1]} : fxld(rb_S, {i}))'
             return self.captured(f'fxld(rb_S, {i})', 'float', r, raw=(f'ldfx_raw(rb_S, {i})', 'long long', 'vh_fx2f'))
-        pv = self.peel_value(r, ix)
         if pv is not None:
             return f'({pv[0]} == 0 ? {pv[1]} : ldcs(rb_S, {self.g[r]} + {a}))'
         return self.captured(f'ldcs(rb_S, {self.g[r]} + {a})', 'float', r)
@@ -1387,6 +1391,10 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
                     run.append(ss[i + len(run)])
                 self.gen_private(run, out, ind)
                 i += len(run)
+                continue
+            if id(s) in self.splits:
+                self.gen_stream_split(s, self.splits[id(s)], out, ind)
+                i += 1
                 continue
             if p in ('tile', 'lane'):
                 fused = self.fusable(ss, i)

@@ -316,3 +316,216 @@ class MfmaMixin:
         o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {al} + r_ * {SAB} + k8_ * 16) = l_;')
         o.append(f'{I}}}')
         o.append(f'{I}vh_lds_sync();')
+
+    # ------------------------------------------------------------ fold split over blocks
+    def split_of(self, s):
+        """A multi-row stream with too few points per block for a matrix tile
+        whose statement adds the sum to a base, y = BASE + fold sum k: A * W:
+        the fold is split over blocks too, each block multiplying a slice of A
+        into tiles of its point group, and the partial tiles are added into y
+        kept as a 64-bit fixed-point sum (exact: the order of the adds does not
+        change it), whose BASE is stored in the phase before. Returns the
+        geometry, or None."""
+        if s[0] != 'let' or self.place.get(id(s)) not in ('tile', 'lane'):
+            return None
+        c = self.info[id(s)]
+        st = self.stream_of(c)
+        if st is None:
+            return None
+        name, r = s[1], self.root(s[1])
+        R = self.size(c.reg_axes)
+        P = self.size(st.pts)
+        if not (self.res[st.src][1] == 'f16' and MFMA_ROWS_MIN <= R <= 16 and st.K % 32 == 0
+                and st.c0 % 8 == 0 and st.rowlen % 8 == 0):
+            return None
+        if -(-P // self.grid) >= MFMA_POINTS_MIN:
+            return None
+        if name in self.outputs or r in self.private or r in self.outputs or r in self.fx:
+            return None
+        if list(s[2]) != list(c.reg_axes) + list(st.pts) or list(self.axes_of[r]) != list(s[2]):
+            return None
+        if not self._additive(c.epi, ('name', '__acc'), '__acc'):
+            return None
+        if c.A[0] != 'idx' or c.A[1] not in self.axes_of:
+            return None
+        # point groups of NTS tiles, the fold in KS slices: the fewest bytes per block
+        NKB, K = st.K // 32, st.K
+        best = None
+        for NTS in range(1, 5):
+            NPG = -(-P // (16 * NTS))
+            KS = min(self.grid // NPG, NKB)
+            if KS < 2:
+                continue
+            KSL = -(-NKB // KS)
+            cost = R * KSL * 32 * 4 + 16 * NTS * KSL * 32 * 2
+            if best is None or cost < best[0]:
+                best = (cost, NTS, NPG, KS, KSL)
+        if best is None:
+            return None
+        _, NTS, NPG, KS, KSL = best
+        base = self.rebuild_expr(c.epi, lambda n: ('num', 0.0) if n == ('name', '__acc') else n)
+        return dict(c=c, st=st, NTS=NTS, NPG=NPG, KS=KS, KSL=KSL, PG=16 * NTS, base=base)
+
+    def find_splits(self, ss):
+        for s in ss:
+            if s[0] == 'step':
+                self.find_splits(s[6])
+                continue
+            sk = self.split_of(s)
+            if sk is not None:
+                self.splits[id(s)] = sk
+                self.fx.add(self.root(s[1]))
+
+    def gen_stream_split(self, s, sk, out, ind):
+        c, st = sk['c'], sk['st']
+        name, z = s[1], self.root(s[1])
+        reg = list(c.reg_axes)
+        R, P, K, NKB = self.size(reg), self.size(st.pts), st.K, st.K // 32
+        NTS, NPG, KS, KSL, PG = sk['NTS'], sk['NPG'], sk['KS'], sk['KSL'], sk['PG']
+        NW = self.NWAVE - 1
+        if NTS >= NW:
+            TPW, KW = -(-NTS // NW), 1
+        else:
+            TPW, KW = 1, NW // NTS
+        KBW = -(-KSL // KW)
+        # the base, everywhere, in the phase before
+        axes = list(s[2])
+        breads = self.root_reads([sk['base']])
+        self.sync(breads, {z}, out, ind, f'{name} base')
+        self.plan.append((self.show_stmt(s), f'stream (transposed copy) mfma, fold in {KS} slices, '
+                          'fixed-point sum: base in the phase before'))
+        I = ind + '  '
+        out.append(f'{ind}for (int p_ = (int)blockIdx.x + (int)nblk * tid; p_ < {self.count_c(axes)}; '
+                   f'p_ += nthr) {{  // {name} base')
+        env = self.decode('p_', axes, out, I)
+        pre = []
+        v, t = self.expr(sk['base'], env, pre, I)
+        out += pre
+        out.append(f'{I}{self.store(z, [env[a][0] for a in axes], v, t)}')
+        out.append(f'{ind}}}')
+        self.note(breads, {z})
+        self.mark(out, ind, f'{name} base')
+        reads = self.root_reads([c.A]) | {n for n in self.root_reads([s[3]]) if n != z}
+        self.sync(reads, {z}, out, ind, name)
+        sid = self.fresh('k')
+        rr, rs = self.rsrc(st.src), self.res_strides(st.src)
+        role = [f'const int sg_ = (int)blockIdx.x / {KS}, ss_ = (int)blockIdx.x % {KS};',
+                f'const int kb0_ = ss_ * {NKB} / {KS}, nk_ = (ss_ + 1) * {NKB} / {KS} - kb0_;',
+                f'const bool mok_ = (int)blockIdx.x < {NPG * KS} && wave < {NTS * KW};',
+                f'const int mkp_ = wave / {NTS}, mt_ = wave % {NTS};' if KW > 1 else
+                f'const int mkp_ = 0, mt_ = wave;',
+                f'const int mk0_ = mkp_ * nk_ / {KW}, mk1_ = (mkp_ + 1) * nk_ / {KW};']
+
+        def tile(i):
+            return f'mt_ + {i * NW}' if i else 'mt_'
+
+        def wload(i, kb, dst, cond):
+            lines = [f'{{ const int n_ = ({tile(i)}) * 16 + (lane & 15);',
+                     f'  const int p_ = sg_ * {PG} + n_;',
+                     f'  if (mok_ && ({cond}) && ({tile(i)}) < {NTS} && p_ < {P}) {{']
+            env = self.decode('p_', st.pts, lines, '    ', prefix='sp_')
+            pre = []
+            ix = [self.index(x, env, pre, '    ') for x in st.prefix_idx]
+            lines += pre
+            base = self.addr(ix, rs[:-1]) if ix else '0'
+            lines.append(f'    {dst} = ldg16_nt({rr}, (unsigned)({base}) + {st.c0}u + '
+                         f'(unsigned)((kb0_ + {kb}) * 32 + (lane >> 4) * 8));')
+            lines.append(f'  }} else {dst} = vh_u32x4{{0u, 0u, 0u, 0u}};')
+            lines.append('}')
+            return lines
+
+        wm = f'wm_{sid}'
+        self.decls.append(f'vh_u32x4 {wm}[{TPW}][{KBW}];')
+
+        def make(step_override):
+            saved = self.override_step(step_override)
+            try:
+                lines = [f'if (wave < {NW}) {{'] + ['  ' + x for x in role]
+                for i in range(TPW):
+                    for j in range(KBW):
+                        lines += ['  ' + x for x in wload(i, f'mk0_ + {j}', f'{wm}[{i}][{j}]', f'mk0_ + {j} < mk1_')]
+                return lines + ['}']
+            finally:
+                self.restore_step(saved)
+        self.place_prefetch(make, out, ind)
+        o = out
+        o.append(f'{ind}{{  // stream {name} on the matrix cores, fold in {KS} slices: {P} points x {K} from '
+                 f'{st.src}, rows={R}, {PG} points and {KSL} k-blocks per block, waves/tile={KW}')
+        o += [I + x for x in role]
+        top = self.lds_floats + self.stage_top
+        direct = self.direct_lds(c, reg)
+        src = None if direct is not None else self.mfma_global_src(c, reg, K)
+        if direct is None and src is None:
+            self.stage_A(c, reg, 0, R, R, K, str(top), o, I)
+            direct, top = str(top), top + R * K
+        SAB = KSL * 64 + 16
+        ah = top * 4
+        al = ah + R * SAB
+        top = (al + R * SAB) // 4
+        red = top
+        top += NW * 64 * 4 if KW > 1 else 0
+        self.stage_floats = max(self.stage_floats, top - self.lds_floats)
+        # the block's slice of the other factor into fp16 halves
+        K8 = KSL * 4
+        o.append(f'{I}vh_lds_sync();')
+        o.append(f'{I}for (int e_ = tid; e_ < {R * K8}; e_ += {self.BLOCK}) {{')
+        o.append(f'{I}  const int r_ = e_ / {K8}, k8_ = e_ - r_ * {K8};')
+        o.append(f'{I}  float v_[8] = {{0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f}};')
+        o.append(f'{I}  if (k8_ < nk_ * 4) {{')
+        o.append(f'{I}    const int col_ = kb0_ * 32 + k8_ * 8;')
+        if direct is not None:
+            o.append(f'{I}    const float* s_ = sh_f + {direct} + r_ * {K} + col_;')
+            o.append(f'{I}    {self.lds_vec_load(8, "s_", "v_")}')
+        else:
+            o.append(f'{I}    const vh_f32x4 x0_ = ldc4(rb_S, {src}u + (unsigned)(r_ * {K} + col_)), '
+                     f'x1_ = ldc4(rb_S, {src}u + (unsigned)(r_ * {K} + col_ + 4));')
+            o.append(f'{I}    v_[0] = x0_.x; v_[1] = x0_.y; v_[2] = x0_.z; v_[3] = x0_.w; '
+                     f'v_[4] = x1_.x; v_[5] = x1_.y; v_[6] = x1_.z; v_[7] = x1_.w;')
+        o.append(f'{I}  }}')
+        o.append(f'{I}  vh_u32x4 h_, l_;')
+        o.append(f'{I}  vh_split8(v_, h_, l_);')
+        o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {ah} + r_ * {SAB} + k8_ * 16) = h_;')
+        o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {al} + r_ * {SAB} + k8_ * 16) = l_;')
+        o.append(f'{I}}}')
+        o.append(f'{I}vh_lds_sync();')
+        self.mark(o, I, f'stream {name}: halves')
+        o.append(f'{I}vh_f32x4 acc_[{TPW}];')
+        o.append(f'{I}#pragma unroll')
+        o.append(f'{I}for (int i_ = 0; i_ < {TPW}; ++i_) acc_[i_] = vh_f32x4{{0.f, 0.f, 0.f, 0.f}};')
+        o.append(f'{I}if (mok_) {{')
+        for j in range(KBW):
+            o.append(f'{I}  if (mk0_ + {j} < mk1_) {{')
+            o.append(f'{I}    const int ar_ = lane & 15, ak_ = (mk0_ + {j}) * 32 + (lane >> 4) * 8;')
+            o.append(f'{I}    const vh_u32x4 ah_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {ah} + ar_ * {SAB} '
+                     f'+ ak_ * 2) : vh_u32x4{{0u, 0u, 0u, 0u}};')
+            o.append(f'{I}    const vh_u32x4 al_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {al} + ar_ * {SAB} '
+                     f'+ ak_ * 2) : vh_u32x4{{0u, 0u, 0u, 0u}};')
+            for i in range(TPW):
+                o.append(f'{I}    acc_[{i}] = vh_mfma(ah_, {wm}[{i}][{j}], acc_[{i}]);')
+                o.append(f'{I}    acc_[{i}] = vh_mfma(al_, {wm}[{i}][{j}], acc_[{i}]);')
+            o.append(f'{I}  }}')
+        o.append(f'{I}}}')
+        self.mark(o, I, f'stream {name}: products')
+        if KW > 1:
+            o.append(f'{I}if (mok_ && mkp_ > 0) *(vh_f32x4*)(sh_f + {red} + (wave * 64 + lane) * 4) = acc_[0];')
+            o.append(f'{I}vh_lds_sync();')
+            o.append(f'{I}if (mok_ && mkp_ == 0) {{')
+            for q in range(1, KW):
+                o.append(f'{I}  acc_[0] += *(const vh_f32x4*)(sh_f + {red} + ((wave + {q * NTS}) * 64 + lane) * 4);')
+            o.append(f'{I}}}')
+        # the partial tiles into the fixed-point sum
+        o.append(f'{I}if (mok_ && mkp_ == 0) {{')
+        for i in range(TPW):
+            o.append(f'{I}  {{ const int p_ = sg_ * {PG} + ({tile(i)}) * 16 + (lane & 15);')
+            o.append(f'{I}    if (({tile(i)}) < {NTS} && p_ < {P}) {{')
+            o.append(f'{I}      #pragma unroll')
+            o.append(f'{I}      for (int v_ = 0; v_ < 4; ++v_) {{')
+            o.append(f'{I}        const int r_ = (lane >> 4) * 4 + v_;')
+            o.append(f'{I}        if (r_ < {R}) fxadd(S, {self.g[z]}u + 2u * (unsigned)(r_ * {P} + p_), acc_[{i}][v_]);')
+            o.append(f'{I}      }}')
+            o.append(f'{I}    }}')
+            o.append(f'{I}  }}')
+        o.append(f'{I}}}')
+        o.append(f'{ind}}}')
+        self.note(reads, {z})
+        self.mark(out, ind, f'stream {name}')
