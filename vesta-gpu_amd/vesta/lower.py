@@ -74,6 +74,9 @@ BLOCK = WAVE * NWAVE          # threads per block: two waves per SIMD, one block
 KCAP = 32                     # split-K: at most this many partials per tile column block
 GRID_MAX = 1024               # grid reductions keep one partial per block, for up to this many blocks
 GRID_DEFAULT = 256            # blocks per launch: one per CU of an MI355X
+GRID_FEW_ROWS = 128           # ... with fewer than 4 rows, where a step is a chain of grid barriers whose
+                              # release slows with the number of blocks polling them (measured: B=1 255 us
+                              # per step on 128 blocks, 265 on 160, 307 on 256)
 REG_MAX = 8                   # register axes: at most this many accumulator rows per lane
 PRIV_SIZE = 8192              # a private value holds at most this many floats
 PRIV_WORK = 1 << 17           # ... and costs at most this many operations per block
@@ -349,7 +352,7 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
         self.step_env = {}
         self.fb_targets = set()
         self.inlined = []
-        self.grid = int(grid or GRID_DEFAULT)
+        self.grid = int(grid or (GRID_FEW_ROWS if batch < 4 else GRID_DEFAULT))
         self.packs = {}           # transposed copy -> the residue it is made from
         self.decls = []           # kernel-scope declarations (prefetch registers)
         self.pf_slots = []        # prefetch code per grid barrier
