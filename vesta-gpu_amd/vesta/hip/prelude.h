@@ -70,10 +70,35 @@ __device__ __forceinline__ float vh_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
 
+// Whole-wave combine without LDS: rows of 16 lanes as above, then row_bcast:15
+// adds lane 15 of rows 0 and 2 into rows 1 and 3, row_bcast:31 lane 31 into
+// rows 2 and 3, so lane 63 holds the wave's value; every lane gets it from there.
+#define VH_DPP_BCAST15 0x142
+#define VH_DPP_BCAST31 0x143
+template <int CTRL, int ROWS>
+__device__ __forceinline__ float vh_dpp_rows(float v, float ident) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, ident), __builtin_bit_cast(int, v),
+                                                               CTRL, ROWS, 0xF, false));
+}
+#define VH_WAVE_ALL(NAME, OP, IDENT)                                       \
+  __device__ __forceinline__ float NAME(float v) {                         \
+    v = OP(v, vh_dpp<VH_DPP_XOR1>(v));                                     \
+    v = OP(v, vh_dpp<VH_DPP_XOR2>(v));                                     \
+    v = OP(v, vh_dpp<VH_DPP_HALF_MIRROR>(v));                              \
+    v = OP(v, vh_dpp<VH_DPP_MIRROR>(v));                                   \
+    v = OP(v, vh_dpp_rows<VH_DPP_BCAST15, 0xA>(v, IDENT));                 \
+    v = OP(v, vh_dpp_rows<VH_DPP_BCAST31, 0xC>(v, IDENT));                 \
+    return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63)); \
+  }
+VH_WAVE_ALL(wave_red_sum, op_sum, 0.0f)
+VH_WAVE_ALL(wave_red_max, op_max, -INFINITY)
+VH_WAVE_ALL(wave_red_min, op_min, INFINITY)
+
 // Combine over groups of `width` consecutive lanes (width a power of two
 // <= 64): afterwards every lane of a group holds the group's value.
-#define VH_GROUP_RED(NAME, OP)                                             \
+#define VH_GROUP_RED(NAME, OP, ALL)                                        \
   __device__ __forceinline__ float NAME(float v, int width) {              \
+    if (width >= 64) return ALL(v);                                        \
     if (width >= 2) v = OP(v, vh_dpp<VH_DPP_XOR1>(v));                     \
     if (width >= 4) v = OP(v, vh_dpp<VH_DPP_XOR2>(v));                     \
     if (width >= 8) v = OP(v, vh_dpp<VH_DPP_HALF_MIRROR>(v));              \
@@ -82,9 +107,9 @@ __device__ __forceinline__ float vh_dpp(float v) {
     if (width >= 64) v = OP(v, __shfl_xor(v, 32, 64));                     \
     return v;                                                              \
   }
-VH_GROUP_RED(group_red_sum, op_sum)
-VH_GROUP_RED(group_red_max, op_max)
-VH_GROUP_RED(group_red_min, op_min)
+VH_GROUP_RED(group_red_sum, op_sum, wave_red_sum)
+VH_GROUP_RED(group_red_max, op_max, wave_red_max)
+VH_GROUP_RED(group_red_min, op_min, wave_red_min)
 
 // Combine over lane bits [lo, 64) (lo a power of two): lanes that differ only
 // in those bits end with the same value, each group of lo consecutive lanes
@@ -103,9 +128,7 @@ VH_WAVE_RED(wave_red_sum_hi, op_sum)
 VH_WAVE_RED(wave_red_max_hi, op_max)
 VH_WAVE_RED(wave_red_min_hi, op_min)
 
-__device__ __forceinline__ float wave_red_sum(float v) { return group_red_sum(v, 64); }
-__device__ __forceinline__ float wave_red_max(float v) { return group_red_max(v, 64); }
-__device__ __forceinline__ float wave_red_min(float v) { return group_red_min(v, 64); }
+
 
 // Block barrier for LDS traffic only: waits for this wave's LDS operations,
 // not for its global loads (loads issued ahead of time stay in flight).

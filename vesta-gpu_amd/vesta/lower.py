@@ -2311,20 +2311,39 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
         I = ind + '  '
         env = self.decode('p_', axes, o, I)
         o.append(f'{I}float a_ = {FOLD_INIT[op]};')
-        o.append(f'{I}#pragma unroll' + ('' if T <= 16 else ' 8'))
-        o.append(f'{I}for (int it_ = 0; it_ < {T}; ++it_) {{')
-        o.append(f'{I}  const int k_ = lane + it_ * {WAVE};')
-        o.append(f'{I}  if (k_ < {self.ext_c(ax)}) {{')
-        pre = []
-        self.in_fold = True
-        try:
-            v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '    ')
-        finally:
-            self.in_fold = False
-        o += pre
-        o.append(f'{I}    a_ = {FOLD_OP[op]}(a_, {self.as_float(v, t)});')
-        o.append(f'{I}  }}')
-        o.append(f'{I}}}')
+        full = K // WAVE if ax not in self.dynamic else 0
+        if 0 < full <= 16:
+            # whole rounds unrolled here with every LDS read issued before the sums
+            loads, comp = [], []
+            self.in_fold = True
+            try:
+                for it in range(full):
+                    self.lcap = {'prefix': f'lf{it}_', 'loads': [], 'dedupe': {}}
+                    pre = []
+                    v, t = self.expr(body, {**env, ax: (f'(lane + {it * WAVE})', 'int')}, pre, I)
+                    loads += [f'{I}const float {n} = {x};' for n, x in self.lcap['loads']]
+                    self.lcap = None
+                    comp += pre + [f'{I}a_ = {FOLD_OP[op]}(a_, {self.as_float(v, t)});']
+            finally:
+                self.in_fold = False
+                self.lcap = None
+            o += loads + comp
+        if full * WAVE < K or not 0 < full <= 16:
+            start = full if 0 < full <= 16 else 0
+            o.append(f'{I}#pragma unroll' + ('' if T <= 16 else ' 8'))
+            o.append(f'{I}for (int it_ = {start}; it_ < {T}; ++it_) {{')
+            o.append(f'{I}  const int k_ = lane + it_ * {WAVE};')
+            o.append(f'{I}  if (k_ < {self.ext_c(ax)}) {{')
+            pre = []
+            self.in_fold = True
+            try:
+                v, t = self.expr(body, {**env, ax: ('k_', 'int')}, pre, I + '    ')
+            finally:
+                self.in_fold = False
+            o += pre
+            o.append(f'{I}    a_ = {FOLD_OP[op]}(a_, {self.as_float(v, t)});')
+            o.append(f'{I}  }}')
+            o.append(f'{I}}}')
         o.append(f'{I}a_ = wave_red_{op}(a_);')
         o.append(f'{I}if (lane == 0) {self.store(name, [env[a][0] for a in axes], "a_", "float")}')
         o.append(f'{ind}}}')
