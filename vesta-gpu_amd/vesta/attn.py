@@ -210,23 +210,12 @@ class AttnMixin:
         return walk(e)
 
     def gen_proj_base(self, pj, out, ind):
-        """z1 = BASE at every point, spread over all blocks (a few threads each)."""
-        sz, base = pj['sz'], pj['base']
-        z1, axes = sz[1], list(sz[2])
-        reads = self.root_reads([base])
-        self.sync(reads, {z1}, out, ind, f'{z1} base')
-        self.plan.append((self.show_stmt(sz), 'fixed-point sum: base here, projection adds'))
-        I = ind + '  '
-        out.append(f'{ind}for (int p_ = (int)blockIdx.x + (int)nblk * tid; p_ < {self.count_c(axes)}; '
-                   f'p_ += nthr) {{  // {z1} base')
-        env = self.decode('p_', axes, out, I)
-        pre = []
-        v, t = self.expr(base, env, pre, I)
-        out += pre
-        out.append(f'{I}{self.store(z1, [env[a][0] for a in axes], v, t)}')
-        out.append(f'{ind}}}')
-        self.note(reads, {z1})
-        self.mark(out, ind, f'{z1} base')
+        """z1 = BASE at every point, spread over all blocks (a few threads
+        each), unless a private run before did it."""
+        sz = pj['sz']
+        if pj.get('base_done'):
+            return
+        self.emit_base(sz, sz[1], list(sz[2]), pj['base'], out, ind, sync=True)
 
     def _reads_at(self, e, allowed):
         """Does e read group values only at the given index lists (and no folds)?"""

@@ -1392,7 +1392,7 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
                 while i + len(run) < len(ss) and ss[i + len(run)][0] == 'let' \
                         and self.place.get(id(ss[i + len(run)])) == 'private':
                     run.append(ss[i + len(run)])
-                self.gen_private(run, out, ind)
+                self.gen_private(run, out, ind, self.base_after(ss, i + len(run)))
                 i += len(run)
                 continue
             if id(s) in self.splits:
@@ -2026,7 +2026,45 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
         o.append(f'{ind}}}')
 
     # -- private
-    def gen_private(self, run, out, ind):
+    def base_after(self, ss, j):
+        """The fixed-point base the next site of this phase will store (an
+        attention with its projection, or a stream split over its fold), if
+        only contractions and their epilogues come between: (statement for the
+        plan or None, target, axes, expression, the site's description)."""
+        for t in ss[j:]:
+            if id(t) in self.proj:
+                pj = self.proj[id(t)]
+                return pj['sz'], pj['sz'][1], list(pj['sz'][2]), pj['base'], pj
+            if id(t) in self.splits:
+                sk = self.splits[id(t)]
+                return None, self.root(t[1]), list(t[2]), sk['base'], sk
+            if t[0] == 'emit' or (t[0] == 'let' and self.place.get(id(t)) in ('tile', 'lane', 'epilogue')
+                                  and id(t) not in self.groups):
+                continue
+            return None
+        return None
+
+    def emit_base(self, shown, z, axes, base, out, ind, sync):
+        """z = base at every point (z a fixed-point sum that a later site adds
+        into), spread over all blocks, a few threads each."""
+        reads = self.root_reads([base])
+        if sync:
+            self.sync(reads, {z}, out, ind, f'{z} base')
+        if shown is not None:
+            self.plan.append((show_stmt(shown), 'fixed-point sum: base here, projection adds'))
+        I = ind + '  '
+        out.append(f'{ind}for (int p_ = (int)blockIdx.x + (int)nblk * tid; p_ < {self.count_c(axes)}; '
+                   f'p_ += nthr) {{  // {z} base')
+        env = self.decode('p_', axes, out, I)
+        pre = []
+        v, t = self.expr(base, env, pre, I)
+        out += pre
+        out.append(f'{I}{self.store(z, [env[a][0] for a in axes], v, t)}')
+        out.append(f'{ind}}}')
+        self.note(reads, {z})
+        self.mark(out, ind, f'{z} base')
+
+    def gen_private(self, run, out, ind, fx_base=None):
         reads = self.root_reads([t[3] for t in run], exclude={t[1] for t in run})
         self.sync(reads, set(), out, ind, run[0][1])
         out.append(f'{ind}vh_lds_sync();')
@@ -2103,6 +2141,16 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
                 o.append(f'{I}}}')
                 o.append(f'{ind}}}')
             self.mark(out, ind, f'private {name}')
+        if fx_base is not None:
+            # the next site's fixed-point base, from the values staged here
+            # (early in the phase, so its loads and stores are not on the path
+            # to the phase's end), when nothing read or wrote its target since
+            # the last barrier
+            shown, z, axes, bexpr, info = fx_base
+            if (z not in self.readers and z not in self.dirty
+                    and not (self.root_reads([bexpr]) & self.dirty)):
+                self.emit_base(shown, z, axes, bexpr, out, ind, sync=False)
+                info['base_done'] = True
         out.append(f'{ind}vh_lds_sync();')
         self.staged = {}
 

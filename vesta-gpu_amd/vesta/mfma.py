@@ -389,22 +389,11 @@ class MfmaMixin:
             TPW, KW = 1, NW // NTS
         KBW = -(-KSL // KW)
         # the base, everywhere, in the phase before
-        axes = list(s[2])
-        breads = self.root_reads([sk['base']])
-        self.sync(breads, {z}, out, ind, f'{name} base')
         self.plan.append((self.show_stmt(s), f'stream (transposed copy) mfma, fold in {KS} slices, '
                           'fixed-point sum: base in the phase before'))
+        if not sk.get('base_done'):
+            self.emit_base(None, z, list(s[2]), sk['base'], out, ind, sync=True)
         I = ind + '  '
-        out.append(f'{ind}for (int p_ = (int)blockIdx.x + (int)nblk * tid; p_ < {self.count_c(axes)}; '
-                   f'p_ += nthr) {{  // {name} base')
-        env = self.decode('p_', axes, out, I)
-        pre = []
-        v, t = self.expr(sk['base'], env, pre, I)
-        out += pre
-        out.append(f'{I}{self.store(z, [env[a][0] for a in axes], v, t)}')
-        out.append(f'{ind}}}')
-        self.note(breads, {z})
-        self.mark(out, ind, f'{name} base')
         reads = self.root_reads([c.A]) | {n for n in self.root_reads([s[3]]) if n != z}
         self.sync(reads, {z}, out, ind, name)
         sid = self.fresh('k')
