@@ -104,6 +104,60 @@ def test_batch8_rows_match_oracle(small):
         assert (nx[:, r] == onx).all() or all(mg < 1e-3 for a, b, mg in zip(nx[:, r], onx, marg) if a != b)
 
 
+@pytest.mark.parametrize('B', [4, 8])
+def test_matrix_core_rows_long_context_match_oracle(small, B):
+    """Batches on the matrix-core streams (B >= 4: MFMA tiles, the feed-forward
+    down-projection split over its fold into a fixed-point residual) with the
+    context past two attention slots of 56 positions: prompt and generated
+    tokens in one-launch prefill and one multi-step launch, logits of the
+    last step and every token against the oracle run on the GPU's inputs."""
+    torch = _torch()
+    from oracle import decode
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import random_prompts
+    hf, W, text = small
+    P, G, T = 100, 24, 128
+    m = VestaGPT2(hf, batch=B, tmax=T)
+    m.reset()
+    pr = random_prompts(B, P, 50257, seed=11 + B)
+    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32))
+    torch.cuda.synchronize()
+    first = m.x.cpu().numpy().copy()
+    hist = torch.zeros((G - 1) * B, dtype=torch.int32, device='cuda')
+    m.step(G - 1, hist)
+    torch.cuda.synchronize()
+    gen = np.concatenate([first[None], hist.view(G - 1, B).cpu().numpy()])     # [G, B]
+    last = m.logits().float().cpu().numpy()                                       # after step P + G - 2
+    for r in range(B):
+        inputs = np.concatenate([pr[r], gen[:-1, r]])                             # what step i saw
+        onx, olog, marg = decode.teacher_forced(text, W, inputs, T)
+        assert np.abs(last[r] - olog[-1]).max() < LOGIT_TOL, r
+        want = onx[P - 1:]
+        bad = [k for k in range(G) if gen[k, r] != want[k] and marg[P - 1 + k] >= 1e-3]
+        assert not bad, (r, bad)
+
+
+def test_batch8_launches_are_bit_reproducible(small):
+    """Values several blocks add into are exact fixed-point sums, so two runs
+    of the same launch give the same bits (logits and cache)."""
+    torch = _torch()
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import random_prompts
+    hf, _, _ = small
+    B = 8
+    m = VestaGPT2(hf, batch=B, tmax=64)
+    pr = torch.from_numpy(random_prompts(B, 20, 50257, seed=5)).to('cuda', torch.int32)
+    outs = []
+    for _ in range(2):
+        m.reset()
+        m.prefill(pr)
+        m.step(8)
+        torch.cuda.synchronize()
+        outs.append((m.logits().clone(), m.keys.clone(), m.x.clone()))
+    assert torch.equal(outs[0][0], outs[1][0])
+    assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
+
+
 def test_multistep_launch_and_prefill_match_single_steps(small):
     torch = _torch()
     from vesta.gpt2 import VestaGPT2
