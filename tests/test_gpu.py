@@ -137,6 +137,65 @@ def test_matrix_core_rows_long_context_match_oracle(small, B):
         assert not bad, (r, bad)
 
 
+def _prefill_and_generate(m, pr, G):
+    """Prompt in one launch, G - 1 more steps in one launch: generated tokens
+    [G, B] and the logits of the last step."""
+    torch = _torch()
+    B = pr.shape[0]
+    m.reset()
+    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32))
+    torch.cuda.synchronize()
+    first = m.x.cpu().numpy().copy()
+    hist = torch.zeros((G - 1) * B, dtype=torch.int32, device='cuda')
+    m.step(G - 1, hist)
+    torch.cuda.synchronize()
+    return np.concatenate([first[None], hist.view(G - 1, B).cpu().numpy()]), m.logits().float().cpu().numpy()
+
+
+def _check_rows(text, W, pr, gen, last, T, rows):
+    from oracle import decode
+    P, G = pr.shape[1], gen.shape[0]
+    for r in rows:
+        inputs = np.concatenate([pr[r], gen[:-1, r]])
+        onx, olog, marg = decode.teacher_forced(text, W, inputs, T)
+        assert np.abs(last[r] - olog[-1]).max() < LOGIT_TOL, r
+        bad = [k for k in range(G) if gen[k, r] != onx[P - 1 + k] and marg[P - 1 + k] >= 1e-3]
+        assert not bad, (r, bad)
+
+
+@pytest.mark.slow
+def test_medium_long_context_matches_oracle():
+    """GPT-2 medium (configs[3] shape, 24 layers, d 1024, 16 heads) at B=1 with
+    a 512-position cache: more attention slots than registers hold, so the
+    softmax runs over chunks of positions (running maximum and sum)."""
+    from oracle import decode
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import RandomGPT2, random_prompts, stacked
+    hf = RandomGPT2('medium', 0)
+    W = decode.oracle_weights(stacked(hf.numpy_state(), 24))
+    text = open(os.path.join(PKG, 'vesta', 'programs', 'gpt2_medium.vst')).read()
+    T = 512
+    m = VestaGPT2(hf, batch=1, tmax=T)
+    pr = random_prompts(1, 70, 50257, seed=21)
+    gen, last = _prefill_and_generate(m, pr, 6)
+    _check_rows(text, W, pr, gen, last, T, [0])
+
+
+@pytest.mark.slow
+def test_batch32_long_cache_matches_oracle(small):
+    """configs[2]'s batch (32 rows: more (row, head) points than blocks, the
+    out-projection as its own stream, contractions on VALU row chunks) with a
+    512-position cache (chunked softmax), rows checked against the oracle."""
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import random_prompts
+    hf, W, text = small
+    T = 512
+    m = VestaGPT2(hf, batch=32, tmax=T)
+    pr = random_prompts(32, 60, 50257, seed=23)
+    gen, last = _prefill_and_generate(m, pr, 5)
+    _check_rows(text, W, pr, gen, last, T, [0, 13, 31])
+
+
 def test_batch8_launches_are_bit_reproducible(small):
     """Values several blocks add into are exact fixed-point sums, so two runs
     of the same launch give the same bits (logits and cache)."""

@@ -175,3 +175,19 @@ def test_c_abi_exports_every_declared_symbol():
         assert hasattr(lib, sym), sym
     lib.vh_error_string.restype = ctypes.c_char_p
     assert lib.vh_error_string(0) == b'success'
+
+
+@pytest.mark.parametrize('budget', [16, 32, 64])
+def test_chunked_attention_loads_every_slot(budget):
+    """Long caches run the softmax over chunks of slots; whatever the prefetch
+    register budget, every slot's key and value rows are loaded somewhere."""
+    import re as _re
+    from vesta.lower import lower
+    text = open(os.path.join(PKG, 'vesta', 'programs', 'gpt2.vst')).read()
+    low = lower(text, gpt2_spec(1, 512), {'s': 512}, batch=1, per_token=('x', 'keys', 'vals'),
+                outputs=('logit', 'next'), feedback={'x': 'next', 't': 1}, prefetch_vgprs=budget)
+    assert '// chunk 0' in low.src
+    for arr in ('kq', 'vq'):
+        name = _re.search(arr + r'_\w+\[10\];', low.src).group(0).split('[')[0]
+        loaded = {int(k) for k in _re.findall(_re.escape(name) + r'\[(\d+)\] = ldc16_h', low.src)}
+        assert loaded == set(range(10)), (arr, sorted(loaded))

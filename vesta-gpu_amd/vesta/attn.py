@@ -27,9 +27,9 @@ from __future__ import annotations
 
 import math
 
-from .stream import PREFETCH_VGPRS
 
 ATTN_PREFETCH_SLOTS = 8      # cache rows per lane issued early (K and V each)
+ATTN_CHUNK = 4               # longer contexts: slots per chunk of the running (online) softmax
 PROJ_MIN_REPLICAS = 2        # fuse the out-projection only if every leading point gets this many blocks
 PROJ_EARLY_SLOTS = 4         # projection weights issued at the barrier when a lane needs at most this many loads
 
@@ -254,7 +254,13 @@ class AttnMixin:
         PPP = NW * PPW                     # positions per block per slot
         smax = self.static[S]
         NPS = -(-smax // PPP)
-        NPF = min(NPS, ATTN_PREFETCH_SLOTS, PREFETCH_VGPRS // 8)
+        NPF = min(NPS, ATTN_PREFETCH_SLOTS, self.pf_budget // 8)
+        # more slots than registers hold: the softmax runs over chunks of slots
+        # (running maximum and sum, rescaled), the rows of the next chunk in
+        # flight while a chunk is used
+        online = NPS > ATTN_PREFETCH_SLOTS and self._softmax_form(at)
+        if online:
+            NPF = min(NPF, ATTN_CHUNK)          # the first chunk at the barrier, the rest streamed
         G = self.size(lead)
         R = pj['R'] if pj is not None else 1      # blocks per leading point (each redoes its attention)
         GR = G * R
@@ -372,7 +378,7 @@ class AttnMixin:
         # the step's own row (and every row when this is not the block's first point)
         el, ev = erow_c(lenv)
         o += [I + x for x in el]
-        for k in range(NPS):
+        for k in range(NPF if online else NPS):
             o.append(f'{I}{{ const int s{k}_ = {k * PPP} + wave * {PPW} + sub_;')
             if k < NPF:
                 o.append(f'{I}  if (!first_ || s{k}_ == ({ev}) || s{k}_ >= {T}) {{')
@@ -400,6 +406,18 @@ class AttnMixin:
         o += pre
         o.append(f'{I}  qv_[v_] = {self.as_float(qv, qt)};')
         o.append(f'{I}}}')
+        if online:
+            self.attn_online(at, o, I, lenv, NPS, NPF, PPP, PPW, LPE, NW, T, nE, kq, vq, slot_env, load_kv,
+                             red_o, pj, po_ref := [])
+            po = po_ref[0]
+            if pj is not None:
+                if not early:
+                    o += [I + x for x in proj_loads(lenv, 'rp_')]
+                self.gen_proj_tail(pj, lenv, lead, po, wp, NQP, NW, PPW, LPE, o, I)
+            o.append(f'{ind}}}' + ('}' if once else ''))
+            self.note(reads, writes)
+            self.mark(out, ind, f'attention {t1[1]}..{t4[1]}')
+            return
         # scores
         o.append(f'{I}float sk_[{NPS}];')
         o.append(f'{I}float mloc_ = -INFINITY;')
@@ -515,6 +533,127 @@ class AttnMixin:
             o.append(f'{J}}}')
         o.append(f'{I}}}')
         self.mark(o, I, 'attention: projection')
+
+    def _softmax_form(self, at):
+        """Are the statistics the max-subtracted softmax, F = exp(sc - mx) and
+        the weight A4 = F / hs (what the running form computes)?"""
+        t1, t2, t3, _ = at['t']
+        same = [('name', a) for a in at['lead'] + [at['S']]]
+        at_lead = [('name', a) for a in at['lead']]
+        F = ('call', 'exp', ('bin', '-', ('idx', t1[1], same), ('idx', t2[1], at_lead)))
+        return t3[3][3] == F and at['c4'].A == ('bin', '/', F, ('idx', t3[1], at_lead))
+
+    def attn_online(self, at, o, I, lenv, NPS, NPF, PPP, PPW, LPE, NW, T, nE, kq, vq, slot_env, load_kv,
+                    red_o, pj, po_ref):
+        """Scores, softmax and weighted values over chunks of ATTN_CHUNK slots:
+        each lane group keeps its positions' running maximum m, sum l of
+        exp(score - m) and weighted values (rescaled by exp(m_old - m_new) when
+        m grows); the groups of a wave, then the waves, are combined the same
+        way, and the values divided by the sum. The rows of chunk c + 1 are
+        loaded while chunk c is used. The query chunk qv_ is loaded already.
+        Writes the output to LDS (projection) or stores it; po_ref gets the
+        LDS offset."""
+        t1, t2, t3, t4 = at['t']
+        c1, c4 = at['c1'], at['c4']
+        CH = ATTN_CHUNK
+        NCH = -(-NPS // CH)
+        o.append(f'{I}float m_ = -INFINITY, l_ = 0.0f, ov_[8];')
+        o.append(f'{I}#pragma unroll')
+        o.append(f'{I}for (int v_ = 0; v_ < 8; ++v_) ov_[v_] = 0.0f;')
+        first = [k for k in range(min(NPS, CH)) if k >= NPF]
+        if first:
+            # the first chunk's slots not loaded at the barrier
+            for k in first:
+                o += [I + x for x in load_kv(k, lenv, False)]
+        for c in range(NCH):
+            ks = list(range(c * CH, min(NPS, (c + 1) * CH)))
+            nxt = [k for k in range((c + 1) * CH, min(NPS, (c + 2) * CH)) if k >= NPF]
+            if nxt:
+                o.append(f'{I}if ({(c + 1) * CH * PPP} < {T}) {{  // rows of chunk {c + 1}')
+                for k in nxt:
+                    o += [I + '  ' + x for x in load_kv(k, lenv, False)]
+                o.append(f'{I}}}')
+            o.append(f'{I}if ({c * CH * PPP} < {T}) {{  // chunk {c}')
+            J = I + '  '
+            for k in ks:
+                o.append(f'{J}float sk{k}_;')
+                o.append(f'{J}{{ const int s{k}_ = {k * PPP} + wave * {PPW} + sub_;')
+                o.append(f'{J}  float wf_[8];')
+                o.append(f'{J}  unpack8({kq}[{k}], wf_);')
+                o.append(f'{J}  float d_ = 0.0f;')
+                o.append(f'{J}  #pragma unroll')
+                o.append(f'{J}  for (int v_ = 0; v_ < 8; ++v_) d_ = fmaf(qv_[v_], wf_[v_], d_);')
+                o.append(f'{J}  d_ = group_red_sum(d_, {LPE});')
+                venv = dict(slot_env(k, lenv))
+                venv['__acc'] = ('d_', 'float')
+                pre = []
+                sv, st_ = self.expr(c1.epi, venv, pre, J + '  ')
+                o += pre
+                o.append(f'{J}  sk{k}_ = (wave < {NW} && s{k}_ < {T}) ? {self.as_float(sv, st_)} : -INFINITY;')
+                o.append(f'{J}}}')
+            o.append(f'{J}float mn_ = m_;')
+            for k in ks:
+                o.append(f'{J}mn_ = fmaxf(mn_, sk{k}_);')
+            o.append(f'{J}if (mn_ > -INFINITY) {{')
+            o.append(f'{J}  const float f_ = expf(m_ - mn_);')
+            o.append(f'{J}  l_ *= f_;')
+            o.append(f'{J}  #pragma unroll')
+            o.append(f'{J}  for (int v_ = 0; v_ < 8; ++v_) ov_[v_] *= f_;')
+            for k in ks:
+                o.append(f'{J}  {{ const float p_ = sk{k}_ > -INFINITY ? expf(sk{k}_ - mn_) : 0.0f;')
+                o.append(f'{J}    l_ += p_;')
+                o.append(f'{J}    float wf_[8];')
+                o.append(f'{J}    unpack8({vq}[{k}], wf_);')
+                o.append(f'{J}    #pragma unroll')
+                o.append(f'{J}    for (int v_ = 0; v_ < 8; ++v_) ov_[v_] = fmaf(p_, wf_[v_], ov_[v_]);')
+                o.append(f'{J}  }}')
+            o.append(f'{J}  m_ = mn_;')
+            o.append(f'{J}}}')
+            o.append(f'{I}}}')
+        self.mark(o, I, 'attention: chunks')
+        # the wave's lane groups, then the waves
+        o.append(f'{I}{{ const float M_ = wave_red_max_hi(m_, {LPE});')
+        o.append(f'{I}  const float f_ = m_ > -INFINITY ? expf(m_ - M_) : 0.0f;')
+        o.append(f'{I}  const float L_ = wave_red_sum_hi(l_ * f_, {LPE});')
+        o.append(f'{I}  #pragma unroll')
+        o.append(f'{I}  for (int v_ = 0; v_ < 8; ++v_) ov_[v_] = wave_red_sum_hi(ov_[v_] * f_, {LPE});')
+        red_m = red_o + NW * nE
+        po = red_m + 2 * 8
+        self.stage_floats = max(self.stage_floats, self.stage_top + NW * nE + 16 + nE)
+        o.append(f'{I}  if (wave < {NW} && sub_ == 0) {{')
+        o.append(f'{I}    #pragma unroll')
+        o.append(f'{I}    for (int v_ = 0; v_ < 8; ++v_) sh_f[{red_o} + wave * {nE} + cl_ * 8 + v_] = ov_[v_];')
+        o.append(f'{I}    if (lane == 0) {{ sh_f[{red_m} + wave] = M_; sh_f[{red_m + 8} + wave] = L_; }}')
+        o.append(f'{I}  }}')
+        o.append(f'{I}}}')
+        o.append(f'{I}vh_lds_sync();')
+        o.append(f'{I}if (tid < {nE}) {{')
+        o.append(f'{I}  float M_ = sh_f[{red_m}];')
+        o.append(f'{I}  #pragma unroll')
+        o.append(f'{I}  for (int w_ = 1; w_ < {NW}; ++w_) M_ = fmaxf(M_, sh_f[{red_m} + w_]);')
+        o.append(f'{I}  float L_ = 0.0f, a_ = 0.0f;')
+        o.append(f'{I}  #pragma unroll')
+        o.append(f'{I}  for (int w_ = 0; w_ < {NW}; ++w_) {{')
+        o.append(f'{I}    const float mw_ = sh_f[{red_m} + w_];')
+        o.append(f'{I}    const float f_ = mw_ > -INFINITY ? expf(mw_ - M_) : 0.0f;')
+        o.append(f'{I}    L_ = fmaf(sh_f[{red_m + 8} + w_], f_, L_);')
+        o.append(f'{I}    a_ = fmaf(sh_f[{red_o} + w_ * {nE} + tid], f_, a_);')
+        o.append(f'{I}  }}')
+        o.append(f'{I}  a_ = a_ / L_;')
+        fenv = dict(lenv)
+        fenv[at['E4']] = ('tid', 'int')
+        fenv['__acc'] = ('a_', 'float')
+        pre = []
+        ov, ot = self.expr(c4.epi, fenv, pre, I + '  ')
+        o += pre
+        if pj is None:
+            o.append(f'{I}  {self.store(t4[1], [fenv[a][0] for a in t4[2]], ov, ot)}')
+        else:
+            o.append(f'{I}  sh_f[{po} + tid] = {self.as_float(ov, ot)};')
+        o.append(f'{I}}}')
+        o.append(f'{I}vh_lds_sync();')
+        self.mark(o, I, 'attention: combine')
+        po_ref.append(po)
 
     def _subst(self, e, repl):
         """e with reads of the named group values replaced by C variables:

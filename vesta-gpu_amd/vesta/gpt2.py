@@ -19,7 +19,7 @@ from __future__ import annotations
 
 from . import PROGRAMS
 from .gpt2_program import gpt2_program
-from .launch import TORCH_DT, Kernel
+from .launch import TORCH_DT, Kernel, lower_fitted
 from .lower import lower
 
 SHAPE_PROGRAMS = {(12, 768, 12): 'gpt2.vst', (24, 1024, 16): 'gpt2_medium.vst', (48, 1600, 25): 'gpt2_xl.vst'}
@@ -89,7 +89,8 @@ class VestaGPT2:
                                              outputs=('logit', 'next'),
                                              feedback={'x': 'next', 't': 1} if feedback else None))
         self._R, self._bps, self._timing = R, blocks_per_sm, timing
-        self.low = lower(text, spec, **self._lower_args[2], timing=timing, kernel_name=f'vesta_step_b{batch}')
+        self.low = lower_fitted(lower, text, spec, **self._lower_args[2], timing=timing,
+                                kernel_name=f'vesta_step_b{batch}')
         self.k = Kernel(self.low, blocks_per_sm=blocks_per_sm)
         self.k.bind(R)
         self._kp = None
@@ -113,7 +114,7 @@ class VestaGPT2:
         warm-up (so profiles of the decode kernel hold decode launches only)."""
         if self._kp is None:
             text, spec, kw = self._lower_args
-            low = lower(text, spec, **kw, timing=self._timing, kernel_name=f'vesta_prefill_b{self.B}')
+            low = lower_fitted(lower, text, spec, **kw, timing=self._timing, kernel_name=f'vesta_prefill_b{self.B}')
             self._kp = Kernel(low, blocks_per_sm=self._bps)
             self._kp.bind(self._R)
         return self._kp

@@ -100,6 +100,35 @@ def compile_code(src: str, arch: str = ARCH, opts=RTC_OPTS, cache: bool = True) 
     return blob
 
 
+PREFETCH_BUDGETS = (64, 32, 16)   # registers per lane a site may prefetch into, tried in turn
+SPILLS_OK = 8                     # spilled registers a kernel may keep (outside its hot loops)
+
+
+def code_spills(code: bytes) -> int:
+    """The ``.vgpr_spill_count`` recorded in a code object's kernel metadata
+    (a MessagePack map: the key string, then an unsigned integer)."""
+    key = b'.vgpr_spill_count'
+    i = code.find(key)
+    if i < 0:
+        return 0
+    j = i + len(key)
+    b = code[j]
+    if b <= 0x7f:
+        return b
+    width = {0xcc: 1, 0xcd: 2, 0xce: 4, 0xcf: 8}.get(b)
+    return int.from_bytes(code[j + 1:j + 1 + width], 'big') if width else 0
+
+
+def lower_fitted(lower_fn, text, res, **kw):
+    """``lower_fn(text, res, **kw)`` with the largest prefetch register budget
+    whose kernel spills at most SPILLS_OK registers (compiling each try; the
+    code objects are cached, so the chosen one is not compiled again)."""
+    for budget in PREFETCH_BUDGETS:
+        low = lower_fn(text, res, prefetch_vgprs=budget, **kw)
+        if budget == PREFETCH_BUDGETS[-1] or code_spills(compile_code(low.src)) <= SPILLS_OK:
+            return low
+
+
 def device_info(dev: int = 0) -> dict:
     cu, coop, lds = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
     arch = ctypes.create_string_buffer(128)

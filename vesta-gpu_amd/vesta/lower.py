@@ -64,7 +64,7 @@ import numpy as np
 
 from .interp import parse
 from .attn import AttnMixin
-from .stream import StreamMixin
+from .stream import StreamMixin, PREFETCH_VGPRS
 from .mfma import MfmaMixin
 
 PRELUDE_PATH = Path(__file__).resolve().parent / 'hip' / 'prelude.h'
@@ -329,7 +329,7 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
     nodes_of = staticmethod(nodes)
     rebuild_expr = staticmethod(rebuild)
 
-    def __init__(self, stmts, res, axis_max, outputs, batch, timing=False, grid=None):
+    def __init__(self, stmts, res, axis_max, outputs, batch, timing=False, grid=None, prefetch_vgprs=None):
         self.res = {n: (tuple(int(x) for x in shp), dt) for n, (shp, dt) in res.items()}
         self.axis_max = dict(axis_max or {})
         self.outputs = set(outputs)
@@ -353,6 +353,7 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
         self.fb_targets = set()
         self.inlined = []
         self.grid = int(grid or (GRID_FEW_ROWS if batch < 4 else GRID_DEFAULT))
+        self.pf_budget = int(prefetch_vgprs or PREFETCH_VGPRS)   # registers per lane a site may prefetch into
         self.packs = {}           # transposed copy -> the residue it is made from
         self.decls = []           # kernel-scope declarations (prefetch registers)
         self.pf_slots = []        # prefetch code per grid barrier
@@ -2952,7 +2953,7 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
 
 
 def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None, timing=False,
-          kernel_name='vesta_step', grid=None):
+          kernel_name='vesta_step', grid=None, prefetch_vgprs=None):
     """Program text -> Lowered: HIP source of one persistent kernel.
 
     Kernel ABI: ``<kernel_name>(R_<residue>... in spec order, float* S,
@@ -2966,7 +2967,7 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
     the first launch and is left consistent by every launch.
     """
     stmts = batch_lift(parse(text), batch, set(per_token))
-    low = Lowering(stmts, res, axis_max, outputs, batch, timing, grid)
+    low = Lowering(stmts, res, axis_max, outputs, batch, timing, grid, prefetch_vgprs)
     for o in outputs:
         if o not in low.axes_of:
             raise NameError(f'output {o} is not a value of the program')

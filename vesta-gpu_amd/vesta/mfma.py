@@ -19,12 +19,10 @@ compute waves, wave w makes tiles w, w + NW, .. over the whole fold; with
 fewer, KW waves share a tile, each over its own range of the fold, and the
 partial tiles are added through LDS in wave order (a fixed order, so results
 do not depend on timing). The weights of a wave's share are loaded at the
-barrier before the site when they fit in PREFETCH_VGPRS registers, else
+barrier before the site when they fit in the prefetch register budget, else
 streamed MFMA_PIPE k-blocks ahead through two register sets.
 """
 from __future__ import annotations
-
-from .stream import PREFETCH_VGPRS
 
 MFMA_ROWS_MIN = 4            # rows from which a stream runs on the matrix cores
 MFMA_PIPE = 3                # k-blocks of weights in flight per tile when not prefetched
@@ -60,7 +58,7 @@ class MfmaMixin:
         else:
             TPW, KW = 1, NW // NT
         KBW = -(-NKB // KW)
-        prefetch = TPW * KBW * 4 <= PREFETCH_VGPRS
+        prefetch = TPW * KBW * 4 <= self.pf_budget
         sid = self.fresh('m')
         CT = NW * 64                          # the epilogue: one (row, point) item per compute thread
         NI = -(-(R * PPB) // CT)

@@ -28,7 +28,7 @@ from __future__ import annotations
 import math
 from dataclasses import dataclass
 
-PREFETCH_VGPRS = 64          # registers per lane one site may hold prefetched weights in
+PREFETCH_VGPRS = 64          # registers per lane one site may hold prefetched weights in (default budget)
 PI_STREAM = 4                # slots whose loads are issued together when not prefetched
 PB_MAX = 4                   # points one lane group makes at once (each LDS read of the other factor serves them all)
 PB_ACC = 32                  # ... holding at most this many partial sums per lane
@@ -188,7 +188,7 @@ class StreamMixin:
         nrch = -(-R // rch)
         ltype = self.load_type(dt, vec)
         vregs = -(-PPB // (NW * ppw)) * pl * max(1, vec * esz // 4)
-        prefetch = vregs <= PREFETCH_VGPRS
+        prefetch = vregs <= self.pf_budget
         # a long stream with several rows: a lane group makes PB points at once,
         # so each value of the other factor read from LDS serves PB weight
         # vectors (a short one keeps every wave busy instead)
