@@ -69,6 +69,19 @@ template <int CTRL>
 __device__ __forceinline__ float vh_dpp(float v) {
   return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
 }
+// Lanes i and i^16 (rows 0<->1, 2<->3), or i and i^32 (halves), both values in
+// every lane, through v_permlane16_swap / v_permlane32_swap (no LDS): swapping
+// v with itself gives rows (r0, r0, r2, r2) and (r1, r1, r3, r3), or halves
+// (h0, h0) and (h1, h1).
+#define VH_PAIR(NAME, SWAP)                                                            \
+  template <typename F>                                                               \
+  __device__ __forceinline__ float NAME(float v, F op) {                              \
+    const unsigned u = __builtin_bit_cast(unsigned, v);                               \
+    const auto p = SWAP(u, u, false, false);                                          \
+    return op(__builtin_bit_cast(float, (unsigned)p[0]), __builtin_bit_cast(float, (unsigned)p[1])); \
+  }
+VH_PAIR(vh_pair16, __builtin_amdgcn_permlane16_swap)
+VH_PAIR(vh_pair32, __builtin_amdgcn_permlane32_swap)
 
 // Whole-wave combine without LDS: rows of 16 lanes as above, then row_bcast:15
 // adds lane 15 of rows 0 and 2 into rows 1 and 3, row_bcast:31 lane 31 into
@@ -103,8 +116,7 @@ VH_WAVE_ALL(wave_red_min, op_min, INFINITY)
     if (width >= 4) v = OP(v, vh_dpp<VH_DPP_XOR2>(v));                     \
     if (width >= 8) v = OP(v, vh_dpp<VH_DPP_HALF_MIRROR>(v));              \
     if (width >= 16) v = OP(v, vh_dpp<VH_DPP_MIRROR>(v));                  \
-    if (width >= 32) v = OP(v, __shfl_xor(v, 16, 64));                     \
-    if (width >= 64) v = OP(v, __shfl_xor(v, 32, 64));                     \
+    if (width >= 32) v = vh_pair16(v, OP);                                 \
     return v;                                                              \
   }
 VH_GROUP_RED(group_red_sum, op_sum, wave_red_sum)
@@ -120,8 +132,8 @@ VH_GROUP_RED(group_red_min, op_min, wave_red_min)
     if (lo <= 2) v = OP(v, vh_dpp<VH_DPP_XOR2>(v));                        \
     if (lo <= 4) v = OP(v, __shfl_xor(v, 4, 64));                          \
     if (lo <= 8) v = OP(v, vh_dpp<VH_DPP_ROR8>(v));                        \
-    if (lo <= 16) v = OP(v, __shfl_xor(v, 16, 64));                        \
-    if (lo <= 32) v = OP(v, __shfl_xor(v, 32, 64));                        \
+    if (lo <= 16) v = vh_pair16(v, OP);                                    \
+    if (lo <= 32) v = vh_pair32(v, OP);                                    \
     return v;                                                              \
   }
 VH_WAVE_RED(wave_red_sum_hi, op_sum)
