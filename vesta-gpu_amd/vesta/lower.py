@@ -1344,7 +1344,7 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
         self.mark(out, ind, f'barrier before {what}')
 
     def mark(self, out, ind, label):
-        if not self.timing:
+        if self.timing is not True:
             # a site boundary the compiler keeps: code is not scheduled across
             # it, which keeps register live ranges inside their site
             out.append(f'{ind}asm volatile("");')
@@ -2958,7 +2958,10 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
 
     Kernel ABI: ``<kernel_name>(R_<residue>... in spec order, float* S,
     unsigned* bar, unsigned long long* TS, int nsteps, int* tok_out,
-    const int* tok_in)``. One launch runs ``nsteps`` steps back to back
+    const int* tok_in)``. ``timing``: True adds per-site clock sums (TS
+    [site][block]) and, after them, each block's arrival and release time at
+    the barriers of a launch's last step; 'trace' records only the latter (no
+    clock reads between barriers). One launch runs ``nsteps`` steps back to back
     (feedback between them; reference launches always run one). With token
     feedback, the token chosen at step k of the launch is stored in
     ``tok_out[k * B + b]`` when ``tok_out`` is not null, and when ``tok_in``
@@ -3047,7 +3050,7 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
            + (f'  __shared__ unsigned long long ts_sh[{max(1, len(low.sites))}];\n'
               f'  for (int i_ = tid; i_ < {max(1, len(low.sites))}; i_ += {BLOCK}) ts_sh[i_] = 0ull;\n'
               '  __syncthreads();\n'
-              '  unsigned long long tlast_ = vh_clock();\n' if timing else '')
+              '  unsigned long long tlast_ = vh_clock();\n' if timing is True else '')
            + '\n'.join(pre) + '\n'
            + ''.join(f'  {d}\n' for d in low.shared_decls)
            + ''.join(fb_init)
@@ -3063,7 +3066,7 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
            + '  }\n'
            + ('  __syncthreads();\n'
               f'  for (int i_ = tid; i_ < {len(low.sites)}; i_ += {BLOCK}) TS[i_ * nblk + blockIdx.x] += ts_sh[i_];\n'
-              if timing else '')
+              if timing is True else '')
            + '  grid_exit(bar, nblk);\n}\n')
     scratch = {}
     for n in low.axes_of:
