@@ -88,6 +88,31 @@ def test_tiny_gpt2_matches_reference_golden():
     assert np.abs(keys[:, :used] - g['keys'][:, :used].astype(np.float32)).max() < 2e-3
 
 
+def test_local_checkpoint_matches_oracle(tmp_path):
+    """A transformers GPT-2 saved with save_pretrained (safetensors + config.json),
+    read back through LocalGPT2 into the decode API, two rows."""
+    pytest.importorskip('transformers')
+    from oracle import decode
+    from test_weights import _hf_tiny
+    from vesta.gpt2 import VestaGPT2
+    from vesta.gpt2_program import gpt2_program
+    from vesta.weights import LocalGPT2, stacked
+    hf = _hf_tiny(3, wscale=5.0)
+    hf.save_pretrained(tmp_path, safe_serialization=True)
+    local = LocalGPT2(tmp_path)
+    m = VestaGPT2(local, batch=2, tmax=16)
+    m.reset()
+    feed = [[5, 30], [9, 1], [3, 36], [30, 0]]
+    ins, lg, nx = _run_steps(m, feed, 12)
+    sd = {k: v.numpy().astype(np.float16) for k, v in local.state_dict().items()}
+    W = decode.oracle_weights(stacked(sd, 2))
+    text = gpt2_program(2, 16, 4, 64, 37, 'tiny')
+    for r in range(2):
+        onx, olog, marg = decode.teacher_forced(text, W, ins[:, r], 16)
+        assert np.abs(lg[:, r] - olog).max() < 1e-3, r
+        assert all(a == b or mg < 1e-3 for a, b, mg in zip(nx[:, r], onx, marg)), r
+
+
 def test_batch8_rows_match_oracle(small):
     from oracle import decode
     from vesta.gpt2 import VestaGPT2

@@ -1,9 +1,12 @@
 """Seeded random-init GPT-2 weights with Hugging Face names.
 
-There is no network for checkpoints, so the benchmark and the tests run on
-random-init weights of the real architecture. The reference's decode API only
-needs an object with ``.state_dict()`` carrying HF GPT-2 names
-(reference ``vesta/gpt2.py:18-25``); ``RandomGPT2`` is that object.
+The reference's decode API only needs an object with ``.state_dict()``
+carrying HF GPT-2 names (reference ``vesta/gpt2.py:18-25``). Two such objects
+live here: ``RandomGPT2`` (seeded random init of the real architecture: there
+is no network for checkpoints, so the benchmark and the tests run on it) and
+``LocalGPT2`` (a checkpoint already on disk: a ``save_pretrained`` directory
+or a single ``.safetensors`` / ``.bin`` file, with or without the
+``transformer.`` prefix).
 
 Recipe (fixed, so every run and the CPU oracle see the same numbers):
   * ``rng = numpy.random.default_rng(seed)`` (PCG64);
@@ -110,3 +113,113 @@ def stacked(sd: dict, n_layer: int) -> dict[str, np.ndarray]:
                 ow=st('attn.c_proj.weight'), ob=st('attn.c_proj.bias'), ln2w=st('ln_2.weight'), ln2b=st('ln_2.bias'),
                 fcw=st('mlp.c_fc.weight'), fcb=st('mlp.c_fc.bias'), pw=st('mlp.c_proj.weight'), pb=st('mlp.c_proj.bias'),
                 lnfw=np.asarray(sd['transformer.ln_f.weight']), lnfb=np.asarray(sd['transformer.ln_f.bias']))
+
+
+# Non-parameter entries some GPT-2 checkpoints carry (the causal mask buffers).
+_BUFFER_SUFFIXES = ('.attn.bias', '.attn.masked_bias')
+
+
+def normalize_state(sd: dict) -> dict:
+    """Checkpoint entries -> ``GPT2LMHeadModel`` names (``transformer.`` prefix).
+
+    Accepts both the LM-head model's names and the bare ``GPT2Model`` names
+    of hub checkpoints (``h.0.attn.c_attn.weight``, ``wte.weight``), drops the
+    attention mask buffers, and checks that an ``lm_head.weight`` present is
+    the word table: the program's output head is tied to ``wte`` (gpt2.vst
+    Q9), so an untied head cannot be run and is an error."""
+    out = {}
+    head = None
+    for k, v in sd.items():
+        if k == 'lm_head.weight':
+            head = v
+            continue
+        name = k if k.startswith('transformer.') else 'transformer.' + k
+        if name.endswith(_BUFFER_SUFFIXES):
+            continue
+        out[name] = v
+    if 'transformer.wte.weight' not in out:
+        raise KeyError('checkpoint has no word table (wte.weight)')
+    if head is not None:
+        a, b = np.asarray(_host(head), np.float32), np.asarray(_host(out['transformer.wte.weight']), np.float32)
+        if a.shape != b.shape or not np.array_equal(a, b):
+            raise ValueError('lm_head.weight differs from wte.weight: the program ties the output head to wte')
+    return out
+
+
+def _host(v):
+    """A tensor or array as a host array (bf16 tensors widened to fp32)."""
+    if isinstance(v, np.ndarray):
+        return v
+    import torch
+    t = v.detach().cpu()
+    if t.dtype == torch.bfloat16:
+        t = t.float()
+    return t.numpy()
+
+
+def read_checkpoint(path) -> dict:
+    """Tensors of a checkpoint on disk, as torch CPU tensors keyed as stored.
+
+    ``path``: a ``.safetensors`` file, a ``.bin``/``.pt`` file (read with
+    ``torch.load(weights_only=True)``, which executes nothing from the file),
+    or a directory holding ``model.safetensors``, a sharded
+    ``model.safetensors.index.json`` or ``pytorch_model.bin``."""
+    import json
+    import os
+    import torch
+    path = os.fspath(path)
+    if os.path.isdir(path):
+        index = os.path.join(path, 'model.safetensors.index.json')
+        if os.path.exists(index):
+            with open(index, encoding='utf-8') as fh:
+                shards = sorted(set(json.load(fh)['weight_map'].values()))
+            out = {}
+            for sh in shards:
+                out.update(read_checkpoint(os.path.join(path, sh)))
+            return out
+        for name in ('model.safetensors', 'pytorch_model.bin'):
+            if os.path.exists(os.path.join(path, name)):
+                return read_checkpoint(os.path.join(path, name))
+        raise FileNotFoundError(f'no model.safetensors or pytorch_model.bin in {path}')
+    if path.endswith('.safetensors'):
+        from safetensors.torch import load_file
+        return load_file(path)
+    if path.endswith(('.bin', '.pt', '.pth')):
+        sd = torch.load(path, map_location='cpu', weights_only=True)
+        return sd.get('state_dict', sd) if isinstance(sd, dict) else sd
+    raise ValueError(f'unknown checkpoint format: {path}')
+
+
+class _Config:
+    """The GPT-2 hyper-parameters ``VestaGPT2`` reads (``n_head``), from a
+    ``config.json`` when there is one."""
+
+    def __init__(self, d: dict):
+        self.__dict__.update(d)
+
+
+class LocalGPT2:
+    """A GPT-2 checkpoint on local disk, as the object ``VestaGPT2`` takes.
+
+        m = VestaGPT2(LocalGPT2('/models/gpt2'), batch=8, tmax=1024)
+
+    ``state_dict()`` returns ``GPT2LMHeadModel``-named torch tensors in the
+    checkpoint's dtype (``VestaGPT2`` converts them); ``config`` carries
+    ``config.json``'s fields (``n_head`` among them) when the directory has
+    one, else None (the head count then follows from the width)."""
+
+    def __init__(self, path):
+        import json
+        import os
+        self.path = os.fspath(path)
+        self.config = None
+        cfg = os.path.join(self.path if os.path.isdir(self.path) else os.path.dirname(self.path), 'config.json')
+        if os.path.exists(cfg):
+            with open(cfg, encoding='utf-8') as fh:
+                self.config = _Config(json.load(fh))
+        self._sd = None
+
+    def state_dict(self):
+        if self._sd is None:
+            self._sd = normalize_state(read_checkpoint(self.path))
+        return self._sd
