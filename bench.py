@@ -212,6 +212,131 @@ def cpu_baseline(B, sample_steps):
                        f'BLAS threads {threads})')
 
 
+class TorchDecode:
+    """Comparison arm, not the product: the same GPT-2 decode step written with
+    PyTorch-ROCm operators (hipBLASLt GEMMs, fp16 storage and arithmetic), on
+    the residues the Vesta kernel binds (reference arms ``bench/g0_bench.py:78-164``).
+
+    Every step attends over the whole cache with positions past ``pos`` masked,
+    so shapes are static and one step can be captured in a HIP graph. Keys are
+    cached transposed (``[L, B, H, E, tmax]``) so both attention products are
+    batched matrix products with contiguous right operands. ``step`` also feeds
+    the chosen tokens back (``tok``, ``pos`` advance on the device)."""
+
+    def __init__(self, W, n_head, batch, tmax):
+        import torch
+        self.W, self.B, self.H, self.tmax = W, batch, n_head, tmax
+        self.L, self.D = W['qkvw'].shape[0], W['wte'].shape[1]
+        self.E = self.D // n_head
+        dt, dev = W['wte'].dtype, W['wte'].device
+        self.kt = torch.zeros(self.L, batch, n_head, self.E, tmax, dtype=dt, device=dev)
+        self.v = torch.zeros(self.L, batch, n_head, tmax, self.E, dtype=dt, device=dev)
+        self.slots = torch.arange(tmax, device=dev)
+        self.tok = torch.zeros(batch, dtype=torch.long, device=dev)
+        self.pos = torch.zeros((), dtype=torch.long, device=dev)
+
+    def reset(self):
+        self.kt.zero_()
+        self.v.zero_()
+        self.pos.zero_()
+
+    def step(self):
+        import torch
+        import torch.nn.functional as F
+        W, B, H, E, D = self.W, self.B, self.H, self.E, self.D
+        x = W['wte'].index_select(0, self.tok) + W['wpe'].index_select(0, self.pos.view(1))
+        neg = torch.where(self.slots <= self.pos, 0.0, float('-inf')).to(x.dtype)
+        at = self.pos.view(1)
+        for l in range(self.L):
+            h = F.layer_norm(x, (D,), W['ln1w'][l], W['ln1b'][l], 1e-5)
+            q, k, v = torch.addmm(W['qkvb'][l], h, W['qkvw'][l]).view(B, 3, H, E).unbind(1)
+            self.kt[l].index_copy_(3, at, k.unsqueeze(-1))
+            self.v[l].index_copy_(2, at, v.unsqueeze(2))
+            sc = torch.matmul(q.unsqueeze(2), self.kt[l]) * (E ** -0.5) + neg
+            a = torch.matmul(torch.softmax(sc.float(), -1).to(x.dtype), self.v[l]).reshape(B, D)
+            x = x + torch.addmm(W['ob'][l], a, W['ow'][l])
+            h = F.layer_norm(x, (D,), W['ln2w'][l], W['ln2b'][l], 1e-5)
+            h = F.gelu(torch.addmm(W['fcb'][l], h, W['fcw'][l]), approximate='tanh')
+            x = x + torch.addmm(W['pb'][l], h, W['pw'][l])
+        x = F.layer_norm(x, (D,), W['lnfw'], W['lnfb'], 1e-5)
+        nxt = torch.matmul(x, W['wte'].t()).argmax(-1)
+        self.tok.copy_(nxt)
+        self.pos.add_(1)
+        return nxt
+
+
+def run_arm(name, B, steps, warmup, seed=0):
+    """Tokens per second of one PyTorch arm on the benchmark workload
+    (prompt fed one token per step untimed, ``warmup`` untimed steps, then
+    ``steps`` timed steps), and its generated tokens [steps, B]."""
+    import torch
+    from vesta.gpt2 import gpt2_weights
+    from vesta.weights import RandomGPT2, random_prompts
+    W = {k: v.to('cuda', torch.float16).contiguous() for k, v in gpt2_weights(RandomGPT2('small', seed)).items()}
+    tmax = min(1024, ((PROMPT + steps + warmup + 63) // 64) * 64)
+    m = TorchDecode(W, 12, B, tmax)
+    prompts = torch.from_numpy(random_prompts(B, PROMPT, 50257, seed=1)).to('cuda', torch.long)
+    fn = m.step
+    if name == 'torch_compile_graph':
+        fn = torch.compile(m.step, fullgraph=True)
+    graph = None
+    if name in ('torch_graph', 'torch_compile_graph'):
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(3):
+                fn()
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            fn()
+
+    def one():
+        if graph is not None:
+            graph.replay()
+        else:
+            fn()
+    m.reset()
+    for i in range(PROMPT):
+        m.tok.copy_(prompts[:, i])
+        one()
+    for _ in range(warmup):
+        one()
+    out = torch.zeros(steps, B, dtype=torch.long, device='cuda')
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        one()
+        out[i].copy_(m.tok)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return B * steps / dt, out.cpu()
+
+
+def arms_line(names, steps, warmup, batches=(1, 8)):
+    """The PyTorch comparison arms beside the Vesta kernel on the same
+    workload: tok/s per arm and batch, and whether each graph arm's tokens
+    equal its eager run's (a HIP graph replay must reproduce eager results)."""
+    import numpy as np
+    res = {}
+    for B in batches:
+        vesta = run_config(B, steps, warmup, 32)
+        res.setdefault('vesta', {})[f'b{B}'] = round(vesta['tok_s'], 1)
+        eager_toks = None
+        for name in names:
+            tok_s, toks = run_arm(name, B, steps, warmup)
+            rec = res.setdefault(name, {})
+            rec[f'b{B}'] = round(tok_s, 1)
+            if name == 'torch_eager':
+                eager_toks = toks
+            elif eager_toks is not None:
+                rec[f'b{B}_tokens_equal_eager'] = bool(np.array_equal(toks.numpy(), eager_toks.numpy()))
+    return {'metric': 'decode tok/s, GPT-2-small fp16, comparison arms on one MI355X', 'unit': 'tok/s',
+            'steps': steps, 'warmup': warmup, 'prompt': PROMPT, 'arms': res,
+            'note': 'torch arms: fp16 storage and arithmetic, whole-cache masked attention, one HIP graph per '
+                    'step for the graph arms; vesta: the persistent kernel, 32 steps per launch'}
+
+
 def roofline(cfg, peak):
     """The roofline object of one configuration's kernel: algorithmic bytes
     per launch over the launch duration (HIP events on the launch stream),
@@ -244,7 +369,17 @@ def main():
     ap.add_argument('--calibrate-copy', type=int, default=0, metavar='MiB',
                     help='first run one plain device-to-device copy of this many MiB (a kernel of known '
                          'traffic, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)')
+    ap.add_argument('--arms', default='', metavar='LIST',
+                    help='instead of the benchmark line, time PyTorch comparison arms beside the Vesta kernel '
+                         '(comma list of torch_eager, torch_graph, torch_compile_graph) at B=1 and B=8')
     args = ap.parse_args()
+    if args.arms:
+        names = [a for a in args.arms.split(',') if a]
+        bad = set(names) - {'torch_eager', 'torch_graph', 'torch_compile_graph'}
+        if bad:
+            sys.exit(f'unknown arms: {sorted(bad)}')
+        print(json.dumps(arms_line(names, args.steps, args.warmup)), flush=True)
+        return
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary, calib_mib=args.calibrate_copy or 1024)
         return
