@@ -337,6 +337,36 @@ def arms_line(names, steps, warmup, batches=(1, 8)):
                     'step for the graph arms; vesta: the persistent kernel, 32 steps per launch'}
 
 
+def prefill_line(shapes, reps=3):
+    """Wall time of one prompt prefill per (B, P): all positions through each
+    layer together (``mode='batched'``) against P decode steps in one launch
+    (``mode='steps'``); each timed ``reps`` times (host clock around the call
+    and a synchronize), the last one reported (the first pays compilation)."""
+    import torch
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import RandomGPT2, random_prompts
+    out = {}
+    for B, P in shapes:
+        tmax = min(1024, max(384, ((P + 64 + 63) // 64) * 64))
+        m = VestaGPT2(RandomGPT2('small', 0), batch=B, tmax=tmax)
+        prompt = torch.from_numpy(random_prompts(B, P, 50257, seed=1)).to('cuda', torch.int32)
+        rec = {}
+        for mode in ('batched', 'steps'):
+            for _ in range(reps):
+                m.reset()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                m.prefill(prompt, mode=mode)
+                torch.cuda.synchronize()
+                rec[f'{mode}_ms'] = round((time.perf_counter() - t0) * 1e3, 3)
+        rec['ratio'] = round(rec['steps_ms'] / rec['batched_ms'], 1)
+        out[f'{B}x{P}'] = rec
+        del m
+        torch.cuda.empty_cache()
+    return {'metric': 'prompt prefill wall time, GPT-2 small fp16, batched vs one decode step per position',
+            'unit': 'ms', 'higher_is_better': False, 'shapes': out}
+
+
 def roofline(cfg, peak):
     """The roofline object of one configuration's kernel: algorithmic bytes
     per launch over the launch duration (HIP events on the launch stream),
@@ -372,7 +402,14 @@ def main():
     ap.add_argument('--arms', default='', metavar='LIST',
                     help='instead of the benchmark line, time PyTorch comparison arms beside the Vesta kernel '
                          '(comma list of torch_eager, torch_graph, torch_compile_graph) at B=1 and B=8')
+    ap.add_argument('--prefill', default='', metavar='BxP,...',
+                    help='instead of the benchmark line, time prompt prefill (batched against one decode step '
+                         'per position) for these shapes, e.g. 1x128,8x128')
     args = ap.parse_args()
+    if args.prefill:
+        shapes = [tuple(int(v) for v in x.split('x')) for x in args.prefill.split(',') if x]
+        print(json.dumps(prefill_line(shapes)), flush=True)
+        return
     if args.arms:
         names = [a for a in args.arms.split(',') if a]
         bad = set(names) - {'torch_eager', 'torch_graph', 'torch_compile_graph'}

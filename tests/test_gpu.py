@@ -145,7 +145,7 @@ def test_matrix_core_rows_long_context_match_oracle(small, B):
     m = VestaGPT2(hf, batch=B, tmax=T)
     m.reset()
     pr = random_prompts(B, P, 50257, seed=11 + B)
-    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32))
+    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32), mode='steps')
     torch.cuda.synchronize()
     first = m.x.cpu().numpy().copy()
     hist = torch.zeros((G - 1) * B, dtype=torch.int32, device='cuda')
@@ -168,7 +168,7 @@ def _prefill_and_generate(m, pr, G):
     torch = _torch()
     B = pr.shape[0]
     m.reset()
-    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32))
+    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32), mode='steps')
     torch.cuda.synchronize()
     first = m.x.cpu().numpy().copy()
     hist = torch.zeros((G - 1) * B, dtype=torch.int32, device='cuda')
@@ -257,7 +257,7 @@ def test_multistep_launch_and_prefill_match_single_steps(small):
     # prefill in one launch, then G-1 steps in one launch with the token history
     m.reset()
     hist = torch.zeros((G - 1) * B, dtype=torch.int32, device='cuda')
-    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32))
+    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32), mode='steps')
     torch.cuda.synchronize()
     first = m.x.cpu().numpy().copy()
     m.step(G - 1, hist)
@@ -266,6 +266,84 @@ def test_multistep_launch_and_prefill_match_single_steps(small):
     assert (got == ref).all()
     assert int(m.t.item()) == P + G - 1
     assert torch.equal(m.keys, keys_ref)
+
+
+def _prefill_both(m, prompt):
+    """The model state after prefilling ``prompt`` step by step, then batched:
+    (keys, vals, x, logits) of each."""
+    torch = _torch()
+    out = []
+    for mode in ('steps', 'batched'):
+        m.reset()
+        m.prefill(prompt, mode=mode)
+        torch.cuda.synchronize()
+        assert int(m.t.item()) == prompt.shape[1]
+        out.append((m.keys.float().clone(), m.vals.float().clone(), m.x.cpu().numpy().copy(),
+                    m.logits().float().cpu().numpy().copy()))
+    return out
+
+
+@pytest.mark.parametrize('B,P', [(1, 37), (8, 128)])
+def test_batched_prefill_matches_step_prefill(small, B, P):
+    """All prompt positions through each layer together (matrix-core products)
+    against P decode steps: the cache rows, the next token and its logits."""
+    torch = _torch()
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import random_prompts
+    hf, _, _ = small
+    m = VestaGPT2(hf, batch=B, tmax=160)
+    prompt = torch.from_numpy(random_prompts(B, P, 50257, seed=11)).to('cuda', torch.int32)
+    (k0, v0, x0, l0), (k1, v1, x1, l1) = _prefill_both(m, prompt)
+    for a, b in ((k0, k1), (v0, v1)):
+        assert (a[:, :, P:] == 0).all() and (b[:, :, P:] == 0).all()
+        d = (a[:, :, :P] - b[:, :, :P]).abs()
+        print(f'cache rows: max diff {d.max().item():.3g}, mean {d.mean().item():.3g}, '
+              f'differing {(d > 0).float().mean().item():.4f}, mean magnitude {a[:, :, :P].abs().mean().item():.3g}')
+        assert d.max().item() < 2e-2, d.max().item()
+        assert d.mean().item() < 1e-4
+    assert np.abs(l0 - l1).max() < LOGIT_TOL
+    top2 = np.sort(l0, axis=-1)[:, -2:]
+    sure = (top2[:, 1] - top2[:, 0]) > 1e-3
+    assert (x0[sure] == x1[sure]).all()
+
+
+def test_batched_prefill_matches_oracle_and_continues(small):
+    """Batched prefill at a nonzero start position (a second prompt after a
+    first), then decode steps, against the oracle fed the same tokens."""
+    torch = _torch()
+    from oracle import decode
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import random_prompts
+    hf, W, text = small
+    B, P1, P2, G = 2, 5, 7, 4
+    m = VestaGPT2(hf, batch=B, tmax=32)
+    pr = random_prompts(B, P1 + P2, 50257, seed=12)
+    m.reset()
+    m.prefill(torch.from_numpy(pr[:, :P1]).to('cuda', torch.int32), mode='batched')
+    m.prefill(torch.from_numpy(pr[:, P1:]).to('cuda', torch.int32), mode='batched')
+    torch.cuda.synchronize()
+    assert int(m.t.item()) == P1 + P2
+    lg = [m.logits().float().cpu().numpy().copy()]
+    ins = [m.x.cpu().numpy().copy()]
+    for _ in range(G):
+        m.step()
+        torch.cuda.synchronize()
+        lg.append(m.logits().float().cpu().numpy().copy())
+        ins.append(m.x.cpu().numpy().copy())
+    for r in range(B):
+        seq = np.concatenate([pr[r], [ins[k][r] for k in range(G)]])
+        onx, olog, marg = decode.teacher_forced(text, W, seq, 32)
+        got = np.stack([lg[k][r] for k in range(G + 1)])
+        assert np.abs(got - olog[P1 + P2 - 1:]).max() < LOGIT_TOL, r
+        nxt = np.array([ins[k][r] for k in range(G + 1)])
+        want = onx[P1 + P2 - 1:]
+        assert all(a == b or mg < 1e-3 for a, b, mg in zip(nxt, want, marg[P1 + P2 - 1:])), r
+        keys = m.keys[r].float().cpu().numpy()
+        row = decode.Row(text, W, 32)
+        for i, tok in enumerate(seq[:P1 + P2]):
+            row.x, row.t = int(tok), i
+            row.step()
+        assert np.abs(keys[:, :P1 + P2] - row.keys[:, :P1 + P2].astype(np.float32)).max() < 2e-2
 
 
 def _grammar_cases():

@@ -94,6 +94,7 @@ class VestaGPT2:
         self.k = Kernel(self.low, blocks_per_sm=blocks_per_sm)
         self.k.bind(R)
         self._kp = None
+        self._pf = None
         self.weight_bytes = sum(v.numel() * v.element_size() for n, v in self.W.items() if n != 'wpe') \
             + D * self.W['wpe'].element_size()
 
@@ -119,23 +120,52 @@ class VestaGPT2:
             self._kp.bind(self._R)
         return self._kp
 
-    def prefill(self, prompt, tokens=None):
-        """Feed a prompt [B, P] (int32 device tensor) one token per step in ONE
-        launch; afterwards x holds the token chosen after the last prompt token
-        (as after P reference-style steps)."""
+    def prefill(self, prompt, tokens=None, mode='auto'):
+        """Feed a prompt [B, P] (int32 device tensor) at positions t .. t + P - 1;
+        afterwards x holds the token chosen after the last prompt token and t
+        has advanced by P (as after P reference-style steps).
+
+        ``mode``: 'batched' runs all positions through each layer together
+        (matrix-core products, ``vesta.prefill``); 'steps' runs P decode steps
+        in one launch and can write each step's chosen token into ``tokens``;
+        'auto' takes 'batched' when no per-step tokens are asked for and the
+        shapes allow it."""
         P = prompt.shape[1]
         if prompt.shape[0] != self.B:
             raise ValueError(f'prompt has {prompt.shape[0]} rows, the model {self.B}')
         if P < 1:
             raise ValueError('empty prompt')
+        if mode not in ('auto', 'batched', 'steps'):
+            raise ValueError(f'unknown prefill mode {mode!r}')
+        from .prefill import supported
+        fits = supported(self.D, self.H, self.W['fcw'].shape[2])
+        if mode == 'batched' and (tokens is not None or not fits):
+            raise ValueError('batched prefill writes no per-step tokens and needs 64-wide heads and widths '
+                             'that are multiples of 32')
+        if mode == 'batched' or (mode == 'auto' and tokens is None and fits):
+            if self._pf is None:
+                from .prefill import Prefill
+                self._pf = Prefill(self)
+            self._pf.run(prompt.to(dtype=self.x.dtype), int(self.t.item()))
+            return
         ins = prompt.t().contiguous().to(dtype=self.x.dtype)
         self.x.copy_(ins[0])
         self._prefill_kernel().launch(P, tokens, ins)
+        self._take_outputs()
 
     def warm(self, n):
         """n decode steps through the prefill kernel (untimed warm-up)."""
         if n > 0:
             self._prefill_kernel().launch(n)
+            self._take_outputs()
+
+    def _take_outputs(self):
+        """The prefill kernel's last logits and tokens into the decode
+        kernel's scratch, so ``logits()``/``next()`` answer for the last step
+        whichever kernel ran it (a device copy on the current stream)."""
+        kp = self._prefill_kernel()
+        for name in ('logit', 'next'):
+            self.k.view(name).copy_(kp.view(name))
 
     def logits(self):
         return self.k.view('logit')

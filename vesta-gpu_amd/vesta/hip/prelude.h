@@ -291,6 +291,22 @@ __device__ __forceinline__ void vh_split8(const float* v, vh_u32x4& hi, vh_u32x4
   lo = __builtin_bit_cast(vh_u32x4, l);
 }
 
+// The same with the remainder scaled by 2^11 before rounding (exact), so lo
+// keeps 11 significant bits whatever the magnitude (an unscaled remainder of a
+// value below ~0.03 is an fp16 subnormal): v = hi + lo / 2048 to 22 bits.
+// Products with lo go to their own accumulator, scaled back at the end.
+#define VH_LO_SCALE 2048.0f
+__device__ __forceinline__ void vh_split8s(const float* v, vh_u32x4& hi, vh_u32x4& lo) {
+  vh_h8 h, l;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    h[j] = (_Float16)v[j];
+    l[j] = (_Float16)((v[j] - (float)h[j]) * VH_LO_SCALE);
+  }
+  hi = __builtin_bit_cast(vh_u32x4, h);
+  lo = __builtin_bit_cast(vh_u32x4, l);
+}
+
 // Fixed-point accumulators: fp32 values summed exactly as 64-bit integers in
 // units of 2^-32 (any order of atomic adds gives the same bits), read back as
 // fp32. Element i of such a buffer is the 8 bytes at float index i of global

@@ -1,0 +1,180 @@
+"""Multi-token prefill: a prompt's positions go through each layer together.
+
+The reference feeds a prompt one token per launch (reference
+``bench/g0_bench.py:172-173``): P decode steps, each reading every weight.
+Here the B rows' P positions form one M = B * P row batch and each layer is
+a handful of ordinary launches (``hip/prefill.hip``): LayerNorm, the qkv
+product writing the key/value cache rows, causal attention over the cache,
+the out-projection with its residual, LayerNorm, the widening product with
+GELU, the narrowing product with its residual. The products run on the
+matrix cores. Only the last position of each row goes through the final
+LayerNorm and the tied output head; its argmax becomes the next input.
+
+Afterwards the model is in the state P decode steps would leave: cache rows
+t0 .. t0 + P - 1 written, ``x`` the token chosen after the last prompt token,
+``t`` advanced by P, ``logits()`` that step's logits.
+"""
+from __future__ import annotations
+
+import ctypes
+from pathlib import Path
+
+from .launch import compile_code, lib, ok
+
+PREFILL_SRC = Path(__file__).resolve().parent / 'hip' / 'prefill.hip'
+PRELUDE_SRC = Path(__file__).resolve().parent / 'hip' / 'prelude.h'
+BLOCK = 256
+TILE = 32
+HEAD = 64
+KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_attn', 'pf_argmax')
+MODE_PLAIN, MODE_RESID, MODE_GELU, MODE_QKV = 0, 1, 2, 3
+
+
+def supported(D, H, F):
+    """Shapes the prefill kernels take: 64-wide heads and products whose fold
+    lengths are multiples of the 32-deep matrix-core step."""
+    return H * HEAD == D and D % 32 == 0 and F % 32 == 0 and D <= 8 * BLOCK
+
+
+def prefill_source(tmax: int) -> str:
+    return (f'#define VBLOCK {BLOCK}\n#define PF_TMAX {tmax}\n' + PRELUDE_SRC.read_text() + '\n'
+            + PREFILL_SRC.read_text())
+
+
+class _Args:
+    """A kernel argument array for the C-ABI launch: pointers to each value."""
+
+    def __init__(self, vals):
+        self.vals = vals
+        ptrs = [ctypes.cast(ctypes.pointer(v), ctypes.c_void_p) for v in vals]
+        self.array = (ctypes.c_void_p * len(ptrs))(*ptrs)
+
+
+def _p(t):
+    return ctypes.c_void_p(t.data_ptr() if t is not None else 0)
+
+
+def _i(v):
+    return ctypes.c_int(int(v))
+
+
+class Prefill:
+    """The prefill kernels bound to one ``VestaGPT2``'s weights and cache."""
+
+    def __init__(self, model):
+        self.m = model
+        if not supported(model.D, model.H, model.W['fcw'].shape[2]):
+            raise ValueError(f'prefill kernels need 64-wide heads and widths that are multiples of 32 '
+                             f'(d={model.D}, H={model.H})')
+        self.code = compile_code(prefill_source(model.tmax))
+        L = lib()
+        mod = ctypes.c_void_p()
+        ok(L.vh_module_load(self.code, ctypes.byref(mod)), 'prefill module load')
+        self.mod = mod
+        self.fn = {}
+        for name in KERNELS:
+            fn = ctypes.c_void_p()
+            ok(L.vh_module_get_function(mod, name.encode(), ctypes.byref(fn)), name)
+            self.fn[name] = fn
+        self._buf = {}
+        self._own = {}
+        self._plans = {}
+        self._plan = []
+
+    def close(self):
+        if getattr(self, 'mod', None) is not None and self.mod.value:
+            try:
+                lib().vh_synchronize()
+                lib().vh_module_unload(self.mod)
+            except Exception:
+                pass
+            self.mod = None
+
+    def __del__(self):
+        self.close()
+
+    def _launch(self, name, grid, vals):
+        """Record one launch of the plan being built."""
+        self._plan.append((name, self.fn[name], int(grid), _Args(vals)))
+
+    def _buffers(self, M):
+        import torch
+        if self._buf.get('M') != M:
+            m = self.m
+            F = m.W['fcw'].shape[2]
+            f32 = dict(dtype=torch.float32, device='cuda')
+            self._buf = dict(M=M, Z=torch.empty(M, m.D, **f32), A=torch.empty(M, m.D, **f32),
+                             Q=torch.empty(M, m.D, **f32), G=torch.empty(M, F, **f32),
+                             C=torch.empty(m.B, m.D, **f32),
+                             tok=torch.empty(M, dtype=torch.int32, device='cuda'))
+            self._plans = {}
+        return self._buf
+
+    def _transposed(self, name):
+        """The weight copy ``name`` (``<w>__t``: [L, out, in]); the decode
+        kernel's own when it binds one, else made here. Held here from first
+        use on, so launch plans never point at freed memory."""
+        if name not in self._own:
+            packed = getattr(self.m.k, '_packed', {})
+            self._own[name] = packed[name] if name in packed else \
+                self.m.W[name[:-3]].transpose(-1, -2).contiguous()
+        return self._own[name]
+
+    def _gemm(self, A, lda, Wt, bias, M, N, K, mode, out, ldo, layer=0, P=1, t0=0):
+        m = self.m
+        grid = -(-M // TILE) * -(-N // TILE)
+        self._launch('pf_gemm', grid, [_p(A), _i(lda), _p(Wt), _p(bias), _i(M), _i(N), _i(K), _i(mode), _p(out),
+                                       _i(ldo), _p(m.keys), _p(m.vals), _i(P), _i(t0), _i(layer), _i(m.L),
+                                       _i(m.tmax)])
+
+    def run(self, prompt, t0: int):
+        """Prefill ``prompt`` (int32 device tensor [B, P]) at positions t0 .. t0 + P - 1.
+
+        The launch sequence with its argument arrays is built once per
+        (P, t0) and replayed: every pointer it holds (weights, cache, this
+        object's activation buffers and prompt copy) stays fixed."""
+        import torch
+        m = self.m
+        B, P = prompt.shape
+        if t0 + P > m.tmax:
+            raise ValueError(f'positions {t0}..{t0 + P - 1} exceed the cache (tmax {m.tmax})')
+        buf = self._buffers(B * P)
+        buf['tok'].copy_(prompt.reshape(-1))
+        key = (P, t0)
+        if key not in self._plans:
+            self._plan = []
+            self._build(buf, B, P, t0)
+            self._plans[key] = self._plan
+        stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+        L = lib()
+        for name, fn, grid, a in self._plans[key]:
+            ok(L.vh_launch(fn, grid, BLOCK, 0, stream, a.array), name)
+        m.t.fill_(t0 + P)
+
+    def _build(self, buf, B, P, t0):
+        m = self.m
+        M, D, H, L = B * P, m.D, m.H, m.L
+        F = m.W['fcw'].shape[2]
+        V = m.W['wte'].shape[0]
+        W = m.W
+        Z, A, Q, G, C, tok = buf['Z'], buf['A'], buf['Q'], buf['G'], buf['C'], buf['tok']
+        self._launch('pf_embed', M, [_p(tok), _i(P), _i(t0), _p(W['wte']), _p(W['wpe']), _p(Z), _i(D), _i(V)])
+        for layer in range(L):
+            def lw(name):
+                return W[name][layer]
+
+            def lt(name):
+                return self._transposed(name)[layer]
+            self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln1w')), _p(lw('ln1b')), _p(A), _i(D)])
+            self._gemm(A, D, lt('qkvw__t'), lw('qkvb'), M, 3 * D, D, MODE_QKV, Q, D, layer, P, t0)
+            self._launch('pf_attn', -(-M * H // (BLOCK // 64)),
+                         [_p(Q), _p(m.keys), _p(m.vals), _p(A), _i(M), _i(P), _i(t0), _i(layer), _i(L), _i(m.tmax),
+                          _i(H)])
+            self._gemm(A, D, lt('ow__t'), lw('ob'), M, D, D, MODE_RESID, Z, D)
+            self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln2w')), _p(lw('ln2b')), _p(A), _i(D)])
+            self._gemm(A, D, lt('fcw__t'), lw('fcb'), M, F, D, MODE_GELU, G, F)
+            self._gemm(G, F, lt('pw__t'), lw('pb'), M, D, F, MODE_RESID, Z, D)
+        self._launch('pf_ln', B, [_p(Z), _i(P - 1), _i(P), _p(W['lnfw']), _p(W['lnfb']), _p(C), _i(D)])
+        logit = m.k.view('logit')
+        self._gemm(C, D, W['wte'], None, B, V, D, MODE_PLAIN, logit, V)
+        self._launch('pf_argmax', B, [_p(logit), _i(V), _p(m.x), _p(m.k.view('next'))])
