@@ -62,11 +62,11 @@ def test_gpt2_small_b1_plan():
     low = lower_gpt2(1)
     p = placements(low)
     # three projections stream rows of a transposed weight copy, no split-K; the
-    # attention's blocks do the out-projection (10 of the 128 blocks per head) and add it
+    # attention's blocks do the out-projection (12 of the 144 blocks per head) and add it
     # into z1, a fixed-point sum whose base z + ob is stored in the phase before
     for name in ('qkv', 'u', 'z2'):
         assert p[name].startswith('stream (transposed copy)'), (name, p[name])
-    assert p['oo'] == 'attention[bt, h] projection x10'
+    assert p['oo'] == 'attention[bt, h] projection x12'
     assert p['z1'].startswith('fixed-point sum')
     assert low.packs == {'qkvw__t': 'qkvw', 'ow__t': 'ow', 'fcw__t': 'fcw', 'pw__t': 'pw'}
     # attention: scores, softmax statistics and weighted values in one block per (bt, h)

@@ -182,6 +182,8 @@ class AttnMixin:
         G = self.size(lead)
         R = self.grid // G
         if R < PROJ_MIN_REPLICAS:
+            if self.grid_wide // G >= PROJ_MIN_REPLICAS:
+                self.proj_wider = True
             return None
         # fold position of (F.., e): the flat index over the fold axes, last fastest
         strides, acc = {}, 1

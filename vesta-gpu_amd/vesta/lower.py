@@ -73,10 +73,13 @@ WAVE, NWAVE = 64, 8
 BLOCK = WAVE * NWAVE          # threads per block: two waves per SIMD, one block per CU
 KCAP = 32                     # split-K: at most this many partials per tile column block
 GRID_MAX = 1024               # grid reductions keep one partial per block, for up to this many blocks
-GRID_DEFAULT = 256            # blocks per launch: one per CU of an MI355X
-GRID_FEW_ROWS = 128           # ... with fewer than 4 rows, where a step is a chain of grid barriers whose
-                              # release slows with the number of blocks polling them (measured: B=1 255 us
-                              # per step on 128 blocks, 265 on 160, 307 on 256)
+GRID_WIDE = 256               # blocks per launch: one per CU of an MI355X; from 16 rows on
+GRID_DEFAULT = 192            # ... from 4 to 15 rows: a step is a chain of grid barriers, cheaper over
+                              # fewer blocks, and 192 keeps two replica blocks per (row, head) of GPT-2
+                              # small's attention at B=8 (measured B=8: 331 us per step on 192 blocks,
+                              # 345 on 256, 353-355 on 208-240, 429 on 176; B=4: 291 on 192, 305 on 256)
+GRID_FEW_ROWS = 144           # ... below 4 rows (measured B=1: 227 us on 144, 233 on 128 and 120, 240 on
+                              # 156, 252 on 192, 274 on 96)
 REG_MAX = 8                   # register axes: at most this many accumulator rows per lane
 PRIV_SIZE = 8192              # a private value holds at most this many floats
 PRIV_WORK = 1 << 17           # ... and costs at most this many operations per block
@@ -352,7 +355,10 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
         self.step_env = {}
         self.fb_targets = set()
         self.inlined = []
-        self.grid = int(grid or (GRID_FEW_ROWS if batch < 4 else GRID_DEFAULT))
+        self.grid_auto = grid is None
+        self.grid = int(grid or (GRID_FEW_ROWS if batch < 4 else GRID_DEFAULT if batch < 16 else GRID_WIDE))
+        self.grid_wide = GRID_WIDE
+        self.proj_wider = False       # an attention projection would get its replicas on GRID_WIDE blocks
         self.pf_budget = int(prefetch_vgprs or PREFETCH_VGPRS)   # registers per lane a site may prefetch into
         self.packs = {}           # transposed copy -> the residue it is made from
         self.decls = []           # kernel-scope declarations (prefetch registers)
@@ -2971,6 +2977,9 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
     """
     stmts = batch_lift(parse(text), batch, set(per_token))
     low = Lowering(stmts, res, axis_max, outputs, batch, timing, grid, prefetch_vgprs)
+    if low.grid_auto and low.proj_wider:
+        # the default grid is too small for replicated attention projections; the full one is not
+        low = Lowering(stmts, res, axis_max, outputs, batch, timing, GRID_WIDE, prefetch_vgprs)
     for o in outputs:
         if o not in low.axes_of:
             raise NameError(f'output {o} is not a value of the program')
