@@ -367,6 +367,42 @@ def prefill_line(shapes, reps=3):
             'unit': 'ms', 'higher_is_better': False, 'shapes': out}
 
 
+def xl_line(steps, warmup, batch=64, prompt=128, seed=0):
+    """GPT-2 XL greedy decode at 64 rows (128-token
+    prompts, 128 generated tokens, a 256-position cache). The persistent kernel
+    does not fit these shapes (its LDS need exceeds a CU's), so the model runs
+    each step as per-layer launches; the line says which engine ran."""
+    import torch
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import RandomGPT2, random_prompts
+    tmax = 256
+    if prompt + warmup + steps > tmax:
+        sys.exit(f'prompt + warmup + steps must stay within the {tmax}-position cache of this configuration')
+    m = VestaGPT2(RandomGPT2('xl', seed), batch=batch, tmax=tmax)
+    prompts = torch.from_numpy(random_prompts(batch, prompt, 50257, seed=1)).to('cuda', torch.int32)
+    m.reset()
+    m.prefill(prompts)
+    m.warm(warmup)
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    a.record()
+    m.step(steps)
+    b.record()
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    pos0 = prompt + warmup
+    nbytes = sum(step_bytes(m, pos0 + k + 1) for k in range(steps))
+    dev_s = a.elapsed_time(b) / 1e3
+    return {'metric': 'decode tok/s, GPT-2-XL fp16 b64 (configs[4])', 'value': round(batch * steps / elapsed, 1),
+            'unit': 'tok/s', 'ms_per_step': round(elapsed / steps * 1e3, 3), 'steps': steps, 'warmup': warmup,
+            'engine': m.engine, 'why': m.why_layered,
+            'hbm': {'achieved': round(nbytes / dev_s / 1e9, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
+                    'frac': round(nbytes / dev_s / 1e9 / HBM_PEAK_GBPS, 4),
+                    'bytes_per_step_MB': round(step_bytes(m, pos0 + steps // 2) / 1e6, 1)},
+            'data': 'synthetic: random-init GPT-2-XL fp16 weights N(0,0.02) seed 0, uniform-random prompts'}
+
+
 def roofline(cfg, peak):
     """The roofline object of one configuration's kernel: algorithmic bytes
     per launch over the launch duration (HIP events on the launch stream),
@@ -405,7 +441,13 @@ def main():
     ap.add_argument('--prefill', default='', metavar='BxP,...',
                     help='instead of the benchmark line, time prompt prefill (batched against one decode step '
                          'per position) for these shapes, e.g. 1x128,8x128')
+    ap.add_argument('--xl', action='store_true',
+                    help='instead of the benchmark line, measure GPT-2 XL decode at 64 rows (configs[4]); '
+                         'give --steps 120 or fewer')
     args = ap.parse_args()
+    if args.xl:
+        print(json.dumps(xl_line(args.steps, args.warmup)), flush=True)
+        return
     if args.prefill:
         shapes = [tuple(int(v) for v in x.split('x')) for x in args.prefill.split(',') if x]
         print(json.dumps(prefill_line(shapes)), flush=True)

@@ -346,6 +346,73 @@ def test_batched_prefill_matches_oracle_and_continues(small):
         assert np.abs(keys[:, :P1 + P2] - row.keys[:, :P1 + P2].astype(np.float32)).max() < 2e-2
 
 
+def test_layered_engine_matches_persistent(small):
+    """The per-layer launch sequence as a decode engine against the persistent
+    kernel: the same prompt, then decode steps with tokens recorded."""
+    torch = _torch()
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import random_prompts
+    hf, _, _ = small
+    B, P, G = 8, 9, 6
+    prompt = torch.from_numpy(random_prompts(B, P, 50257, seed=21)).to('cuda', torch.int32)
+    out = []
+    for engine in ('persistent', 'layered'):
+        m = VestaGPT2(hf, batch=B, tmax=32, engine=engine)
+        assert m.engine == engine
+        m.reset()
+        m.prefill(prompt)
+        toks = torch.zeros(G * B, dtype=torch.int32, device='cuda')
+        first = m.x.clone()
+        m.step(G, toks)
+        torch.cuda.synchronize()
+        assert int(m.t.item()) == P + G
+        out.append((first.cpu().numpy(), toks.view(G, B).cpu().numpy(), m.logits().float().cpu().numpy().copy(),
+                    m.keys.float().clone()))
+        del m
+    (f0, t0, l0, k0), (f1, t1, l1, k1) = out
+    assert (f0 == f1).all()
+    same = (t0 == t1).all(axis=0)
+    assert same.sum() >= B - 1, (t0, t1)
+    assert np.abs(l0[same] - l1[same]).max() < LOGIT_TOL
+    assert (k0[same] - k1[same]).abs().max().item() < 2e-2
+
+
+@pytest.mark.parametrize('B', [64])
+def test_xl_widths_large_batch_take_layered_engine(B):
+    """GPT-2 XL widths (d 1600, 25 heads, f 6400) at 64 rows: the persistent
+    kernel would need more LDS than a CU has, so the model runs per-layer
+    launches; two of its rows against the oracle (two layers, to keep the
+    oracle quick)."""
+    torch = _torch()
+    from oracle import decode
+    from vesta.gpt2 import VestaGPT2
+    from vesta.gpt2_program import gpt2_program
+    from vesta.weights import GPT2Shape, RandomGPT2, random_prompts, stacked
+    shape = GPT2Shape(2, 1600, 25, 6400)
+    hf = RandomGPT2(shape, 4)
+    m = VestaGPT2(hf, batch=B, tmax=16)
+    assert m.engine == 'layered' and 'LDS' in m.why_layered, m.why_layered
+    P, G = 4, 3
+    pr = random_prompts(B, P, 50257, seed=22)
+    m.reset()
+    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32))
+    lg, ins = [m.logits().float().cpu().numpy().copy()], [m.x.cpu().numpy().copy()]
+    for _ in range(G):
+        m.step()
+        torch.cuda.synchronize()
+        lg.append(m.logits().float().cpu().numpy().copy())
+        ins.append(m.x.cpu().numpy().copy())
+    W = decode.oracle_weights(stacked(hf.numpy_state(), 2))
+    text = gpt2_program(2, 1600, 25, 6400, 50257, 'custom')
+    for r in (0, B - 1):
+        seq = np.concatenate([pr[r], [ins[k][r] for k in range(G)]])
+        onx, olog, marg = decode.teacher_forced(text, W, seq, 16)
+        got = np.stack([lg[k][r] for k in range(G + 1)])
+        assert np.abs(got - olog[P - 1:]).max() < LOGIT_TOL, r
+        nxt = np.array([ins[k][r] for k in range(G + 1)])
+        assert all(a == b or mg < 1e-3 for a, b, mg in zip(nxt, onx[P - 1:], marg[P - 1:])), r
+
+
 def _grammar_cases():
     return json.load(open(os.path.join(GOLD, 'grammar_cases.json')))
 

@@ -19,8 +19,11 @@ from __future__ import annotations
 
 from . import PROGRAMS
 from .gpt2_program import gpt2_program
-from .launch import TORCH_DT, Kernel, lower_fitted
+from .launch import TORCH_DT, Kernel, code_spills, compile_code, lower_fitted
 from .lower import lower
+
+LDS_PER_CU = 160 * 1024      # bytes of LDS one block of the persistent kernel may use
+SPILLS_LAYERED = 64          # spilled registers beyond which 'auto' takes the layered engine
 
 SHAPE_PROGRAMS = {(12, 768, 12): 'gpt2.vst', (24, 1024, 16): 'gpt2_medium.vst', (48, 1600, 25): 'gpt2_xl.vst'}
 
@@ -58,8 +61,18 @@ def _n_head(hf, d):
 
 class VestaGPT2:
     def __init__(self, hf, dtype='f16', batch=1, tmax=1024, feedback=True, program=None, timing=False,
-                 blocks_per_sm=None):
+                 blocks_per_sm=None, engine='auto'):
+        """``engine``: 'persistent' lowers the program to one persistent kernel
+        per launch (the reference design); 'layered' runs each step as a
+        sequence of ordinary per-layer launches (``vesta.prefill``: the
+        multi-token prefill kernels with one position per row); 'auto' takes
+        the persistent kernel unless it does not fit the device (LDS beyond a
+        CU's 160 KB, or more than ``SPILLS_LAYERED`` spilled registers), as
+        for GPT-2 XL at 64 rows. With the layered engine ``low`` and ``k``
+        are None."""
         import torch
+        if engine not in ('auto', 'persistent', 'layered'):
+            raise ValueError(f'unknown engine {engine!r}')
         tdt = TORCH_DT[dtype]
         self.W = {k: v.detach().to('cuda', tdt).contiguous() for k, v in gpt2_weights(hf).items()}
         L = self.W['qkvw'].shape[0]
@@ -89,14 +102,40 @@ class VestaGPT2:
                                              outputs=('logit', 'next'),
                                              feedback={'x': 'next', 't': 1} if feedback else None))
         self._R, self._bps, self._timing = R, blocks_per_sm, timing
-        self.low = lower_fitted(lower, text, spec, **self._lower_args[2], timing=timing,
-                                kernel_name=f'vesta_step_b{batch}')
-        self.k = Kernel(self.low, blocks_per_sm=blocks_per_sm)
-        self.k.bind(R)
-        self._kp = None
-        self._pf = None
+        self.low, self.k, self._kp, self._pf = None, None, None, None
+        self.engine, self.why_layered = 'persistent', None
+        if engine == 'layered':
+            self.why_layered = 'asked for'
+        else:
+            self.why_layered = self._persistent(text, spec, batch, timing, blocks_per_sm, strict=engine == 'persistent')
+        if self.k is None:
+            from .prefill import Prefill, supported
+            if not supported(D, H, F):
+                raise ValueError(f'the persistent kernel does not fit ({self.why_layered}) and the layered '
+                                 f'engine needs 64-wide heads and widths that are multiples of 32')
+            self.engine = 'layered'
+            self._logit = torch.zeros(batch, V, dtype=torch.float32, device='cuda')
+            self._next = torch.zeros(batch, dtype=torch.float32, device='cuda')
+            self._pf = Prefill(self)
         self.weight_bytes = sum(v.numel() * v.element_size() for n, v in self.W.items() if n != 'wpe') \
             + D * self.W['wpe'].element_size()
+
+    def _persistent(self, text, spec, batch, timing, blocks_per_sm, strict):
+        """Build the persistent kernel; returns None, or (when it does not fit
+        and ``strict`` is off) why not."""
+        kw = dict(**self._lower_args[2], timing=timing, kernel_name=f'vesta_step_b{batch}')
+        if not strict:
+            lds = lower(text, spec, **kw).shared_bytes
+            if lds > LDS_PER_CU:
+                return f'{lds} bytes of LDS per block'
+        low = lower_fitted(lower, text, spec, **kw)
+        spills = code_spills(compile_code(low.src))
+        if not strict and spills > SPILLS_LAYERED:
+            return f'{spills} spilled registers'
+        self.low = low
+        self.k = Kernel(low, blocks_per_sm=blocks_per_sm)
+        self.k.bind(self._R)
+        return None
 
     def reset(self):
         self.keys.zero_()
@@ -108,6 +147,9 @@ class VestaGPT2:
         launch, writing each step's tokens into ``tokens`` [n, B] if given."""
         if tokens is not None and tokens.numel() < n * self.B:
             raise ValueError(f'tokens holds {tokens.numel()} ids, {n * self.B} needed')
+        if self.k is None:
+            self._pf.decode(n, tokens)
+            return
         self.k.launch(n, tokens)
 
     def _prefill_kernel(self):
@@ -142,20 +184,30 @@ class VestaGPT2:
         if mode == 'batched' and (tokens is not None or not fits):
             raise ValueError('batched prefill writes no per-step tokens and needs 64-wide heads and widths '
                              'that are multiples of 32')
+        t0 = int(self.t.item())
+        if t0 + P > self.tmax:
+            raise ValueError(f'positions {t0}..{t0 + P - 1} exceed the cache (tmax {self.tmax})')
         if mode == 'batched' or (mode == 'auto' and tokens is None and fits):
             if self._pf is None:
                 from .prefill import Prefill
                 self._pf = Prefill(self)
-            self._pf.run(prompt.to(dtype=self.x.dtype), int(self.t.item()))
+            self._pf.run(prompt.to(dtype=self.x.dtype))
             return
         ins = prompt.t().contiguous().to(dtype=self.x.dtype)
+        if self.k is None:
+            for i in range(P):
+                self.x.copy_(ins[i])
+                self._pf.decode(1, None if tokens is None else tokens[i * self.B:])
+            return
         self.x.copy_(ins[0])
         self._prefill_kernel().launch(P, tokens, ins)
         self._take_outputs()
 
     def warm(self, n):
         """n decode steps through the prefill kernel (untimed warm-up)."""
-        if n > 0:
+        if n > 0 and self.k is None:
+            self._pf.decode(n)
+        elif n > 0:
             self._prefill_kernel().launch(n)
             self._take_outputs()
 
@@ -168,10 +220,10 @@ class VestaGPT2:
             self.k.view(name).copy_(kp.view(name))
 
     def logits(self):
-        return self.k.view('logit')
+        return self._logit if self.k is None else self.k.view('logit')
 
     def next(self):
-        return self.k.view('next')
+        return self._next if self.k is None else self.k.view('next')
 
     def kv_bytes(self, n_ctx):
         return 2 * self.L * self.B * n_ctx * self.D * self.keys.element_size()

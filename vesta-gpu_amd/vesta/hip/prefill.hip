@@ -5,8 +5,11 @@
 // run time by hipRTC.
 //
 // Row m of every activation buffer is position p = m % P of batch row
-// b = m / P, at sequence position t0 + p. Activations are fp32 [M, width];
-// the key/value cache is the decode kernel's [B, L, tmax, H, 64] fp16.
+// b = m / P, at sequence position t0 + p, t0 read from the device (the
+// model's position counter, advanced by P at the end). Activations are fp32
+// [M, width]; the key/value cache is the decode kernel's [B, L, tmax, H, 64]
+// fp16. Positions at or past tmax write no cache row and attend to rows
+// 0 .. tmax - 1 only.
 //
 // Arithmetic follows the program's statements (fp16 weights, fp32 math, the
 // cache rounded to fp16 before attention reads it); products run on
@@ -18,15 +21,18 @@
 #define PF_TILE 32              // output tile of one block: 32 rows x 32 columns
 
 // ---------------------------------------------------------------- embedding
-// Z[m] = wte[tok[m]] + wpe[t0 + p]   (gpt2.vst Q1). One block per row.
-extern "C" __global__ __launch_bounds__(256) void pf_embed(const int* __restrict__ tok, int P, int t0,
+// Z[m] = wte[tok[m]] + wpe[t0 + p]   (gpt2.vst Q1; ids and positions
+// clamped into their tables). One block per row.
+extern "C" __global__ __launch_bounds__(256) void pf_embed(const int* __restrict__ tok, int P,
+                                                            const int* __restrict__ tp,
                                                             const vh_half* __restrict__ wte,
                                                             const vh_half* __restrict__ wpe, float* __restrict__ Z,
-                                                            int D, int V) {
+                                                            int D, int V, int npos) {
   const int m = blockIdx.x;
   int x = tok[m];
   x = x < 0 ? 0 : (x >= V ? V - 1 : x);
-  const int pos = t0 + m % P;
+  int pos = *tp + m % P;
+  pos = pos < 0 ? 0 : (pos >= npos ? npos - 1 : pos);
   for (int i = threadIdx.x; i < D; i += blockDim.x)
     Z[(size_t)m * D + i] = h2f(wte[(size_t)x * D + i]) + h2f(wpe[(size_t)pos * D + i]);
 }
@@ -104,7 +110,8 @@ __device__ __forceinline__ void pf_split_a(vh_f32x4 x0, vh_f32x4 x1, vh_u32x4& h
 extern "C" __global__ __launch_bounds__(256) void pf_gemm(
     const float* __restrict__ A, int lda, const vh_half* __restrict__ Wt, const vh_half* __restrict__ bias,
     int M, int N, int K, int mode, float* __restrict__ out, int ldo,
-    vh_half* __restrict__ kc, vh_half* __restrict__ vc, int P, int t0, int layer, int L, int tmax) {
+    vh_half* __restrict__ kc, vh_half* __restrict__ vc, int P, const int* __restrict__ tp, int layer, int L,
+    int tmax) {
   __shared__ vh_f32x4 part[VNWAVE][2][2][2][64];     // [wave][hi/lo][i][j][lane]
   const int ntn = (N + PF_TILE - 1) / PF_TILE;
   const int tn = blockIdx.x % ntn, tm = blockIdx.x / ntn;
@@ -184,9 +191,11 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm(
       if (n < D) {
         out[(size_t)m * ldo + n] = val;
       } else {
-        const int b = m / P, pos = t0 + m % P;
-        const size_t at = ((size_t)(b * L + layer) * tmax + pos) * D + (n % D);
-        (n < 2 * D ? kc : vc)[at] = f2h(val);
+        const int b = m / P, pos = *tp + m % P;
+        if (pos >= 0 && pos < tmax) {
+          const size_t at = ((size_t)(b * L + layer) * tmax + pos) * D + (n % D);
+          (n < 2 * D ? kc : vc)[at] = f2h(val);
+        }
       }
     }
   }
@@ -200,7 +209,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm(
 // `ws` holds each wave's scores, then weights, for up to PF_TMAX positions.
 extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restrict__ Q, const vh_half* __restrict__ kc,
                                                            const vh_half* __restrict__ vc, float* __restrict__ O,
-                                                           int M, int P, int t0, int layer, int L, int tmax, int H) {
+                                                           int M, int P, const int* __restrict__ tp, int layer,
+                                                           int L, int tmax, int H) {
   __shared__ float qs[VNWAVE][PF_E];
   __shared__ float ws[VNWAVE][PF_TMAX];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -208,7 +218,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restric
   const bool live = item < M * H;
   const int m = live ? item / H : 0, h = live ? item % H : 0;
   const int D = H * PF_E;
-  const int b = m / P, pos = t0 + m % P;
+  const int b = m / P, at = *tp + m % P;
+  const int pos = at < tmax ? at : tmax - 1;
   const size_t base = (size_t)(b * L + layer) * tmax * D + (size_t)h * PF_E;
   if (live) qs[wave][lane] = Q[(size_t)m * D + h * PF_E + lane];
   vh_lds_sync();
@@ -253,9 +264,11 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restric
 // ---------------------------------------------------------------- argmax
 // Per row of logits [B, V]: the largest value, a tie to the lowest id
 // (gpt2.vst Q10). Writes the token into x (the next step's input) and, as a
-// float, into `next`. One block per row.
+// float, into `next`; block 0 advances the position counter by P. One block
+// per row.
 extern "C" __global__ __launch_bounds__(256) void pf_argmax(const float* __restrict__ logit, int V,
-                                                             int* __restrict__ x, float* __restrict__ next) {
+                                                             int* __restrict__ x, float* __restrict__ next,
+                                                             int* __restrict__ tp, int P) {
   __shared__ float rv[VNWAVE];
   __shared__ int ri[VNWAVE];
   const float* lg = logit + (size_t)blockIdx.x * V;
@@ -266,5 +279,6 @@ extern "C" __global__ __launch_bounds__(256) void pf_argmax(const float* __restr
   if (threadIdx.x == 0) {
     x[blockIdx.x] = id;
     next[blockIdx.x] = (float)id;
+    if (blockIdx.x == 0) *tp += P;     // the last kernel of a pass: advance the position
   }
 }

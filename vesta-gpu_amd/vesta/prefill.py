@@ -76,7 +76,7 @@ class Prefill:
             fn = ctypes.c_void_p()
             ok(L.vh_module_get_function(mod, name.encode(), ctypes.byref(fn)), name)
             self.fn[name] = fn
-        self._buf = {}
+        self._bufs = {}
         self._own = {}
         self._plans = {}
         self._plan = []
@@ -98,17 +98,17 @@ class Prefill:
         self._plan.append((name, self.fn[name], int(grid), _Args(vals)))
 
     def _buffers(self, M):
+        """Activation buffers for M rows (one set per row count, kept)."""
         import torch
-        if self._buf.get('M') != M:
+        if M not in self._bufs:
             m = self.m
             F = m.W['fcw'].shape[2]
             f32 = dict(dtype=torch.float32, device='cuda')
-            self._buf = dict(M=M, Z=torch.empty(M, m.D, **f32), A=torch.empty(M, m.D, **f32),
-                             Q=torch.empty(M, m.D, **f32), G=torch.empty(M, F, **f32),
-                             C=torch.empty(m.B, m.D, **f32),
-                             tok=torch.empty(M, dtype=torch.int32, device='cuda'))
-            self._plans = {}
-        return self._buf
+            self._bufs[M] = dict(Z=torch.empty(M, m.D, **f32), A=torch.empty(M, m.D, **f32),
+                                 Q=torch.empty(M, m.D, **f32), G=torch.empty(M, F, **f32),
+                                 C=torch.empty(m.B, m.D, **f32),
+                                 tok=torch.empty(M, dtype=torch.int32, device='cuda'))
+        return self._bufs[M]
 
     def _transposed(self, name):
         """The weight copy ``name`` (``<w>__t``: [L, out, in]); the decode
@@ -120,45 +120,62 @@ class Prefill:
                 self.m.W[name[:-3]].transpose(-1, -2).contiguous()
         return self._own[name]
 
-    def _gemm(self, A, lda, Wt, bias, M, N, K, mode, out, ldo, layer=0, P=1, t0=0):
+    def _gemm(self, A, lda, Wt, bias, M, N, K, mode, out, ldo, layer=0, P=1):
         m = self.m
         grid = -(-M // TILE) * -(-N // TILE)
         self._launch('pf_gemm', grid, [_p(A), _i(lda), _p(Wt), _p(bias), _i(M), _i(N), _i(K), _i(mode), _p(out),
-                                       _i(ldo), _p(m.keys), _p(m.vals), _i(P), _i(t0), _i(layer), _i(m.L),
+                                       _i(ldo), _p(m.keys), _p(m.vals), _i(P), _p(m.t), _i(layer), _i(m.L),
                                        _i(m.tmax)])
 
-    def run(self, prompt, t0: int):
-        """Prefill ``prompt`` (int32 device tensor [B, P]) at positions t0 .. t0 + P - 1.
-
-        The launch sequence with its argument arrays is built once per
-        (P, t0) and replayed: every pointer it holds (weights, cache, this
-        object's activation buffers and prompt copy) stays fixed."""
+    def _replay(self, plan):
         import torch
-        m = self.m
-        B, P = prompt.shape
-        if t0 + P > m.tmax:
-            raise ValueError(f'positions {t0}..{t0 + P - 1} exceed the cache (tmax {m.tmax})')
-        buf = self._buffers(B * P)
-        buf['tok'].copy_(prompt.reshape(-1))
-        key = (P, t0)
-        if key not in self._plans:
-            self._plan = []
-            self._build(buf, B, P, t0)
-            self._plans[key] = self._plan
         stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         L = lib()
-        for name, fn, grid, a in self._plans[key]:
+        for name, fn, grid, a in plan:
             ok(L.vh_launch(fn, grid, BLOCK, 0, stream, a.array), name)
-        m.t.fill_(t0 + P)
 
-    def _build(self, buf, B, P, t0):
+    def run(self, prompt):
+        """Prefill ``prompt`` (int32 device tensor [B, P]) at positions t .. t + P - 1
+        (t the model's position counter, read and advanced on the device).
+
+        The launch sequence with its argument arrays is built once per P and
+        replayed: every pointer it holds (weights, cache, this object's
+        activation buffers and prompt copy) stays fixed."""
+        B, P = prompt.shape
+        buf = self._buffers(B * P)
+        buf['tok'].copy_(prompt.reshape(-1))
+        if P not in self._plans:
+            self._plan = []
+            self._build(buf, B, P, buf['tok'])
+            self._plans[P] = self._plan
+        self._replay(self._plans[P])
+
+    def decode(self, n, tokens=None):
+        """``n`` greedy decode steps, each one pass with P = 1 over the
+        model's input ``x`` (the last pass's argmax): the layer-at-a-time
+        path for shapes the persistent kernel does not fit. ``tokens`` (int32
+        device tensor, at least n * B) receives each step's chosen tokens."""
+        m = self.m
+        buf = self._buffers(m.B)
+        if 'decode' not in self._plans:
+            self._plan = []
+            self._build(buf, m.B, 1, m.x)
+            self._plans['decode'] = self._plan
+        plan = self._plans['decode']
+        for k in range(n):
+            self._replay(plan)
+            if tokens is not None:
+                tokens[k * m.B:(k + 1) * m.B].copy_(m.x)
+
+    def _build(self, buf, B, P, tok):
         m = self.m
         M, D, H, L = B * P, m.D, m.H, m.L
         F = m.W['fcw'].shape[2]
         V = m.W['wte'].shape[0]
         W = m.W
-        Z, A, Q, G, C, tok = buf['Z'], buf['A'], buf['Q'], buf['G'], buf['C'], buf['tok']
-        self._launch('pf_embed', M, [_p(tok), _i(P), _i(t0), _p(W['wte']), _p(W['wpe']), _p(Z), _i(D), _i(V)])
+        Z, A, Q, G, C = buf['Z'], buf['A'], buf['Q'], buf['G'], buf['C']
+        self._launch('pf_embed', M, [_p(tok), _i(P), _p(m.t), _p(W['wte']), _p(W['wpe']), _p(Z), _i(D), _i(V),
+                                     _i(W['wpe'].shape[0])])
         for layer in range(L):
             def lw(name):
                 return W[name][layer]
@@ -166,15 +183,15 @@ class Prefill:
             def lt(name):
                 return self._transposed(name)[layer]
             self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln1w')), _p(lw('ln1b')), _p(A), _i(D)])
-            self._gemm(A, D, lt('qkvw__t'), lw('qkvb'), M, 3 * D, D, MODE_QKV, Q, D, layer, P, t0)
+            self._gemm(A, D, lt('qkvw__t'), lw('qkvb'), M, 3 * D, D, MODE_QKV, Q, D, layer, P)
             self._launch('pf_attn', -(-M * H // (BLOCK // 64)),
-                         [_p(Q), _p(m.keys), _p(m.vals), _p(A), _i(M), _i(P), _i(t0), _i(layer), _i(L), _i(m.tmax),
+                         [_p(Q), _p(m.keys), _p(m.vals), _p(A), _i(M), _i(P), _p(m.t), _i(layer), _i(L), _i(m.tmax),
                           _i(H)])
             self._gemm(A, D, lt('ow__t'), lw('ob'), M, D, D, MODE_RESID, Z, D)
             self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln2w')), _p(lw('ln2b')), _p(A), _i(D)])
             self._gemm(A, D, lt('fcw__t'), lw('fcb'), M, F, D, MODE_GELU, G, F)
             self._gemm(G, F, lt('pw__t'), lw('pb'), M, D, F, MODE_RESID, Z, D)
         self._launch('pf_ln', B, [_p(Z), _i(P - 1), _i(P), _p(W['lnfw']), _p(W['lnfb']), _p(C), _i(D)])
-        logit = m.k.view('logit')
+        logit, nxt = m.logits(), m.next()
         self._gemm(C, D, W['wte'], None, B, V, D, MODE_PLAIN, logit, V)
-        self._launch('pf_argmax', B, [_p(logit), _i(V), _p(m.x), _p(m.k.view('next'))])
+        self._launch('pf_argmax', B, [_p(logit), _i(V), _p(m.x), _p(nxt), _p(m.t), _i(P)])
