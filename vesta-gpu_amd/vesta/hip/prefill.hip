@@ -90,7 +90,9 @@ __device__ __forceinline__ float pf_gelu(float u) {
   return 0.5f * u * (1.0f + tanhf(0.7978845608028654f * (u + 0.044715f * u * u * u)));
 }
 
-#define PF_UNROLL 4              // k-steps whose loads are issued together
+#ifndef PF_UNROLL
+#define PF_UNROLL 2              // k-steps whose loads are issued together (2: measured best of 2, 4, 8)
+#endif
 
 __device__ __forceinline__ void pf_load_a(const float* __restrict__ A, int lda, int row, int M, int k,
                                           vh_f32x4& x0, vh_f32x4& x1) {
@@ -107,14 +109,48 @@ __device__ __forceinline__ void pf_split_a(vh_f32x4 x0, vh_f32x4 x1, vh_u32x4& h
   vh_split8s(v, hi, lo);
 }
 
+// The epilogue of one output value c = C[m, n] (modes above).
+__device__ __forceinline__ void pf_epi(int mode, int m, int n, float c, const vh_half* __restrict__ bias, int N,
+                                       float* __restrict__ out, int ldo, vh_half* __restrict__ kc,
+                                       vh_half* __restrict__ vc, int P, const int* __restrict__ tp, int layer,
+                                       int L, int tmax) {
+  const float bn = bias ? h2f(bias[n]) : 0.0f;
+  if (mode == 0) {
+    out[(size_t)m * ldo + n] = c + bn;
+  } else if (mode == 1) {
+    float* o = out + (size_t)m * ldo + n;
+    *o = (*o + c) + bn;
+  } else if (mode == 2) {
+    out[(size_t)m * ldo + n] = pf_gelu(c + bn);
+  } else {
+    const int D = N / 3;
+    const float val = c + bn;
+    if (n < D) {
+      out[(size_t)m * ldo + n] = val;
+    } else {
+      const int b = m / P, pos = *tp + m % P;
+      if (pos >= 0 && pos < tmax) {
+        const size_t at = ((size_t)(b * L + layer) * tmax + pos) * D + (n % D);
+        (n < 2 * D ? kc : vc)[at] = f2h(val);
+      }
+    }
+  }
+}
+
+// `ksplit` > 1 splits K over blocks as well: block b makes part b / tiles of
+// the fold for tile b % tiles and stores its partial tile in ws[part][m][n];
+// pf_reduce then adds the parts in part order and applies the epilogue.
 extern "C" __global__ __launch_bounds__(256) void pf_gemm(
     const float* __restrict__ A, int lda, const vh_half* __restrict__ Wt, const vh_half* __restrict__ bias,
     int M, int N, int K, int mode, float* __restrict__ out, int ldo,
     vh_half* __restrict__ kc, vh_half* __restrict__ vc, int P, const int* __restrict__ tp, int layer, int L,
-    int tmax) {
+    int tmax, int ksplit, float* __restrict__ ws) {
   __shared__ vh_f32x4 part[VNWAVE][2][2][2][64];     // [wave][hi/lo][i][j][lane]
-  const int ntn = (N + PF_TILE - 1) / PF_TILE;
-  const int tn = blockIdx.x % ntn, tm = blockIdx.x / ntn;
+  const int ntn = (N + PF_TILE - 1) / PF_TILE, ntm = (M + PF_TILE - 1) / PF_TILE;
+  const int tile = blockIdx.x % (ntn * ntm), kp = blockIdx.x / (ntn * ntm);
+  const int tn = tile % ntn, tm = tile / ntn;
+  const int nks = K / 32, ks0 = kp * nks / ksplit, ks1 = (kp + 1) * nks / ksplit;
+  const int kend = 32 * ks1;
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int m0 = tm * PF_TILE, n0 = tn * PF_TILE;
   const int r = lane & 15, kq = (lane >> 4) * 8;
@@ -126,14 +162,14 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm(
   const int c0 = n0 + r, c1 = n0 + 16 + r;
   const vh_half* w0 = Wt + (size_t)(c0 < N ? c0 : 0) * K;
   const vh_half* w1 = Wt + (size_t)(c1 < N ? c1 : 0) * K;
-  for (int k0 = 32 * wave; k0 < K; k0 += 32 * VNWAVE * PF_UNROLL) {
+  for (int k0 = 32 * (ks0 + wave); k0 < kend; k0 += 32 * VNWAVE * PF_UNROLL) {
     vh_f32x4 xa[PF_UNROLL][2][2];
     vh_u32x4 bw[PF_UNROLL][2];
 #pragma unroll
     for (int u = 0; u < PF_UNROLL; ++u) {
       const int ks = k0 + 32 * VNWAVE * u;
       const int k = ks + kq;
-      const bool in = ks < K;
+      const bool in = ks < kend;
       pf_load_a(A, lda, in ? m0 + r : M, M, k, xa[u][0][0], xa[u][0][1]);
       pf_load_a(A, lda, in ? m0 + 16 + r : M, M, k, xa[u][1][0], xa[u][1][1]);
       bw[u][0] = in && c0 < N ? ld16(w0 + k) : vh_u32x4{0u, 0u, 0u, 0u};
@@ -141,7 +177,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm(
     }
 #pragma unroll
     for (int u = 0; u < PF_UNROLL; ++u) {
-      if (k0 + 32 * VNWAVE * u >= K) break;
+      if (k0 + 32 * VNWAVE * u >= kend) break;
       vh_u32x4 ah[2], al[2];
       pf_split_a(xa[u][0][0], xa[u][0][1], ah[0], al[0]);
       pf_split_a(xa[u][1][0], xa[u][1][1], ah[1], al[1]);
@@ -172,33 +208,30 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm(
   }
   const int n = n0 + 16 * j + r;
   if (n >= N) return;
-  const int D = N / 3;
-  const float bn = bias ? h2f(bias[n]) : 0.0f;
 #pragma unroll
   for (int v = 0; v < 4; ++v) {
     const int m = m0 + 16 * i + 4 * (lane >> 4) + v;
     if (m >= M) continue;
     const float c = fmaf(lo[v], 1.0f / VH_LO_SCALE, hi[v]);
-    if (mode == 0) {
-      out[(size_t)m * ldo + n] = c + bn;
-    } else if (mode == 1) {
-      float* o = out + (size_t)m * ldo + n;
-      *o = (*o + c) + bn;
-    } else if (mode == 2) {
-      out[(size_t)m * ldo + n] = pf_gelu(c + bn);
-    } else {
-      const float val = c + bn;
-      if (n < D) {
-        out[(size_t)m * ldo + n] = val;
-      } else {
-        const int b = m / P, pos = *tp + m % P;
-        if (pos >= 0 && pos < tmax) {
-          const size_t at = ((size_t)(b * L + layer) * tmax + pos) * D + (n % D);
-          (n < 2 * D ? kc : vc)[at] = f2h(val);
-        }
-      }
-    }
+    if (ksplit > 1)
+      ws[((size_t)kp * M + m) * N + n] = c;
+    else
+      pf_epi(mode, m, n, c, bias, N, out, ldo, kc, vc, P, tp, layer, L, tmax);
   }
+}
+
+// The parts of a split product added in part order, then the epilogue. One
+// thread per output value.
+extern "C" __global__ __launch_bounds__(256) void pf_reduce(
+    const float* __restrict__ ws, int ksplit, const vh_half* __restrict__ bias, int M, int N, int mode,
+    float* __restrict__ out, int ldo, vh_half* __restrict__ kc, vh_half* __restrict__ vc, int P,
+    const int* __restrict__ tp, int layer, int L, int tmax) {
+  const size_t e = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= (size_t)M * N) return;
+  const int m = (int)(e / N), n = (int)(e % N);
+  float c = ws[e];
+  for (int k = 1; k < ksplit; ++k) c += ws[(size_t)k * M * N + e];
+  pf_epi(mode, m, n, c, bias, N, out, ldo, kc, vc, P, tp, layer, L, tmax);
 }
 
 // ---------------------------------------------------------------- attention

@@ -26,7 +26,9 @@ PRELUDE_SRC = Path(__file__).resolve().parent / 'hip' / 'prelude.h'
 BLOCK = 256
 TILE = 32
 HEAD = 64
-KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_attn', 'pf_argmax')
+KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_attn', 'pf_argmax')
+SPLIT_BLOCKS = 512            # a product with fewer output tiles than this splits its fold over blocks ...
+SPLIT_MIN_STEPS = 16          # ... into parts of at least this many 32-deep steps
 MODE_PLAIN, MODE_RESID, MODE_GELU, MODE_QKV = 0, 1, 2, 3
 
 
@@ -78,6 +80,8 @@ class Prefill:
             self.fn[name] = fn
         self._bufs = {}
         self._own = {}
+        self._ws = None
+        self._grew = False
         self._plans = {}
         self._plan = []
 
@@ -121,11 +125,41 @@ class Prefill:
         return self._own[name]
 
     def _gemm(self, A, lda, Wt, bias, M, N, K, mode, out, ldo, layer=0, P=1):
+        """One product launch; with few output tiles, or a long fold, the fold
+        is split over blocks too (partial tiles into a workspace, then
+        ``pf_reduce`` adds them in order and applies the epilogue)."""
         m = self.m
-        grid = -(-M // TILE) * -(-N // TILE)
-        self._launch('pf_gemm', grid, [_p(A), _i(lda), _p(Wt), _p(bias), _i(M), _i(N), _i(K), _i(mode), _p(out),
-                                       _i(ldo), _p(m.keys), _p(m.vals), _i(P), _p(m.t), _i(layer), _i(m.L),
-                                       _i(m.tmax)])
+        tiles = -(-M // TILE) * -(-N // TILE)
+        ks = max(1, min(-(-SPLIT_BLOCKS // tiles), (K // 32) // SPLIT_MIN_STEPS))
+        ws = self._workspace(ks * M * N) if ks > 1 else None
+        tail = [_p(m.keys), _p(m.vals), _i(P), _p(m.t), _i(layer), _i(m.L), _i(m.tmax)]
+        self._launch('pf_gemm', tiles * ks, [_p(A), _i(lda), _p(Wt), _p(bias), _i(M), _i(N), _i(K), _i(mode),
+                                             _p(out), _i(ldo)] + tail + [_i(ks), _p(ws)])
+        if ks > 1:
+            self._launch('pf_reduce', -(-M * N // BLOCK), [_p(ws), _i(ks), _p(bias), _i(M), _i(N), _i(mode),
+                                                            _p(out), _i(ldo)] + tail)
+
+    def _workspace(self, n):
+        """Partial tiles of split products: one buffer, grown to the largest
+        need (launches on one stream run one after another)."""
+        import torch
+        if self._ws is None or self._ws.numel() < n:
+            self._ws = torch.empty(n, dtype=torch.float32, device='cuda')
+            self._plans = {}            # plans hold the old pointer
+            self._grew = True
+        return self._ws
+
+    def _plan_for(self, key, buf, B, P, tok):
+        """The launch plan ``key``, built on first use (twice when the build
+        grew the workspace, so that no launch keeps the old pointer)."""
+        if key not in self._plans:
+            for _ in range(2):
+                self._plan, self._grew = [], False
+                self._build(buf, B, P, tok)
+                if not self._grew:
+                    break
+            self._plans[key] = self._plan
+        return self._plans[key]
 
     def _replay(self, plan):
         import torch
@@ -144,11 +178,7 @@ class Prefill:
         B, P = prompt.shape
         buf = self._buffers(B * P)
         buf['tok'].copy_(prompt.reshape(-1))
-        if P not in self._plans:
-            self._plan = []
-            self._build(buf, B, P, buf['tok'])
-            self._plans[P] = self._plan
-        self._replay(self._plans[P])
+        self._replay(self._plan_for(P, buf, B, P, buf['tok']))
 
     def decode(self, n, tokens=None):
         """``n`` greedy decode steps, each one pass with P = 1 over the
@@ -157,11 +187,7 @@ class Prefill:
         device tensor, at least n * B) receives each step's chosen tokens."""
         m = self.m
         buf = self._buffers(m.B)
-        if 'decode' not in self._plans:
-            self._plan = []
-            self._build(buf, m.B, 1, m.x)
-            self._plans['decode'] = self._plan
-        plan = self._plans['decode']
+        plan = self._plan_for('decode', buf, m.B, 1, m.x)
         for k in range(n):
             self._replay(plan)
             if tokens is not None:
