@@ -307,6 +307,9 @@ __device__ __forceinline__ void vh_split8s(const float* v, vh_u32x4& hi, vh_u32x
   lo = __builtin_bit_cast(vh_u32x4, l);
 }
 
+// hi + lo / 2048 for partial sums of the two halves (see vh_split8s).
+__device__ __forceinline__ float vh_hilo(float h, float l) { return fmaf(l, 1.0f / VH_LO_SCALE, h); }
+
 // Fixed-point accumulators: fp32 values summed exactly as 64-bit integers in
 // units of 2^-32 (any order of atomic adds gives the same bits), read back as
 // fp32. Element i of such a buffer is the 8 bytes at float index i of global

@@ -9,10 +9,14 @@ A[l % 16][k0 + 8 (l / 16) ..+8], W[k0 + 8 (l / 16) ..+8][point l % 16] (one
 y[4 (l / 16) + v][point l % 16] for v < 4.
 
 The other factor is fp32; it is split into fp16 halves a = hi + lo (hi the
-nearest fp16, lo the nearest fp16 to the exact remainder), both multiplied
-into the same fp32 accumulator, so a keeps 22 significant bits (the weights
-are fp16 already, and every product is exact). Values beyond the fp16 range
-(65504) are not representable on this path.
+nearest fp16, lo the nearest fp16 to the exact remainder), so a keeps 22
+significant bits (the weights are fp16 already, and every product is exact).
+Values beyond the fp16 range (65504) are not representable on this path.
+With at most 8 rows both halves share one MFMA: rows 0-7 of the A tile hold
+the rows' hi halves and rows 8-15 their lo halves, the remainder scaled by
+2^11 (exact) so it keeps 11 bits at any magnitude; the result rows r and
+r + 8 (lanes l and l + 32) are combined as hi + lo / 2048 after the loop.
+With more rows hi and lo go through separate MFMAs into one accumulator.
 
 Work split: a block's points form NT tiles. With at least as many tiles as
 compute waves, wave w makes tiles w, w + NW, .. over the whole fold; with
@@ -130,15 +134,16 @@ class MfmaMixin:
                 self.stage_A(c, reg, 0, R, R, K, str(top), o, I)
                 direct, top = str(top), top + R * K
         SAB = K * 2 + 16                      # bytes per row of a half array (padded against bank conflicts)
+        packed = R <= 8                       # hi rows 0-7 and lo rows 8-15 of one A tile
         ah = top * 4
-        al = ah + R * SAB
+        al = ah + (8 if packed else R) * SAB
         top = (al + R * SAB) // 4
         red = top
         if KW > 1:
             top += NW * 64 * 4
         accb = top                            # the sums, [row][own point]
         top += -(-R * PPB // 4) * 4
-        self.mfma_split(direct, src, R, K, SAB, ah, al, o, I)
+        self.mfma_split(direct, src, R, K, SAB, ah, al, o, I, scaled=packed)
         self.mark(o, I, f'stream {name}: halves')
         # values of the site (as in the other streams)
         fused_ids = {id(t) for _, t, _ in fused}
@@ -159,6 +164,8 @@ class MfmaMixin:
 
         def kstep(kb, wsrc, J):
             """Lines of one k-block (C expression kb, relative to mk0_) from weight registers wsrc(i)."""
+            if packed:
+                return self.mfma_kstep_packed(f'mk0_ + {kb}', wsrc, TPW, R, SAB, ah, J)
             lines = [f'{J}{{ const int kb_ = mk0_ + {kb};',
                      f'{J}  const int ar_ = lane & 15, ak_ = kb_ * 32 + (lane >> 4) * 8;',
                      f'{J}  const vh_u32x4 ah_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {ah} + ar_ * {SAB} + ak_ * 2) '
@@ -210,6 +217,8 @@ class MfmaMixin:
         # point l % 16 of each of its tiles); then every compute thread finishes
         # one (row, point) item at a time, consecutive threads consecutive points
         o.append(f'{I}if (mok_ && mkp_ == 0) {{')
+        if packed:
+            o += self.mfma_combine_packed(TPW, I + '  ')
         for i in range(TPW):
             o.append(f'{I}  {{ const int n_ = ({self.mfma_tile(geo, i)}) * 16 + (lane & 15);')
             o.append(f'{I}    if (({self.mfma_tile(geo, i)}) < {NT} && n_ < {PPB}) {{')
@@ -292,9 +301,32 @@ class MfmaMixin:
             return None
         return self.g[r]
 
-    def mfma_split(self, direct, src, R, K, SAB, ah, al, o, I):
+    def mfma_kstep_packed(self, kb, wsrc, TPW, R, SAB, ah, J):
+        """One k-block (C expression kb) with hi and lo halves in one A tile:
+        lane l reads row l % 16 of the [16][SAB] half array (rows 8-15: lo)."""
+        lines = [f'{J}{{ const int kb_ = {kb};',
+                 f'{J}  const int ar_ = lane & 15, ak_ = kb_ * 32 + (lane >> 4) * 8;',
+                 f'{J}  const vh_u32x4 a_ = (ar_ & 7) < {R} ? *(const vh_u32x4*)((const char*)sh_f + {ah} + ar_ * {SAB} '
+                 f'+ ak_ * 2) : vh_u32x4{{0u, 0u, 0u, 0u}};']
+        for i in range(TPW):
+            lines.append(f'{J}  acc_[{i}] = vh_mfma(a_, {wsrc(i)}, acc_[{i}]);')
+        lines.append(f'{J}}}')
+        return lines
+
+    def mfma_combine_packed(self, TPW, J):
+        """Lanes l and l + 32 hold the hi and lo sums of the same rows and
+        points: every lane gets hi + lo / 2048 (lanes 32-63 then hold rows 8-15,
+        which the callers skip)."""
+        lines = []
+        for i in range(TPW):
+            for v in range(4):
+                lines.append(f'{J}acc_[{i}][{v}] = vh_pair32(acc_[{i}][{v}], vh_hilo);')
+        return lines
+
+    def mfma_split(self, direct, src, R, K, SAB, ah, al, o, I, scaled=False):
         """The other factor (rows x K fp32, in LDS at float offset ``direct``
-        or in global scratch at ``src``) into fp16 halves in LDS."""
+        or in global scratch at ``src``) into fp16 halves in LDS; ``scaled``:
+        the lo half as fp16((v - hi) * 2048)."""
         K8 = K // 8
         o.append(f'{I}vh_lds_sync();')
         o.append(f'{I}for (int e_ = tid; e_ < {R * K8}; e_ += {self.BLOCK}) {{')
@@ -309,7 +341,7 @@ class MfmaMixin:
             o.append(f'{I}  v_[0] = x0_.x; v_[1] = x0_.y; v_[2] = x0_.z; v_[3] = x0_.w; '
                      f'v_[4] = x1_.x; v_[5] = x1_.y; v_[6] = x1_.z; v_[7] = x1_.w;')
         o.append(f'{I}  vh_u32x4 h_, l_;')
-        o.append(f'{I}  vh_split8(v_, h_, l_);')
+        o.append(f'{I}  {"vh_split8s" if scaled else "vh_split8"}(v_, h_, l_);')
         o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {ah} + r_ * {SAB} + k8_ * 16) = h_;')
         o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {al} + r_ * {SAB} + k8_ * 16) = l_;')
         o.append(f'{I}}}')
@@ -446,8 +478,9 @@ class MfmaMixin:
             self.stage_A(c, reg, 0, R, R, K, str(top), o, I)
             direct, top = str(top), top + R * K
         SAB = KSL * 64 + 16
+        packed = R <= 8
         ah = top * 4
-        al = ah + R * SAB
+        al = ah + (8 if packed else R) * SAB
         top = (al + R * SAB) // 4
         red = top
         top += NW * 64 * 4 if KW > 1 else 0
@@ -470,7 +503,7 @@ class MfmaMixin:
                      f'v_[4] = x1_.x; v_[5] = x1_.y; v_[6] = x1_.z; v_[7] = x1_.w;')
         o.append(f'{I}  }}')
         o.append(f'{I}  vh_u32x4 h_, l_;')
-        o.append(f'{I}  vh_split8(v_, h_, l_);')
+        o.append(f'{I}  {"vh_split8s" if packed else "vh_split8"}(v_, h_, l_);')
         o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {ah} + r_ * {SAB} + k8_ * 16) = h_;')
         o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {al} + r_ * {SAB} + k8_ * 16) = l_;')
         o.append(f'{I}}}')
@@ -481,6 +514,11 @@ class MfmaMixin:
         o.append(f'{I}for (int i_ = 0; i_ < {TPW}; ++i_) acc_[i_] = vh_f32x4{{0.f, 0.f, 0.f, 0.f}};')
         o.append(f'{I}if (mok_) {{')
         for j in range(KBW):
+            if packed:
+                o.append(f'{I}  if (mk0_ + {j} < mk1_)')
+                o += self.mfma_kstep_packed(f'mk0_ + {j}', lambda i, j=j: f'{wm}[{i}][{j}]', TPW, R, SAB, ah,
+                                            I + '    ')
+                continue
             o.append(f'{I}  if (mk0_ + {j} < mk1_) {{')
             o.append(f'{I}    const int ar_ = lane & 15, ak_ = (mk0_ + {j}) * 32 + (lane >> 4) * 8;')
             o.append(f'{I}    const vh_u32x4 ah_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {ah} + ar_ * {SAB} '
@@ -502,6 +540,8 @@ class MfmaMixin:
             o.append(f'{I}}}')
         # the partial tiles into the fixed-point sum
         o.append(f'{I}if (mok_ && mkp_ == 0) {{')
+        if packed:
+            o += self.mfma_combine_packed(TPW, I + '  ')
         for i in range(TPW):
             o.append(f'{I}  {{ const int p_ = sg_ * {PG} + ({tile(i)}) * 16 + (lane & 15);')
             o.append(f'{I}    if (({tile(i)}) < {NTS} && p_ < {P}) {{')
