@@ -191,3 +191,17 @@ def test_chunked_attention_loads_every_slot(budget):
         name = _re.search(arr + r'_\w+\[10\];', low.src).group(0).split('[')[0]
         loaded = {int(k) for k in _re.findall(_re.escape(name) + r'\[(\d+)\] = ldc16_h', low.src)}
         assert loaded == set(range(10)), (arr, sorted(loaded))
+
+
+def test_prefill_kernels_compile_for_gfx950():
+    """The multi-token prefill / layered-engine kernels: one code object per
+    cache length, every kernel the host launches present, no spills."""
+    from vesta.prefill import KERNELS, prefill_source, supported
+    for tmax in (384, 1024):
+        code = launch.compile_code(prefill_source(tmax), cache=False)
+        assert code[:4] == b'\x7fELF'
+        for name in KERNELS:
+            assert name.encode() in code, name
+        assert launch.code_spills(code) == 0
+    assert supported(768, 12, 3072) and supported(1600, 25, 6400)
+    assert not supported(16, 4, 64) and not supported(768, 16, 3072)
