@@ -377,12 +377,12 @@ def test_layered_engine_matches_persistent(small):
     assert (k0[same] - k1[same]).abs().max().item() < 2e-2
 
 
-@pytest.mark.parametrize('B', [64])
-def test_xl_widths_large_batch_take_layered_engine(B):
-    """GPT-2 XL widths (d 1600, 25 heads, f 6400) at 64 rows: the persistent
-    kernel would need more LDS than a CU has, so the model runs per-layer
-    launches; two of its rows against the oracle (two layers, to keep the
-    oracle quick)."""
+@pytest.mark.parametrize('B,engine', [(64, 'layered'), (8, 'persistent')])
+def test_xl_widths_match_oracle(B, engine):
+    """GPT-2 XL widths (d 1600, 25 heads, f 6400), two layers to keep the
+    oracle quick. At 64 rows the persistent kernel would need more LDS than a
+    CU has, so the model runs per-layer launches; at 8 rows it is one
+    persistent kernel on the matrix cores. Two rows against the oracle."""
     torch = _torch()
     from oracle import decode
     from vesta.gpt2 import VestaGPT2
@@ -391,7 +391,9 @@ def test_xl_widths_large_batch_take_layered_engine(B):
     shape = GPT2Shape(2, 1600, 25, 6400)
     hf = RandomGPT2(shape, 4)
     m = VestaGPT2(hf, batch=B, tmax=16)
-    assert m.engine == 'layered' and 'LDS' in m.why_layered, m.why_layered
+    assert m.engine == engine, m.why_layered
+    if engine == 'layered':
+        assert 'LDS' in m.why_layered, m.why_layered
     P, G = 4, 3
     pr = random_prompts(B, P, 50257, seed=22)
     m.reset()

@@ -80,6 +80,7 @@ GRID_DEFAULT = 192            # ... from 4 to 15 rows: a step is a chain of grid
                               # 345 on 256, 353-355 on 208-240, 429 on 176; B=4: 291 on 192, 305 on 256)
 GRID_FEW_ROWS = 144           # ... below 4 rows (measured B=1: 227 us on 144, 233 on 128 and 120, 240 on
                               # 156, 252 on 192, 274 on 96)
+LDS_BYTES = 160 * 1024        # LDS of one CU (the kernel runs one block per CU)
 REG_MAX = 8                   # register axes: at most this many accumulator rows per lane
 PRIV_SIZE = 8192              # a private value holds at most this many floats
 PRIV_WORK = 1 << 17           # ... and costs at most this many operations per block
@@ -2975,11 +2976,19 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
     instead (prefill: a prompt in one launch). ``bar`` must be zero before
     the first launch and is left consistent by every launch.
     """
+    args = (text, res, axis_max, batch, per_token, outputs, feedback, timing, kernel_name)
+    out, low = _lower(*args, grid, prefetch_vgprs)
+    if low.grid_auto and low.grid != GRID_WIDE and (low.proj_wider or out.shared_bytes > LDS_BYTES):
+        # the default grid is too small for replicated attention projections, or leaves streams so
+        # many points per block that their staged rows overflow LDS; the full grid may not
+        out, low = _lower(*args, GRID_WIDE, prefetch_vgprs)
+    return out
+
+
+def _lower(text, res, axis_max, batch, per_token, outputs, feedback, timing, kernel_name, grid, prefetch_vgprs):
+    """One lowering on one grid: (Lowered, the Lowering that made it)."""
     stmts = batch_lift(parse(text), batch, set(per_token))
     low = Lowering(stmts, res, axis_max, outputs, batch, timing, grid, prefetch_vgprs)
-    if low.grid_auto and low.proj_wider:
-        # the default grid is too small for replicated attention projections; the full one is not
-        low = Lowering(stmts, res, axis_max, outputs, batch, timing, GRID_WIDE, prefetch_vgprs)
     for o in outputs:
         if o not in low.axes_of:
             raise NameError(f'output {o} is not a value of the program')
@@ -3085,4 +3094,4 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
             scratch[n] = (low.g[r], axes, tuple(low.static[a] for a in axes))
     return Lowered(src, params, scratch, low.goff, (low.lds_floats + low.stage_floats) * 4, low.barriers,
                    low.plan, low.sites, low.counters, BLOCK, low.grid, {n: shp for n, (shp, _) in low.res.items()},
-                   kernel_name, 1, dict(low.packs))
+                   kernel_name, 1, dict(low.packs)), low
