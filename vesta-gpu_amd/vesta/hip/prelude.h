@@ -255,6 +255,11 @@ __device__ __forceinline__ int ldg_i(vh_rsrc r, unsigned i) {
 __device__ __forceinline__ vh_u32x4 ldg16_nt(vh_rsrc r, unsigned i) {
   return __builtin_amdgcn_raw_buffer_load_b128(r, i * 2u, 0, VH_NT);
 }
+// The same 16 bytes with the default (temporal) policy: kept by the caches,
+// for weights that are worth finding there at the next step.
+__device__ __forceinline__ vh_u32x4 ldg16_t(vh_rsrc r, unsigned i) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, i * 2u, 0, 0);
+}
 __device__ __forceinline__ vh_u32x2 ldg8_nt(vh_rsrc r, unsigned i) {
   return __builtin_amdgcn_raw_buffer_load_b64(r, i * 2u, 0, VH_NT);
 }

@@ -69,6 +69,7 @@ class MfmaMixin:
         geo = dict(P=P, PPB=PPB, NW=NW, NT=NT, TPW=TPW, KW=KW, NKB=NKB, KBW=KBW, R=R, reg=list(reg), CT=CT)
         rr = self.rsrc(st.src)
         rs = self.res_strides(st.src)
+        w16 = self.w16('stream')
         I = ind + '  '
         o = out
 
@@ -83,7 +84,7 @@ class MfmaMixin:
             ix = [self.index(x, env, pre, '    ') for x in st.prefix_idx]
             lines += pre
             base = self.addr(ix, rs[:-1]) if ix else '0'
-            lines.append(f'    {dst} = ldg16_nt({rr}, (unsigned)({base}) + {st.c0}u + (unsigned)(({kb}) * 32 + (lane >> 4) * 8));')
+            lines.append(f'    {dst} = {w16}({rr}, (unsigned)({base}) + {st.c0}u + (unsigned)(({kb}) * 32 + (lane >> 4) * 8));')
             lines.append(f'  }} else {dst} = vh_u32x4{{0u, 0u, 0u, 0u}};')
             lines.append('}')
             return lines
@@ -447,7 +448,7 @@ class MfmaMixin:
             ix = [self.index(x, env, pre, '    ') for x in st.prefix_idx]
             lines += pre
             base = self.addr(ix, rs[:-1]) if ix else '0'
-            lines.append(f'    {dst} = ldg16_nt({rr}, (unsigned)({base}) + {st.c0}u + '
+            lines.append(f'    {dst} = {self.w16("split")}({rr}, (unsigned)({base}) + {st.c0}u + '
                          f'(unsigned)((kb0_ + {kb}) * 32 + (lane >> 4) * 8));')
             lines.append(f'  }} else {dst} = vh_u32x4{{0u, 0u, 0u, 0u}};')
             lines.append('}')

@@ -226,7 +226,7 @@ class StreamMixin:
                 lines.append(f'      const int kv_ = cl_ + m_ * {lpp};')
                 cond = '' if exact else f'if (kv_ < {nv}) '
                 lines.append(f'      {cond}{dst}[{j}][m_] = '
-                             f'{self.nt_load(dt, vec, self.rsrc(st.src), "wr_ + kv_ * %d" % vec)};')
+                             f'{self.nt_load(dt, vec, self.rsrc(st.src), "wr_ + kv_ * %d" % vec, self.weights_kept("stream"))};')
                 if not exact:
                     lines.append(f'      else {dst}[{j}][m_] = {self.vec_zero(dt, vec)};')
                 lines.append('    }')
@@ -579,8 +579,25 @@ class StreamMixin:
             return {8: 'vh_u32x4', 4: 'vh_u32x2', 2: 'unsigned', 1: 'vh_half'}[vec]
         return {4: 'vh_f32x4', 2: 'vh_f32x2', 1: 'float'}[vec]
 
-    def nt_load(self, dt, vec, rr, idx):
+    def weights_kept(self, kind):
+        """Load a stream's weights with the temporal cache policy (else
+        nontemporal)? Measured on the MI355X (GPT-2 small): below 4 rows every
+        weight stream (B=1 step 230 -> 221 us); from 4 rows the streams outside
+        the layer loop (the output head, read once a step) and the streams
+        whose fold is split over blocks (B=8 327 -> 312 us; keeping the other
+        layer weights too was slower: the cache then holds neither)."""
+        if self.batch < 4:
+            return True
+        return kind == 'split' or not self.loops
+
+    def w16(self, kind):
+        """The 16-byte weight load function for a stream of ``kind``."""
+        return 'ldg16_t' if self.weights_kept(kind) else 'ldg16_nt'
+
+    def nt_load(self, dt, vec, rr, idx, kept=False):
         """Streamed load of ``vec`` elements at element index ``idx`` through descriptor ``rr``."""
+        if dt == 'f16' and vec == 8 and kept:
+            return f'ldg16_t({rr}, {idx})'
         if dt == 'f16':
             return {8: f'ldg16_nt({rr}, {idx})', 4: f'ldg8_nt({rr}, {idx})', 2: f'ldg4_nt({rr}, {idx})',
                     1: f'(vh_half)(ldg4_nt({rr}, {idx}) & 0xffffu)'}[vec]
