@@ -100,7 +100,9 @@ def compile_code(src: str, arch: str = ARCH, opts=RTC_OPTS, cache: bool = True) 
     return blob
 
 
-PREFETCH_BUDGETS = (64, 32, 16)   # registers per lane a site may prefetch into, tried in turn
+PREFETCH_BUDGETS = (64, 24, 16)   # registers per lane a site may prefetch into, tried in turn (B=8, which
+                                  # spills at 64, with a 384-position cache: 308-310 us per step at 16-28,
+                                  # 320 at 32, 337 at 48; with 448 positions 24 and 32 are even)
 SPILLS_OK = 8                     # spilled registers a kernel may keep (outside its hot loops)
 
 
