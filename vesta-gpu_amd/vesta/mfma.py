@@ -24,12 +24,14 @@ fewer, KW waves share a tile, each over its own range of the fold, and the
 partial tiles are added through LDS in wave order (a fixed order, so results
 do not depend on timing). The weights of a wave's share are loaded at the
 barrier before the site when they fit in the prefetch register budget, else
-streamed MFMA_PIPE k-blocks ahead through two register sets.
+streamed through two register sets of MFMA_PIPE k-blocks each.
 """
 from __future__ import annotations
 
 MFMA_ROWS_MIN = 4            # rows from which a stream runs on the matrix cores
-MFMA_PIPE = 3                # k-blocks of weights in flight per tile when not prefetched
+MFMA_PIPE = 1                # k-blocks of weights per register set when not prefetched (two sets: the
+                             # next set's loads are in flight while one is used; B=8 315 us per step at 3,
+                             # 312.5 at 2, 311.5 at 1, 326 at 4)
 MFMA_POINTS_MIN = 8          # points a block must make (of a tile's 16 columns)
 
 
