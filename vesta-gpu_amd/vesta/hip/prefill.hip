@@ -18,7 +18,9 @@
 // accumulated in fp32 on its own and combined at the end.
 
 #define PF_E 64                 // head width
-#define PF_TILE 32              // output tile of one block: 32 rows x 32 columns
+#define PF_TILE 64              // output tile of one block: 64 rows x 64 columns
+#define PF_BK 64                // fold chunk staged in LDS per step of a block
+#define PF_LDA (PF_BK + 8)      // LDS row pitch of staged operands in halves (16 bytes of padding)
 
 // ---------------------------------------------------------------- embedding
 // Z[m] = wte[tok[m]] + wpe[t0 + p]   (gpt2.vst Q1; ids and positions
@@ -82,31 +84,13 @@ extern "C" __global__ __launch_bounds__(256) void pf_ln(const float* __restrict_
 //   2  out[m, n] = gelu_tanh(C + bias[n])             (feed-forward widening)
 //   3  qkv: n < D -> out[m, n] (queries); D <= n < 2D -> key cache;
 //      2D <= n -> value cache, at this row's sequence position (fp16)
-// A block computes a 32 x 32 tile as 2 x 2 matrix-core tiles; its four waves
-// take every fourth 32-deep step of K (a multiple of 32) and their partial
-// tiles are added through LDS in wave order, so results do not depend on
-// timing. Consecutive blocks take consecutive column tiles of one row band.
+// A block computes a 64 x 64 tile. The fold goes in chunks of 64 staged in
+// LDS (double-buffered: the next chunk's global loads are in flight while
+// one chunk is multiplied): A as fp16 halves (hi, and the remainder scaled by
+// 2^11), Wt as loaded. Wave w multiplies row tile w by the four column tiles,
+// hi and lo halves into separate accumulators. K is a multiple of 64.
 __device__ __forceinline__ float pf_gelu(float u) {
   return 0.5f * u * (1.0f + tanhf(0.7978845608028654f * (u + 0.044715f * u * u * u)));
-}
-
-#ifndef PF_UNROLL
-#define PF_UNROLL 2              // k-steps whose loads are issued together (2: measured best of 2, 4, 8)
-#endif
-
-__device__ __forceinline__ void pf_load_a(const float* __restrict__ A, int lda, int row, int M, int k,
-                                          vh_f32x4& x0, vh_f32x4& x1) {
-  if (row < M) {
-    x0 = *(const vh_f32x4*)(A + (size_t)row * lda + k);
-    x1 = *(const vh_f32x4*)(A + (size_t)row * lda + k + 4);
-  } else {
-    x0 = x1 = vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  }
-}
-
-__device__ __forceinline__ void pf_split_a(vh_f32x4 x0, vh_f32x4 x1, vh_u32x4& hi, vh_u32x4& lo) {
-  const float v[8] = {x0.x, x0.y, x0.z, x0.w, x1.x, x1.y, x1.z, x1.w};
-  vh_split8s(v, hi, lo);
 }
 
 // The epilogue of one output value c = C[m, n] (modes above).
@@ -137,6 +121,57 @@ __device__ __forceinline__ void pf_epi(int mode, int m, int n, float c, const vh
   }
 }
 
+// One chunk's global loads: thread t takes float4 f = t + 256 i of A
+// (row f / 16, columns 4 (f % 16)..+4) and 16-byte piece g = t + 256 i of Wt
+// (row g / 8, columns 8 (g % 8)..+8); rows past M or N read as zero.
+struct PfChunk {
+  vh_f32x4 a[4];
+  vh_u32x4 w[2];
+};
+
+__device__ __forceinline__ void pf_chunk_load(PfChunk& c, const float* __restrict__ A, int lda,
+                                              const vh_half* __restrict__ Wt, int M, int N, int K, int m0, int n0,
+                                              int k0) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = t + 256 * i, row = m0 + (f >> 4), col = k0 + 4 * (f & 15);
+    c.a[i] = row < M ? *(const vh_f32x4*)(A + (size_t)row * lda + col) : vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int g = t + 256 * i, n = n0 + (g >> 3), col = k0 + 8 * (g & 7);
+    c.w[i] = n < N ? ld16(Wt + (size_t)n * K + col) : vh_u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+// The chunk into LDS: A rows as hi / lo fp16 halves, Wt rows as they are.
+__device__ __forceinline__ void pf_chunk_store(const PfChunk& c, vh_half* ah, vh_half* al, vh_half* wl) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int f = t + 256 * i, row = f >> 4, col = 4 * (f & 15);
+    const float v[4] = {c.a[i].x, c.a[i].y, c.a[i].z, c.a[i].w};
+    _Float16 h[4], l[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      h[j] = (_Float16)v[j];
+      l[j] = (_Float16)((v[j] - (float)h[j]) * VH_LO_SCALE);
+    }
+    *(vh_u32x2*)(ah + row * PF_LDA + col) = vh_u32x2{
+        (unsigned)__builtin_bit_cast(unsigned short, h[0]) | ((unsigned)__builtin_bit_cast(unsigned short, h[1]) << 16),
+        (unsigned)__builtin_bit_cast(unsigned short, h[2]) | ((unsigned)__builtin_bit_cast(unsigned short, h[3]) << 16)};
+    *(vh_u32x2*)(al + row * PF_LDA + col) = vh_u32x2{
+        (unsigned)__builtin_bit_cast(unsigned short, l[0]) | ((unsigned)__builtin_bit_cast(unsigned short, l[1]) << 16),
+        (unsigned)__builtin_bit_cast(unsigned short, l[2]) | ((unsigned)__builtin_bit_cast(unsigned short, l[3]) << 16)};
+  }
+#pragma unroll
+  for (int i = 0; i < 2; ++i) {
+    const int g = t + 256 * i, n = g >> 3, col = 8 * (g & 7);
+    *(vh_u32x4*)(wl + n * PF_LDA + col) = c.w[i];
+  }
+}
+
 // `ksplit` > 1 splits K over blocks as well: block b makes part b / tiles of
 // the fold for tile b % tiles and stores its partial tile in ws[part][m][n];
 // pf_reduce then adds the parts in part order and applies the epilogue.
@@ -145,78 +180,55 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm(
     int M, int N, int K, int mode, float* __restrict__ out, int ldo,
     vh_half* __restrict__ kc, vh_half* __restrict__ vc, int P, const int* __restrict__ tp, int layer, int L,
     int tmax, int ksplit, float* __restrict__ ws) {
-  __shared__ vh_f32x4 part[VNWAVE][2][2][2][64];     // [wave][hi/lo][i][j][lane]
+  __shared__ __attribute__((aligned(16))) vh_half lds[2][3][PF_TILE * PF_LDA];   // [buffer][hi, lo, Wt]
   const int ntn = (N + PF_TILE - 1) / PF_TILE, ntm = (M + PF_TILE - 1) / PF_TILE;
   const int tile = blockIdx.x % (ntn * ntm), kp = blockIdx.x / (ntn * ntm);
   const int tn = tile % ntn, tm = tile / ntn;
-  const int nks = K / 32, ks0 = kp * nks / ksplit, ks1 = (kp + 1) * nks / ksplit;
-  const int kend = 32 * ks1;
-  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int m0 = tm * PF_TILE, n0 = tn * PF_TILE;
+  const int nch = K / PF_BK, c0 = kp * nch / ksplit, c1 = (kp + 1) * nch / ksplit;
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int r = lane & 15, kq = (lane >> 4) * 8;
-  vh_f32x4 acc[2][2], acl[2][2];
+  vh_f32x4 acc[4], acl[4];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) acc[i][j] = acl[i][j] = vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const int c0 = n0 + r, c1 = n0 + 16 + r;
-  const vh_half* w0 = Wt + (size_t)(c0 < N ? c0 : 0) * K;
-  const vh_half* w1 = Wt + (size_t)(c1 < N ? c1 : 0) * K;
-  for (int k0 = 32 * (ks0 + wave); k0 < kend; k0 += 32 * VNWAVE * PF_UNROLL) {
-    vh_f32x4 xa[PF_UNROLL][2][2];
-    vh_u32x4 bw[PF_UNROLL][2];
-#pragma unroll
-    for (int u = 0; u < PF_UNROLL; ++u) {
-      const int ks = k0 + 32 * VNWAVE * u;
-      const int k = ks + kq;
-      const bool in = ks < kend;
-      pf_load_a(A, lda, in ? m0 + r : M, M, k, xa[u][0][0], xa[u][0][1]);
-      pf_load_a(A, lda, in ? m0 + 16 + r : M, M, k, xa[u][1][0], xa[u][1][1]);
-      bw[u][0] = in && c0 < N ? ld16(w0 + k) : vh_u32x4{0u, 0u, 0u, 0u};
-      bw[u][1] = in && c1 < N ? ld16(w1 + k) : vh_u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int u = 0; u < PF_UNROLL; ++u) {
-      if (k0 + 32 * VNWAVE * u >= kend) break;
-      vh_u32x4 ah[2], al[2];
-      pf_split_a(xa[u][0][0], xa[u][0][1], ah[0], al[0]);
-      pf_split_a(xa[u][1][0], xa[u][1][1], ah[1], al[1]);
-#pragma unroll
-      for (int i = 0; i < 2; ++i)
-#pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          acc[i][j] = vh_mfma(ah[i], bw[u][j], acc[i][j]);
-          acl[i][j] = vh_mfma(al[i], bw[u][j], acl[i][j]);
-        }
-    }
+  for (int j = 0; j < 4; ++j) acc[j] = acl[j] = vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  PfChunk ch;
+  if (c0 < c1) {
+    pf_chunk_load(ch, A, lda, Wt, M, N, K, m0, n0, c0 * PF_BK);
+    pf_chunk_store(ch, lds[0][0], lds[0][1], lds[0][2]);
   }
-#pragma unroll
-  for (int i = 0; i < 2; ++i)
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      part[wave][0][i][j][lane] = acc[i][j];
-      part[wave][1][i][j][lane] = acl[i][j];
-    }
   vh_lds_sync();
-  // wave w finishes matrix-core tile (i, j) = (w / 2, w % 2)
-  const int i = wave >> 1, j = wave & 1;
-  vh_f32x4 hi = part[0][0][i][j][lane], lo = part[0][1][i][j][lane];
+  for (int c = c0; c < c1; ++c) {
+    const int cur = (c - c0) & 1;
+    if (c + 1 < c1) pf_chunk_load(ch, A, lda, Wt, M, N, K, m0, n0, (c + 1) * PF_BK);
 #pragma unroll
-  for (int w = 1; w < VNWAVE; ++w) {
-    hi += part[w][0][i][j][lane];
-    lo += part[w][1][i][j][lane];
+    for (int ks = 0; ks < PF_BK; ks += 32) {
+      const int k = ks + kq;
+      const vh_u32x4 ah = *(const vh_u32x4*)(lds[cur][0] + (16 * wave + r) * PF_LDA + k);
+      const vh_u32x4 al = *(const vh_u32x4*)(lds[cur][1] + (16 * wave + r) * PF_LDA + k);
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const vh_u32x4 b = *(const vh_u32x4*)(lds[cur][2] + (16 * j + r) * PF_LDA + k);
+        acc[j] = vh_mfma(ah, b, acc[j]);
+        acl[j] = vh_mfma(al, b, acl[j]);
+      }
+    }
+    if (c + 1 < c1) pf_chunk_store(ch, lds[cur ^ 1][0], lds[cur ^ 1][1], lds[cur ^ 1][2]);
+    vh_lds_sync();
   }
-  const int n = n0 + 16 * j + r;
-  if (n >= N) return;
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int m = m0 + 16 * i + 4 * (lane >> 4) + v;
-    if (m >= M) continue;
-    const float c = fmaf(lo[v], 1.0f / VH_LO_SCALE, hi[v]);
-    if (ksplit > 1)
-      ws[((size_t)kp * M + m) * N + n] = c;
-    else
-      pf_epi(mode, m, n, c, bias, N, out, ldo, kc, vc, P, tp, layer, L, tmax);
+  for (int j = 0; j < 4; ++j) {
+    const int n = n0 + 16 * j + r;
+    if (n >= N) continue;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const int m = m0 + 16 * wave + 4 * (lane >> 4) + v;
+      if (m >= M) continue;
+      const float cv = fmaf(acl[j][v], 1.0f / VH_LO_SCALE, acc[j][v]);
+      if (ksplit > 1)
+        ws[((size_t)kp * M + m) * N + n] = cv;
+      else
+        pf_epi(mode, m, n, cv, bias, N, out, ldo, kc, vc, P, tp, layer, L, tmax);
+    }
   }
 }
 
@@ -288,9 +300,15 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restric
   }
   vh_lds_sync();
   if (live) {
-    float o = 0.0f;
-    for (int s = 0; s <= pos; ++s) o = fmaf(ws[wave][s], h2f(vc[base + (size_t)s * D + lane]), o);
-    O[(size_t)m * D + h * PF_E + lane] = o;
+    // eight running sums (positions s mod 8), so eight rows are in flight
+    float o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+    int s = 0;
+    for (; s + 8 <= pos + 1; s += 8) {
+#pragma unroll
+      for (int u = 0; u < 8; ++u) o[u] = fmaf(ws[wave][s + u], h2f(vc[base + (size_t)(s + u) * D + lane]), o[u]);
+    }
+    for (int u = 0; s <= pos; ++s, ++u) o[u] = fmaf(ws[wave][s], h2f(vc[base + (size_t)s * D + lane]), o[u]);
+    O[(size_t)m * D + h * PF_E + lane] = ((o[0] + o[1]) + (o[2] + o[3])) + ((o[4] + o[5]) + (o[6] + o[7]));
   }
 }
 

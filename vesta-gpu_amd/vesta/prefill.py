@@ -24,18 +24,19 @@ from .launch import compile_code, lib, ok
 PREFILL_SRC = Path(__file__).resolve().parent / 'hip' / 'prefill.hip'
 PRELUDE_SRC = Path(__file__).resolve().parent / 'hip' / 'prelude.h'
 BLOCK = 256
-TILE = 32
+TILE = 64
+CHUNK = 64                    # fold depth one product step stages in LDS
 HEAD = 64
 KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_attn', 'pf_argmax')
 SPLIT_BLOCKS = 512            # a product with fewer output tiles than this splits its fold over blocks ...
-SPLIT_MIN_STEPS = 16          # ... into parts of at least this many 32-deep steps
+SPLIT_MIN_CHUNKS = 4          # ... into parts of at least this many 64-deep chunks
 MODE_PLAIN, MODE_RESID, MODE_GELU, MODE_QKV = 0, 1, 2, 3
 
 
 def supported(D, H, F):
     """Shapes the prefill kernels take: 64-wide heads and products whose fold
-    lengths are multiples of the 32-deep matrix-core step."""
-    return H * HEAD == D and D % 32 == 0 and F % 32 == 0 and D <= 8 * BLOCK
+    lengths are multiples of the 64-deep chunk a product stages at a time."""
+    return H * HEAD == D and D % CHUNK == 0 and F % CHUNK == 0 and D <= 8 * BLOCK
 
 
 def prefill_source(tmax: int) -> str:
@@ -130,7 +131,7 @@ class Prefill:
         ``pf_reduce`` adds them in order and applies the epilogue)."""
         m = self.m
         tiles = -(-M // TILE) * -(-N // TILE)
-        ks = max(1, min(-(-SPLIT_BLOCKS // tiles), (K // 32) // SPLIT_MIN_STEPS))
+        ks = max(1, min(-(-SPLIT_BLOCKS // tiles), (K // CHUNK) // SPLIT_MIN_CHUNKS))
         ws = self._workspace(ks * M * N) if ks > 1 else None
         tail = [_p(m.keys), _p(m.vals), _i(P), _p(m.t), _i(layer), _i(m.L), _i(m.tmax)]
         self._launch('pf_gemm', tiles * ks, [_p(A), _i(lda), _p(Wt), _p(bias), _i(M), _i(N), _i(K), _i(mode),
