@@ -248,9 +248,10 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce(
 
 // ---------------------------------------------------------------- attention
 // One wave per (row m, head h): scores of the query against cache positions
-// 0 .. t0 + p (gpt2.vst Q5: dot over e, divided by 8), the max-subtracted
-// softmax (Q6), and the weighted values (Q7), read from the fp16 cache the
-// qkv product just wrote. O[m, h * 64 + e] receives the head's output.
+// 0 .. t0 + p (gpt2.vst Q5: dot over e, divided by 8; a lane per position),
+// the max-subtracted softmax (Q6), and the weighted values (Q7: eight lanes
+// per position, 8 dims each), read from the fp16 cache the qkv product just
+// wrote. O[m, h * 64 + e] receives the head's output.
 // `ws` holds each wave's scores, then weights, for up to PF_TMAX positions.
 extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restrict__ Q, const vh_half* __restrict__ kc,
                                                            const vh_half* __restrict__ vc, float* __restrict__ O,
@@ -300,15 +301,40 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restric
   }
   vh_lds_sync();
   if (live) {
-    // eight running sums (positions s mod 8), so eight rows are in flight
+    // lane 8a + b sums positions s = a (mod 8) over dims 8b..8b+7 (one 16-byte
+    // load of a row per position), four positions of its residue in flight;
+    // then the eight residues are added across lanes
+    const int a = lane >> 3, b = lane & 7;
     float o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-    int s = 0;
-    for (; s + 8 <= pos + 1; s += 8) {
+    for (int s0 = 0; s0 <= pos; s0 += 32) {
+      vh_u32x4 vr[4];
+      float wv[4];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) o[u] = fmaf(ws[wave][s + u], h2f(vc[base + (size_t)(s + u) * D + lane]), o[u]);
+      for (int u = 0; u < 4; ++u) {
+        const int s = s0 + 8 * u + a;
+        const bool in = s <= pos;
+        vr[u] = in ? ld16(vc + base + (size_t)s * D + 8 * b) : vh_u32x4{0u, 0u, 0u, 0u};
+        wv[u] = in ? ws[wave][s] : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float v[8];
+        unpack8(vr[u], v);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] = fmaf(wv[u], v[j], o[j]);
+      }
     }
-    for (int u = 0; s <= pos; ++s, ++u) o[u] = fmaf(ws[wave][s], h2f(vc[base + (size_t)s * D + lane]), o[u]);
-    O[(size_t)m * D + h * PF_E + lane] = ((o[0] + o[1]) + (o[2] + o[3])) + ((o[4] + o[5]) + (o[6] + o[7]));
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      o[j] += __shfl_xor(o[j], 8, 64);
+      o[j] += __shfl_xor(o[j], 16, 64);
+      o[j] += __shfl_xor(o[j], 32, 64);
+    }
+    if (a == 0) {
+      float* dst = O + (size_t)m * D + h * PF_E + 8 * b;
+      *(vh_f32x4*)dst = vh_f32x4{o[0], o[1], o[2], o[3]};
+      *(vh_f32x4*)(dst + 4) = vh_f32x4{o[4], o[5], o[6], o[7]};
+    }
   }
 }
 

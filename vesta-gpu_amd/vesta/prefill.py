@@ -28,7 +28,8 @@ TILE = 64
 CHUNK = 64                    # fold depth one product step stages in LDS
 HEAD = 64
 KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_attn', 'pf_argmax')
-SPLIT_BLOCKS = 512            # a product with fewer output tiles than this splits its fold over blocks ...
+SPLIT_BLOCKS = 384            # a product with fewer output tiles than this splits its fold over blocks ...
+                              # (XL B=64 decode: 4.95 ms per step at 320-384, 5.18 at 256, 5.42 at 512)
 SPLIT_MIN_CHUNKS = 4          # ... into parts of at least this many 64-deep chunks
 MODE_PLAIN, MODE_RESID, MODE_GELU, MODE_QKV = 0, 1, 2, 3
 
