@@ -377,6 +377,38 @@ def test_layered_engine_matches_persistent(small):
     assert (k0[same] - k1[same]).abs().max().item() < 2e-2
 
 
+def test_layered_graph_replays_match_launches(small):
+    """Layered decode steps replayed from a captured HIP graph against the
+    same steps launched kernel by kernel: bit-identical tokens, logits and
+    cache rows at every step, with eager work and synchronizations between
+    the replays."""
+    torch = _torch()
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import random_prompts
+    hf, _, _ = small
+    B, P, G = 4, 6, 5
+    prompt = torch.from_numpy(random_prompts(B, P, 50257, seed=31)).to('cuda', torch.int32)
+    runs = []
+    for graphs in (False, True):
+        m = VestaGPT2(hf, batch=B, tmax=32, engine='layered')
+        m._pf.graphs = graphs
+        m.reset()
+        m.prefill(prompt)
+        seen = []
+        for _ in range(G):
+            m.step()
+            torch.cuda.synchronize()
+            seen.append((m.x.cpu().numpy().copy(), m.logits().float().cpu().numpy().copy()))
+            _ = (m.keys.float().sum() + 1).item()      # eager work between replays
+        runs.append((seen, m.keys.clone(), int(m.t.item())))
+        del m
+    (s0, k0, t0), (s1, k1, t1) = runs
+    assert t0 == t1 == P + G
+    for (x0, l0), (x1, l1) in zip(s0, s1):
+        assert (x0 == x1).all() and np.array_equal(l0, l1)
+    assert torch.equal(k0, k1)
+
+
 @pytest.mark.parametrize('B,engine', [(64, 'layered'), (8, 'persistent')])
 def test_xl_widths_match_oracle(B, engine):
     """GPT-2 XL widths (d 1600, 25 heads, f 6400), two layers to keep the

@@ -65,8 +65,9 @@ def _i(v):
 class Prefill:
     """The prefill kernels bound to one ``VestaGPT2``'s weights and cache."""
 
-    def __init__(self, model):
+    def __init__(self, model, graphs=True):
         self.m = model
+        self.graphs = graphs           # layered decode steps replay a captured HIP graph
         if not supported(model.D, model.H, model.W['fcw'].shape[2]):
             raise ValueError(f'prefill kernels need 64-wide heads and widths that are multiples of 32 '
                              f'(d={model.D}, H={model.H})')
@@ -84,6 +85,7 @@ class Prefill:
         self._own = {}
         self._ws = None
         self._grew = False
+        self._graph = None
         self._plans = {}
         self._plan = []
 
@@ -190,10 +192,26 @@ class Prefill:
         m = self.m
         buf = self._buffers(m.B)
         plan = self._plan_for('decode', buf, m.B, 1, m.x)
+        step = lambda: self._replay(plan)       # noqa: E731
+        if self.graphs:
+            if self._graph is None or self._graph[0] is not plan:
+                self._graph = (plan, self._capture(plan))
+            step = self._graph[1].replay
         for k in range(n):
-            self._replay(plan)
+            step()
             if tokens is not None:
                 tokens[k * m.B:(k + 1) * m.B].copy_(m.x)
+
+    def _capture(self, plan):
+        """One decode pass recorded as a HIP graph: a step is then one graph
+        launch instead of some hundred kernel launches from the host. The pass
+        has no memory sets or host reads, and every pointer it holds stays
+        fixed (the position is read on the device)."""
+        import torch
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            self._replay(plan)
+        return g
 
     def _build(self, buf, B, P, tok):
         m = self.m
