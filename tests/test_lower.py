@@ -205,3 +205,27 @@ def test_prefill_kernels_compile_for_gfx950():
         assert launch.code_spills(code) == 0
     assert supported(768, 12, 3072) and supported(1600, 25, 6400)
     assert not supported(16, 4, 64) and not supported(768, 16, 3072)
+
+
+def test_weight_cache_policy():
+    """Weights kept in the caches (temporal loads): all of them below 4 rows;
+    from 4 rows the output head (outside the layer loop) and the fold-split
+    down-projection only."""
+    import re as _re
+    for B, kept in ((1, {'R_qkvw__t', 'R_ow__t', 'R_fcw__t', 'R_pw__t', 'R_wte'}), (8, {'R_pw__t', 'R_wte'})):
+        src = lower_gpt2(B).src.split('extern "C"')[1]
+        got = set(_re.findall(r'ldg16_t\(mk_rsrc\((R_\w+)', src))
+        streamed = set(_re.findall(r'ldg16_nt\(mk_rsrc\((R_\w+)', src))
+        assert got == kept, (B, got)
+        assert not got & streamed, (B, got & streamed)
+
+
+def test_grid_choice():
+    """144 blocks below 4 rows, 192 from 4 rows; the full 256 when the default
+    grid would overflow LDS (XL widths at 8 rows) or starve the attention
+    projection of replicas (16 heads x 8 rows)."""
+    assert lower_gpt2(1).grid_max == 144
+    assert lower_gpt2(8).grid_max == 192
+    assert lower_gpt2(8, 16, (2, 1600, 25, 6400, 50257)).grid_max == 256
+    assert lower_gpt2(8, 64, (2, 1024, 16, 4096, 50257)).grid_max == 256
+    assert lower_gpt2(8, grid=160).grid_max == 160
