@@ -367,18 +367,27 @@ def prefill_line(shapes, reps=3):
             'unit': 'ms', 'higher_is_better': False, 'shapes': out}
 
 
-def xl_line(steps, warmup, batch=64, prompt=128, seed=0):
-    """GPT-2 XL greedy decode at 64 rows (128-token
-    prompts, 128 generated tokens, a 256-position cache). The persistent kernel
-    does not fit these shapes (its LDS need exceeds a CU's), so the model runs
-    each step as per-layer launches; the line says which engine ran."""
+# BASELINE.json configurations beyond the benchmark line: (model, rows, prompt,
+# generated tokens, cache positions)
+CONFIGS = {3: ('small', 32, 768, 256, 1024), 4: ('medium', 8, 256, 256, 512), '4b1': ('medium', 1, 256, 256, 512),
+           5: ('xl', 64, 128, 128, 256)}
+
+
+def config_line(key, steps=None, warmup=8, chunk=32, seed=0):
+    """Greedy decode throughput of one of BASELINE.json's other configurations
+    (random-init weights of that model, uniform-random prompts fed by the
+    batched prefill, ``warmup`` untimed steps, then ``steps`` timed steps,
+    ``chunk`` per launch). Where the persistent kernel does not fit (GPT-2 XL
+    at 64 rows: its LDS need exceeds a CU's) the model runs each step as
+    per-layer launches; the line says which engine ran."""
     import torch
     from vesta.gpt2 import VestaGPT2
     from vesta.weights import RandomGPT2, random_prompts
-    tmax = 256
+    model, batch, prompt, gen, tmax = CONFIGS[key]
+    steps = min(gen, tmax - prompt - warmup) if steps is None else steps
     if prompt + warmup + steps > tmax:
         sys.exit(f'prompt + warmup + steps must stay within the {tmax}-position cache of this configuration')
-    m = VestaGPT2(RandomGPT2('xl', seed), batch=batch, tmax=tmax)
+    m = VestaGPT2(RandomGPT2(model, seed), batch=batch, tmax=tmax)
     prompts = torch.from_numpy(random_prompts(batch, prompt, 50257, seed=1)).to('cuda', torch.int32)
     m.reset()
     m.prefill(prompts)
@@ -387,20 +396,29 @@ def xl_line(steps, warmup, batch=64, prompt=128, seed=0):
     a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     t0 = time.perf_counter()
     a.record()
-    m.step(steps)
+    left = steps
+    while left > 0:
+        m.step(min(chunk, left))
+        left -= chunk
     b.record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
     pos0 = prompt + warmup
     nbytes = sum(step_bytes(m, pos0 + k + 1) for k in range(steps))
     dev_s = a.elapsed_time(b) / 1e3
-    return {'metric': 'decode tok/s, GPT-2-XL fp16 b64 (configs[4])', 'value': round(batch * steps / elapsed, 1),
-            'unit': 'tok/s', 'ms_per_step': round(elapsed / steps * 1e3, 3), 'steps': steps, 'warmup': warmup,
-            'engine': m.engine, 'why': m.why_layered,
+    return {'metric': f'decode tok/s, GPT-2-{model} fp16 b{batch} (BASELINE.json configs {key})',
+            'value': round(batch * steps / elapsed, 1), 'unit': 'tok/s', 'ms_per_step': round(elapsed / steps * 1e3, 3),
+            'steps': steps, 'warmup': warmup, 'prompt': prompt, 'tmax': tmax, 'engine': m.engine,
+            'why': m.why_layered, 'grid': m.k.grid if m.k is not None else None,
             'hbm': {'achieved': round(nbytes / dev_s / 1e9, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
                     'frac': round(nbytes / dev_s / 1e9 / HBM_PEAK_GBPS, 4),
                     'bytes_per_step_MB': round(step_bytes(m, pos0 + steps // 2) / 1e6, 1)},
-            'data': 'synthetic: random-init GPT-2-XL fp16 weights N(0,0.02) seed 0, uniform-random prompts'}
+            'data': f'synthetic: random-init GPT-2-{model} fp16 weights N(0,0.02) seed {seed}, uniform-random prompts'}
+
+
+def xl_line(steps, warmup):
+    """GPT-2 XL greedy decode at 64 rows."""
+    return config_line(5, steps, warmup)
 
 
 def roofline(cfg, peak):
@@ -444,7 +462,17 @@ def main():
     ap.add_argument('--xl', action='store_true',
                     help='instead of the benchmark line, measure GPT-2 XL decode at 64 rows (configs[4]); '
                          'give --steps 120 or fewer')
+    ap.add_argument('--config', default='', metavar='KEY',
+                    help='instead of the benchmark line, measure decode of another configuration: 3 (small, '
+                         'B=32, 768-token prompts), 4 / 4b1 (medium, B=8 / B=1), 5 (XL, B=64)')
     args = ap.parse_args()
+    if args.config:
+        key = int(args.config) if args.config.isdigit() else args.config
+        if key not in CONFIGS:
+            sys.exit(f'unknown configuration {args.config}')
+        print(json.dumps(config_line(key, None if '--steps' not in sys.argv else args.steps, args.warmup)),
+              flush=True)
+        return
     if args.xl:
         print(json.dumps(xl_line(args.steps, args.warmup)), flush=True)
         return
