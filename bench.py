@@ -88,7 +88,7 @@ def run_config(B, steps, warmup, chunk, seed=0):
     out = dict(B=B, steps=steps, tok_s=B * steps / elapsed, ms_per_step=elapsed / steps * 1e3,
                kernel_ms_per_launch=sum(kern_ms) / len(kern_ms), steps_per_launch=chunk,
                bytes_per_step_MB=step_bytes(m, pos0 + steps // 2) / 1e6, achieved_GBps=achieved,
-               grid=m.k.grid, regs=m.k.attrs['regs'], barriers_per_step=m.low.barriers_per_launch + 1,
+               grid=m.k.grid, regs=m.k.attrs['regs'], barriers_per_step=m.low.barriers_per_launch + ('feedback visible to the next step' in m.low.src),
                weight_MB=m.weight_bytes / 1e6, tmax=tmax, kernel=m.low.name,
                src_sha=hashlib.sha256(m.low.src.encode()).hexdigest()[:16],
                algorithmic_bytes_per_launch=sum(per_launch_bytes) / len(per_launch_bytes))
