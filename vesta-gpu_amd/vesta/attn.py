@@ -343,7 +343,7 @@ class AttnMixin:
                 pre = []
                 ix = [self.index(x, {c5.contig: ('d_', 'int')}, pre, '    ') for x in st5.prefix_idx]
                 lines += pre
-                lines.append(f'    {wp}[{q}] = {self.w16("proj")}({self.rsrc(st5.src)}, (unsigned)({self.addr(ix, rs[:-1])}) + '
+                lines.append(f'    {wp}[{q}] = {self.w16("proj", st5.src)}({self.rsrc(st5.src)}, (unsigned)({self.addr(ix, rs[:-1])}) + '
                              f'{st5.c0}u + (unsigned)({foff}) + (unsigned)cl_ * 8u);')
                 lines.append(f'  }} else {wp}[{q}] = vh_u32x4{{0u, 0u, 0u, 0u}};')
                 lines.append('}')

@@ -29,6 +29,7 @@ import math
 from dataclasses import dataclass
 
 PREFETCH_VGPRS = 64          # registers per lane one site may hold prefetched weights in (default budget)
+PROJ_KEPT_BYTES = 64 << 20   # out-projection weights (all layers) kept in the caches up to this size
 PI_STREAM = 2                # slots whose loads are issued together when not prefetched
 PB_MAX = 2                   # points one lane group makes at once (each LDS read of the other factor serves them all)
                              # (B=1, the output head's stream: 229 us per step at 4 and 4, 219 at 2 and 2)
@@ -580,20 +581,24 @@ class StreamMixin:
             return {8: 'vh_u32x4', 4: 'vh_u32x2', 2: 'unsigned', 1: 'vh_half'}[vec]
         return {4: 'vh_f32x4', 2: 'vh_f32x2', 1: 'float'}[vec]
 
-    def weights_kept(self, kind):
+    def weights_kept(self, kind, src=None):
         """Load a stream's weights with the temporal cache policy (else
         nontemporal)? Measured on the MI355X (GPT-2 small): below 4 rows every
         weight stream (B=1 step 230 -> 221 us); from 4 rows the streams outside
-        the layer loop (the output head, read once a step) and the streams
-        whose fold is split over blocks (B=8 327 -> 312 us; keeping the other
-        layer weights too was slower: the cache then holds neither)."""
+        the layer loop (the output head, read once a step), the streams whose
+        fold is split over blocks (B=8 327 -> 312 us) and the attention
+        out-projection when its copies over all layers are small (B=8
+        320 -> 311 us); keeping the other layer weights too was slower: the
+        cache then holds neither."""
         if self.batch < 4:
             return True
+        if kind == 'proj' and src is not None:
+            return 2 * math.prod(self.res[src][0]) <= PROJ_KEPT_BYTES
         return kind == 'split' or not self.loops
 
-    def w16(self, kind):
-        """The 16-byte weight load function for a stream of ``kind``."""
-        return 'ldg16_t' if self.weights_kept(kind) else 'ldg16_nt'
+    def w16(self, kind, src=None):
+        """The 16-byte weight load function for a stream of ``kind`` (over residue ``src``)."""
+        return 'ldg16_t' if self.weights_kept(kind, src) else 'ldg16_nt'
 
     def nt_load(self, dt, vec, rr, idx, kept=False):
         """Streamed load of ``vec`` elements at element index ``idx`` through descriptor ``rr``."""
