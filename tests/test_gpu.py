@@ -210,12 +210,15 @@ def test_medium_long_context_matches_oracle():
 def test_batch32_long_cache_matches_oracle(small):
     """configs[2]'s batch (32 rows: more (row, head) points than blocks, the
     out-projection as its own stream, contractions on VALU row chunks) with a
-    512-position cache (chunked softmax), rows checked against the oracle."""
+    512-position cache (chunked softmax), rows checked against the oracle;
+    the persistent kernel asked for (at 32 rows 'auto' takes the layered
+    engine)."""
     from vesta.gpt2 import VestaGPT2
     from vesta.weights import random_prompts
     hf, W, text = small
     T = 512
-    m = VestaGPT2(hf, batch=32, tmax=T)
+    m = VestaGPT2(hf, batch=32, tmax=T, engine='persistent')
+    assert m.engine == 'persistent'
     pr = random_prompts(32, 60, 50257, seed=23)
     gen, last = _prefill_and_generate(m, pr, 5)
     _check_rows(text, W, pr, gen, last, T, [0, 13, 31])
@@ -425,7 +428,7 @@ def test_xl_widths_match_oracle(B, engine):
     m = VestaGPT2(hf, batch=B, tmax=16)
     assert m.engine == engine, m.why_layered
     if engine == 'layered':
-        assert 'LDS' in m.why_layered, m.why_layered
+        assert 'LDS' in m.why_layered or m.why_layered.startswith(f'{B} rows'), m.why_layered
     P, G = 4, 3
     pr = random_prompts(B, P, 50257, seed=22)
     m.reset()

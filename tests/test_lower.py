@@ -238,3 +238,12 @@ def test_grid_choice():
     assert lower_gpt2(8, 16, (2, 1600, 25, 6400, 50257)).grid_max == 256
     assert lower_gpt2(8, 64, (2, 1024, 16, 4096, 50257)).grid_max == 256
     assert lower_gpt2(8, grid=160).grid_max == 160
+
+
+def test_xl_widths_at_64_rows_exceed_a_cu_of_lds():
+    """GPT-2 XL widths at 64 rows need more LDS per block than a CU holds,
+    even on the widest grid: the persistent kernel cannot run there, which
+    is one of the reasons ``VestaGPT2(engine='auto')`` takes the layered engine."""
+    from vesta.lower import LDS_BYTES
+    low = lower_gpt2(64, 16, (2, 1600, 25, 6400, 50257))
+    assert low.grid_max == 256 and low.shared_bytes > LDS_BYTES

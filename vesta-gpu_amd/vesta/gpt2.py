@@ -24,6 +24,9 @@ from .lower import lower
 
 LDS_PER_CU = 160 * 1024      # bytes of LDS one block of the persistent kernel may use
 SPILLS_LAYERED = 64          # spilled registers beyond which 'auto' takes the layered engine
+LAYERED_ROWS = 32            # rows from which 'auto' takes the layered engine (GPT-2 small, 32 rows,
+                             # 1024-position cache: 1.39 ms per step layered, 1.50 persistent; 16 rows:
+                             # 0.93 layered, 0.58 persistent)
 
 SHAPE_PROGRAMS = {(12, 768, 12): 'gpt2.vst', (24, 1024, 16): 'gpt2_medium.vst', (48, 1600, 25): 'gpt2_xl.vst'}
 
@@ -66,9 +69,10 @@ class VestaGPT2:
         per launch (the reference design); 'layered' runs each step as a
         sequence of ordinary per-layer launches (``vesta.prefill``: the
         multi-token prefill kernels with one position per row); 'auto' takes
-        the persistent kernel unless it does not fit the device (LDS beyond a
-        CU's 160 KB, or more than ``SPILLS_LAYERED`` spilled registers), as
-        for GPT-2 XL at 64 rows. With the layered engine ``low`` and ``k``
+        the layered engine from ``LAYERED_ROWS`` rows (where it is faster) and
+        the persistent kernel below, unless that does not fit the device (LDS
+        beyond a CU's 160 KB, or more than ``SPILLS_LAYERED`` spilled
+        registers), as for GPT-2 XL at 64 rows. With the layered engine ``low`` and ``k``
         are None."""
         import torch
         if engine not in ('auto', 'persistent', 'layered'):
@@ -104,12 +108,15 @@ class VestaGPT2:
         self._R, self._bps, self._timing = R, blocks_per_sm, timing
         self.low, self.k, self._kp, self._pf = None, None, None, None
         self.engine, self.why_layered = 'persistent', None
+        from .prefill import supported
         if engine == 'layered':
             self.why_layered = 'asked for'
+        elif engine == 'auto' and batch >= LAYERED_ROWS and supported(D, H, F):
+            self.why_layered = f'{batch} rows (layered is faster from {LAYERED_ROWS} rows)'
         else:
             self.why_layered = self._persistent(text, spec, batch, timing, blocks_per_sm, strict=engine == 'persistent')
         if self.k is None:
-            from .prefill import Prefill, supported
+            from .prefill import Prefill
             if not supported(D, H, F):
                 raise ValueError(f'the persistent kernel does not fit ({self.why_layered}) and the layered '
                                  f'engine needs 64-wide heads and widths that are multiples of 32')
