@@ -338,20 +338,139 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restric
   }
 }
 
+// One position per row (a decode step): one block per (row m, head h), every
+// thread of the block on the positions 0 .. t0, so that a step's cache rows
+// are read with a block's worth of loads in flight instead of a wave's. The
+// same arithmetic as pf_attn: each score a dot over e in order, / 8; the
+// max-subtracted softmax (block-wide maximum and sum); the weighted values
+// with wave w, lane 8a + b on positions s = 8w + a (mod 32), dims 8b..8b+7,
+// the four waves' partial outputs added in order through LDS.
+extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restrict__ Q, const vh_half* __restrict__ kc,
+                                                            const vh_half* __restrict__ vc, float* __restrict__ O,
+                                                            const int* __restrict__ tp, int layer, int L, int tmax,
+                                                            int H) {
+  __shared__ float qs[PF_E];
+  __shared__ float ws[PF_TMAX];
+  __shared__ float red[VNWAVE];
+  __shared__ float part[VNWAVE][PF_E];
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+  const int m = blockIdx.x / H, h = blockIdx.x % H;      // grid: rows * H blocks exactly
+  const int D = H * PF_E;
+  const int at = *tp;
+  const int pos = at < tmax ? at : tmax - 1;
+  const size_t base = (size_t)(m * L + layer) * tmax * D + (size_t)h * PF_E;
+  if (tid < PF_E) qs[tid] = Q[(size_t)m * D + h * PF_E + tid];
+  __syncthreads();
+  float mx = -INFINITY;
+  for (int s = tid; s <= pos; s += VBLOCK) {
+    const vh_half* kr = kc + base + (size_t)s * D;
+    float acc = 0.0f;
+#pragma unroll
+    for (int e = 0; e < PF_E; e += 8) {
+      float kv[8];
+      unpack8(ld16(kr + e), kv);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fmaf(qs[e + j], kv[j], acc);
+    }
+    const float sc = acc * 0.125f;      // / 8, exact
+    ws[s] = sc;
+    mx = fmaxf(mx, sc);
+  }
+  mx = wave_red_max(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  mx = red[0];
+#pragma unroll
+  for (int w = 1; w < VNWAVE; ++w) mx = fmaxf(mx, red[w]);
+  __syncthreads();                      // red is reused for the sum
+  float sum = 0.0f;
+  for (int s = tid; s <= pos; s += VBLOCK) {
+    const float ex = expf(ws[s] - mx);
+    ws[s] = ex;
+    sum += ex;
+  }
+  sum = wave_red_sum(sum);
+  if (lane == 0) red[wave] = sum;
+  __syncthreads();
+  sum = red[0];
+#pragma unroll
+  for (int w = 1; w < VNWAVE; ++w) sum += red[w];
+  for (int s = tid; s <= pos; s += VBLOCK) ws[s] = ws[s] / sum;
+  __syncthreads();
+  const int a = lane >> 3, b = lane & 7;
+  float o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = 8 * wave; s0 <= pos; s0 += 32 * 4) {
+    vh_u32x4 vr[4];
+    float wv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = s0 + 32 * u + a;
+      const bool in = s <= pos;
+      vr[u] = in ? ld16(vc + base + (size_t)s * D + 8 * b) : vh_u32x4{0u, 0u, 0u, 0u};
+      wv[u] = in ? ws[s] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float v[8];
+      unpack8(vr[u], v);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = fmaf(wv[u], v[j], o[j]);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    o[j] += __shfl_xor(o[j], 8, 64);
+    o[j] += __shfl_xor(o[j], 16, 64);
+    o[j] += __shfl_xor(o[j], 32, 64);
+  }
+  if (a == 0) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) part[wave][8 * b + j] = o[j];
+  }
+  __syncthreads();
+  if (tid < PF_E) {
+    float r = part[0][tid];
+#pragma unroll
+    for (int w = 1; w < VNWAVE; ++w) r += part[w][tid];
+    O[(size_t)m * D + h * PF_E + tid] = r;
+  }
+}
+
 // ---------------------------------------------------------------- argmax
 // Per row of logits [B, V]: the largest value, a tie to the lowest id
-// (gpt2.vst Q10). Writes the token into x (the next step's input) and, as a
-// float, into `next`; block 0 advances the position counter by P. One block
-// per row.
-extern "C" __global__ __launch_bounds__(256) void pf_argmax(const float* __restrict__ logit, int V,
-                                                             int* __restrict__ x, float* __restrict__ next,
+// (gpt2.vst Q10), in two launches so that a row is read by S blocks at once.
+// pf_argmax_part: block b * S + s takes chunk s of row b and writes its pair
+// (value, id) to pv / pi. pf_argmax: one block per row combines the S pairs
+// (the rule picks the same pair in any order), writes the token into x (the
+// next step's input) and, as a float, into `next`; block 0 advances the
+// position counter by P.
+extern "C" __global__ __launch_bounds__(256) void pf_argmax_part(const float* __restrict__ logit, int V, int S,
+                                                                  float* __restrict__ pv, int* __restrict__ pi) {
+  __shared__ float rv[VNWAVE];
+  __shared__ int ri[VNWAVE];
+  const int b = blockIdx.x / S, s = blockIdx.x % S;
+  const int chunk = (V + S - 1) / S;
+  const int n0 = s * chunk, n1 = min(V, n0 + chunk);
+  const float* lg = logit + (size_t)b * V;
+  float best = -INFINITY;
+  int id = V;
+#pragma unroll 4
+  for (int n = n0 + (int)threadIdx.x; n < n1; n += VBLOCK) argmax_pair(best, id, lg[n], n);
+  block_argmax(best, id, rv, ri);
+  if (threadIdx.x == 0) {
+    pv[blockIdx.x] = best;
+    pi[blockIdx.x] = id;
+  }
+}
+
+extern "C" __global__ __launch_bounds__(256) void pf_argmax(const float* __restrict__ pv, const int* __restrict__ pi,
+                                                             int S, int* __restrict__ x, float* __restrict__ next,
                                                              int* __restrict__ tp, int P) {
   __shared__ float rv[VNWAVE];
   __shared__ int ri[VNWAVE];
-  const float* lg = logit + (size_t)blockIdx.x * V;
   float best = -INFINITY;
-  int id = V;
-  for (int n = threadIdx.x; n < V; n += blockDim.x) argmax_pair(best, id, lg[n], n);
+  int id = 0x7fffffff;
+  for (int k = threadIdx.x; k < S; k += VBLOCK) argmax_pair(best, id, pv[blockIdx.x * S + k], pi[blockIdx.x * S + k]);
   block_argmax(best, id, rv, ri);
   if (threadIdx.x == 0) {
     x[blockIdx.x] = id;
