@@ -63,7 +63,10 @@ from pathlib import Path
 import numpy as np
 
 from .interp import parse
+from .analysis import (BIG, PRIV_SIZE, PRIV_WORK, STAGE_MAX, Analysis, LowerError, batch_lift, replace_node,
+                       top_folds)
 from .attn import AttnMixin
+from .ir import defined_names, is_node, stmt_exprs, transform, walk
 from .stream import StreamMixin, PREFETCH_VGPRS
 from .mfma import MfmaMixin
 
@@ -82,13 +85,9 @@ GRID_FEW_ROWS = 144           # ... below 4 rows (measured B=1: 227 us on 144, 2
                               # 156, 252 on 192, 274 on 96)
 LDS_BYTES = 160 * 1024        # LDS of one CU (the kernel runs one block per CU)
 REG_MAX = 8                   # register axes: at most this many accumulator rows per lane
-PRIV_SIZE = 8192              # a private value holds at most this many floats
-PRIV_WORK = 1 << 17           # ... and costs at most this many operations per block
 PRIV_BUDGET = 16384           # all live private values together: 64 KB of LDS
-STAGE_MAX = 8192              # a private statement reads at most this many floats of locals
 GROUP_WORK = 1 << 14          # a group statement does at most this much work per leading point
 ATTN_WORK = 1 << 17           # ... or this much in a group that streams the key/value cache
-BIG = 1 << 16                 # a residue this large is streamed, never recomputed per point
 LANE_MIN = 32                 # lane-split a fold only if it is at least this long
 GRIDRED_MIN = 1 << 14         # grid reduction for a fold at least this long into few points
 GRIDRED_POINTS = 8
@@ -127,138 +126,10 @@ class Lowered:
 
 
 # ------------------------------------------------------------------ AST helpers
-def is_node(e):
-    return isinstance(e, tuple) and bool(e) and isinstance(e[0], str)
-
-
-def nodes(e):
-    """Every expression node of e, parents first."""
-    if not is_node(e):
-        return
-    yield e
-    for x in e[1:]:
-        if isinstance(x, list):
-            for y in x:
-                yield from nodes(y)
-        elif is_node(x):
-            yield from nodes(x)
-
-
-def rebuild(e, f):
-    """Apply f bottom-up to every expression node."""
-    if not is_node(e):
-        return e
-    k = e[0]
-    if k == 'idx':
-        e = ('idx', e[1], [rebuild(i, f) for i in e[2]])
-    elif k == 'fold':
-        e = ('fold', e[1], e[2], rebuild(e[3], f))
-    elif k == 'neg':
-        e = ('neg', rebuild(e[1], f))
-    elif k == 'call':
-        e = ('call', e[1], rebuild(e[2], f))
-    elif k == 'bin':
-        e = ('bin', e[1], rebuild(e[2], f), rebuild(e[3], f))
-    elif k == 'fork':
-        e = ('fork', rebuild(e[1], f), rebuild(e[2], f), rebuild(e[3], f))
-    return f(e)
-
-
-def stmt_exprs(s):
-    k = s[0]
-    if k == 'let':
-        return [s[3]]
-    if k == 'emit':
-        return list(s[2]) + [s[3]]
-    if k == 'step':
-        return [s[4]]
-    if k == 'ret':
-        return [s[1]]
-    if k == 'axis':
-        return [s[2]]
-    return []
-
-
-def local_names(stmts, out=None):
-    out = set() if out is None else out
-    for s in stmts:
-        if s[0] in ('let', 'step'):
-            out.add(s[1])
-        if s[0] == 'step':
-            out.add(s[5])
-            local_names(s[6], out)
-    return out
-
-
-def batch_lift(stmts, B, per_token, bax='bt'):
-    """A batch is the same program asked of B tokens at once (reference
-    lower.py:109-132): every named value and every per-token residue gains a
-    leading token axis ``bax`` of extent B."""
-    locs = local_names(stmts)
-    per_token = set(per_token)
-
-    def f(e):
-        if e[0] == 'name' and e[1] in per_token and e[1] not in locs:
-            return ('idx', e[1], [('name', bax)])
-        if e[0] == 'idx' and (e[1] in locs or e[1] in per_token):
-            return ('idx', e[1], [('name', bax)] + list(e[2]))
-        return e
-
-    def lift(ss):
-        out = []
-        for s in ss:
-            k = s[0]
-            if k == 'axis':
-                out.append(('axis', s[1], rebuild(s[2], f)))
-            elif k == 'recv':
-                out.append(s)
-            elif k == 'emit':
-                ix = [rebuild(i, f) for i in s[2]]
-                out.append(('emit', s[1], ([('name', bax)] + ix) if s[1] in per_token else ix, rebuild(s[3], f)))
-            elif k == 'let':
-                out.append(('let', s[1], [bax] + list(s[2]), rebuild(s[3], f)))
-            elif k == 'step':
-                out.append(('step', s[1], [bax] + list(s[2]), s[3], rebuild(s[4], f), s[5], lift(s[6])))
-            elif k == 'ret':
-                out.append(('ret', rebuild(s[1], f)))
-        return out
-
-    return [('axis', bax, ('num', B))] + lift(stmts)
-
-
-def top_folds(e):
-    """Outermost fold nodes of e."""
-    if not is_node(e):
-        return []
-    if e[0] == 'fold':
-        return [e]
-    out = []
-    for x in e[1:]:
-        for y in (x if isinstance(x, list) else [x]):
-            out += top_folds(y)
-    return out
-
-
-def replace_node(e, target, repl):
-    """e with the node ``target`` (by identity) replaced by ``repl``."""
-    if e is target:
-        return repl
-    if not is_node(e):
-        return e
-    k = e[0]
-    if k == 'idx':
-        return ('idx', e[1], [replace_node(i, target, repl) for i in e[2]])
-    if k == 'fold':
-        return ('fold', e[1], e[2], replace_node(e[3], target, repl))
-    if k == 'neg':
-        return ('neg', replace_node(e[1], target, repl))
-    if k == 'call':
-        return ('call', e[1], replace_node(e[2], target, repl))
-    if k == 'bin':
-        return ('bin', e[1], replace_node(e[2], target, repl), replace_node(e[3], target, repl))
-    if k == 'fork':
-        return ('fork',) + tuple(replace_node(x, target, repl) for x in e[1:])
-    return e
+# Tree traversal lives in vesta.ir; these names are what the code generators use.
+nodes = walk
+rebuild = transform
+local_names = defined_names
 
 
 def show(e):
@@ -323,11 +194,8 @@ class Contraction:
     vec: int = 1
 
 
-class LowerError(ValueError):
-    pass
 
-
-class Lowering(StreamMixin, MfmaMixin, AttnMixin):
+class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
     NWAVE, BLOCK, REG_MAX = NWAVE, BLOCK, REG_MAX
     show_stmt = staticmethod(show_stmt)
     nodes_of = staticmethod(nodes)
@@ -398,174 +266,7 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
         self.find_splits(stmts)
         self.layout(stmts)
 
-    # ------------------------------------------------------------ program facts
-    def scan(self, ss):
-        for s in ss:
-            k = s[0]
-            if k == 'axis':
-                e = s[2]
-                if e[0] == 'num':
-                    self.static[s[1]] = int(e[1])
-                else:
-                    if s[1] not in self.axis_max:
-                        raise LowerError(f'axis {s[1]} is set at run time: give its upper bound in axis_max')
-                    self.static[s[1]] = int(self.axis_max[s[1]])
-                    self.dynamic[s[1]] = e
-            elif k == 'recv':
-                if s[1] not in self.res:
-                    raise NameError(f'residue {s[1]} not supplied')
-            elif k == 'emit':
-                if s[1] not in self.res:
-                    raise NameError(f'residue {s[1]} not supplied')
-                self.emitted.add(s[1])
-                self.emit_stmts.append(s)
-            elif k == 'let':
-                self.axes_of[s[1]] = tuple(s[2])
-            elif k == 'step':
-                self.steps.add(s[3])
-                self.axes_of[s[1]] = self.axes_of[s[5]] = tuple(s[2])
-                self.scan(s[6])
-
-    def is_axis(self, n):
-        return n in self.static and n not in self.steps
-
-    def ext_c(self, a):
-        """C expression of an axis extent."""
-        return f'E_{a}' if a in self.dynamic else str(self.static[a])
-
-    def size(self, axes):
-        return math.prod(self.static[a] for a in axes) if axes else 1
-
-    def normalise(self, ss):
-        """Bare reads of locals with axes become reads at their own axes."""
-        def f(e):
-            if e[0] == 'name' and e[1] in self.axes_of and self.axes_of[e[1]]:
-                return ('idx', e[1], [('name', a) for a in self.axes_of[e[1]]])
-            return e
-        out = []
-        for s in ss:
-            k = s[0]
-            if k == 'let':
-                out.append(('let', s[1], s[2], rebuild(s[3], f)))
-            elif k == 'emit':
-                out.append(('emit', s[1], [rebuild(i, f) for i in s[2]], rebuild(s[3], f)))
-            elif k == 'step':
-                out.append(('step', s[1], s[2], s[3], rebuild(s[4], f), s[5], self.normalise(s[6])))
-            elif k == 'ret':
-                out.append(('ret', rebuild(s[1], f)))
-            else:
-                out.append(s)
-        return out
-
-    def free_axes(self, e):
-        """Axes e depends on outside its own folds."""
-        if e[0] == 'name':
-            if self.is_axis(e[1]):
-                return {e[1]}
-            return set(self.axes_of.get(e[1], ()))
-        if e[0] == 'fold':
-            return self.free_axes(e[3]) - {e[2]}
-        out = set()
-        for x in e[1:]:
-            for y in (x if isinstance(x, list) else [x]):
-                if is_node(y):
-                    out |= self.free_axes(y)
-        return out
-
-    def reads(self, e):
-        """Names of locals and emitted residues e reads."""
-        out = set()
-        for n in nodes(e):
-            if n[0] in ('name', 'idx') and (n[1] in self.axes_of or n[1] in self.emitted):
-                out.add(n[1])
-        return out
-
-    def res_reads(self, e):
-        return [n for n in nodes(e) if n[0] == 'idx' and n[1] in self.res]
-
-    def big_reads(self, e):
-        return [n for n in self.res_reads(e)
-                if n[1] not in self.emitted and math.prod(self.res[n[1]][0]) > BIG]
-
-    def fold_work(self, e):
-        if not is_node(e):
-            return 1
-        if e[0] == 'fold':
-            return self.static[e[2]] * self.fold_work(e[3])
-        w = 1
-        for x in e[1:]:
-            for y in (x if isinstance(x, list) else [x]):
-                if is_node(y):
-                    w = max(w, self.fold_work(y))
-        return w
-
     # ------------------------------------------------------------ rewrites
-    def hoist(self, ss):
-        """Lift folds that ignore an output axis into their own statement."""
-        out = []
-        for s in ss:
-            if s[0] == 'step':
-                out.append(s[:6] + (self.hoist(s[6]),))
-                continue
-            if s[0] != 'let':
-                out.append(s)
-                continue
-            name, axes, e = s[1], list(s[2]), s[3]
-            new = []
-
-            def lift(fnode):
-                fa = self.free_axes(fnode)
-                if fa >= set(axes) or not fa <= set(axes):
-                    return fnode
-                self.tmp += 1
-                h = f'_h{self.tmp}'
-                hax = [a for a in axes if a in fa]
-                self.axes_of[h] = tuple(hax)
-                new.append(('let', h, hax, fnode))
-                return ('idx', h, [('name', a) for a in hax]) if hax else ('name', h)
-
-            e2 = e
-            for fnode in top_folds(e):
-                e2 = replace_node(e2, fnode, lift(fnode))
-            out += new + [('let', name, axes, e2)]
-        return out
-
-    def find_aliases(self, ss):
-        """carry <- init / carry <- ret need no copy when the value is used
-        only there and its statement does not read the carry; the step's
-        result always shares the carry's storage."""
-        defs, uses = {}, {}
-
-        def index(ss):
-            for s in ss:
-                if s[0] == 'let':
-                    defs[s[1]] = s
-                for e in stmt_exprs(s):
-                    for n in nodes(e):
-                        if n[0] in ('name', 'idx') and n[1] in self.axes_of:
-                            uses[n[1]] = uses.get(n[1], 0) + 1
-                if s[0] == 'step':
-                    index(s[6])
-        index(ss)
-
-        def walk(ss):
-            for s in ss:
-                if s[0] != 'step':
-                    continue
-                _, name, axes, var, init, carry, blk = s
-                walk(blk)
-                rets = [b for b in blk if b[0] == 'ret']
-                if len(rets) != 1:
-                    raise SyntaxError(f'step {name} needs exactly one ->')
-                for e in (init, rets[0][1]):
-                    if e[0] == 'idx' and e[1] in defs and uses.get(e[1]) == 1 \
-                            and [('name', a) for a in self.axes_of[e[1]]] == list(e[2]) \
-                            and self.axes_of[e[1]] == tuple(axes) \
-                            and carry not in self.reads(defs[e[1]][3]) and e[1] not in self.outputs:
-                        self.alias[e[1]] = carry
-                self.alias[name] = carry
-        walk(ss)
-
     def find_peels(self, ss):
         """A step loop whose carry starts from a replicated statement (one
         reading residues only): in the first iteration, reads of the carry
@@ -606,96 +307,7 @@ class Lowering(StreamMixin, MfmaMixin, AttnMixin):
             raise LowerError(f'first value of {r} needs statements of its own')
         return lv, self.as_float(v, t)
 
-    def root(self, n):
-        while n in self.alias:
-            n = self.alias[n]
-        return n
-
-    def big_contraction(self, s):
-        e = s[3] if s[0] == 'let' else None
-        return e is not None and any(self.big_reads(f[3]) for f in top_folds(e))
-
-    def inline(self, ss):
-        """Substitute fold-free values into the statements that read them."""
-        out = list(ss)
-        i = 0
-        while i < len(out):
-            s = out[i]
-            if s[0] == 'step':
-                out[i] = s[:6] + (self.inline(s[6]),)
-                i += 1
-                continue
-            if s[0] != 'let':
-                i += 1
-                continue
-            name = s[1]
-
-            def reads_it(t):
-                if t[0] == 'step':
-                    return name in self.reads(t[4]) or any(reads_it(x) for x in t[6])
-                return any(name in self.reads(e) for e in stmt_exprs(t))
-            readers = [t for t in out[i + 1:] if reads_it(t)]
-            carries = set(self.alias.values())
-            if (readers and not top_folds(s[3]) and name not in self.outputs and name not in self.alias
-                    and name not in carries and all(t[0] in ('let', 'emit') and not self.big_contraction(t)
-                                                     for t in readers)):
-                axes, body = list(s[2]), s[3]
-
-                def subst(e, axes=axes, body=body, name=name):
-                    def f(n):
-                        if n[0] == 'idx' and n[1] == name:
-                            m = dict(zip(axes, n[2]))
-                            return rebuild(body, lambda x: m[x[1]] if x[0] == 'name' and x[1] in m else x)
-                        if n[0] == 'name' and n[1] == name:
-                            return body
-                        return n
-                    return rebuild(e, f)
-                for j in range(i + 1, len(out)):
-                    t = out[j]
-                    if t[0] == 'let':
-                        out[j] = ('let', t[1], t[2], subst(t[3]))
-                    elif t[0] == 'emit':
-                        out[j] = ('emit', t[1], [subst(x) for x in t[2]], subst(t[3]))
-                del out[i]
-                self.inlined.append(name)
-                continue
-            i += 1
-        return out
-
     # ------------------------------------------------------------ placement
-    def place_all(self, ss):
-        self.place = {}           # id(stmt) -> placement string
-        self.info = {}            # id(stmt) -> Contraction / extra info
-        self.groups = {}          # id(first stmt) -> (lead axes, [stmts])
-        self.in_group = set()
-        self.private = set()
-        self.argmax = {}          # id(max statement) -> the lowest-index statement that reads it
-        self.group_local = {}     # id(first stmt of a group) -> names kept in LDS
-        self.readers_of = {}      # name -> ids of statements reading it
-        def index(ss):
-            for t in ss:
-                for e in stmt_exprs(t):
-                    for n in self.reads(e):
-                        self.readers_of.setdefault(n, set()).add(id(t))
-                if t[0] == 'step':
-                    index(t[6])
-        index(ss)
-        self._place_block(ss)
-
-    def priv_ok(self, s):
-        name = s[1]
-        if name in self.outputs or name in self.alias or name in set(self.alias.values()):
-            return False
-        size = self.size(s[2])
-        if size > PRIV_SIZE or size * self.fold_work(s[3]) > PRIV_WORK:
-            return False
-        if any(a in self.dynamic for a in s[2]):
-            return False
-        foot = sum(self.size(self.axes_of[n]) for n in self.reads(s[3]) if n in self.axes_of and n not in self.private)
-        if foot > STAGE_MAX:
-            return False
-        return not any(math.prod(self.res[n[1]][0]) > BIG or n[1] in self.emitted for n in self.res_reads(s[3]))
-
     def _place_block(self, ss):
         i = 0
         made, made_axes = set(), None      # results of the last contraction and its epilogue
