@@ -34,8 +34,13 @@ for p in (os.path.join(ROOT, 'vesta-gpu_amd'), ROOT):
         sys.path.insert(0, p)
 
 HBM_PEAK_GBPS = 8000.0
+FP16_MFMA_PEAK_TFLOPS = 2500.0          # MI355X dense fp16 matrix-core peak
 TRAFFIC_FILE = os.path.join(ROOT, 'profiles', 'traffic.json')
 PROMPT, GEN = 128, 256
+MEAN_CTX = PROMPT + (GEN + 1) / 2       # mean context of configs[1]'s generated tokens: 256.5
+BENCH_TMAX = 448                        # cache positions of the benchmarked kernels
+REPEATS = 5                             # timed repeats; the median is reported (reference g0_bench.py:166-180)
+CV_MAX = 0.05                           # repeats must agree within this coefficient of variation
 
 
 def step_bytes(m, n_ctx):
@@ -44,55 +49,163 @@ def step_bytes(m, n_ctx):
     return m.weight_bytes + m.kv_bytes(n_ctx)
 
 
-def run_config(B, steps, warmup, chunk, seed=0):
-    import torch
+def step_flops(m, n_ctx):
+    """Algorithmic FLOP of one decode step of B rows at context n_ctx: the
+    four layer products and the tied head (2 per multiply-add), scores and
+    weighted values over the context."""
+    F = m.W['fcw'].shape[2]
+    V = m.W['wte'].shape[0]
+    return 2 * m.B * (m.L * (4 * m.D * m.D + 2 * m.D * F) + V * m.D) + 4 * m.B * m.L * n_ctx * m.D
+
+
+def timed_start(steps, warmup):
+    """Position of the first timed step. The timed steps are centred on the
+    configuration's mean context (mean n_ctx of the timed steps = 256.5), after
+    the prompt and the warm-up steps."""
+    return max(PROMPT + warmup, int(round(MEAN_CTX - 0.5 - steps / 2)))
+
+
+def bench_tmax(steps, warmup):
+    need = timed_start(steps, warmup) + steps
+    return BENCH_TMAX if need <= BENCH_TMAX else min(1024, -(-need // 64) * 64)
+
+
+def make_model(B, tmax=BENCH_TMAX, seed=0):
+    """The benchmarked model: GPT-2 small, random-init fp16 weights (seed 0),
+    B rows, a ``tmax``-position cache. The parity tests build the kernels they
+    check through here, so they check exactly the timed ones."""
     from vesta.gpt2 import VestaGPT2
-    from vesta.weights import RandomGPT2, random_prompts
-    hf = RandomGPT2('small', seed)
-    # the cache holds the default run (prompt, 8 warm-up steps, GEN tokens) or
-    # more, so shorter runs (profiling) use the same kernel as the default one
-    tmax = PROMPT + max(steps + warmup, GEN + 8)
-    tmax = min(1024, ((tmax + 63) // 64) * 64)
-    m = VestaGPT2(hf, batch=B, tmax=tmax)
-    prompts = torch.from_numpy(random_prompts(B, PROMPT, 50257, seed=1)).to('cuda', torch.int32)
+    from vesta.weights import RandomGPT2
+    return VestaGPT2(RandomGPT2('small', seed), batch=B, tmax=tmax)
+
+
+def bench_prompts(B):
+    from vesta.weights import random_prompts
+    return random_prompts(B, PROMPT, 50257, seed=1)
+
+
+def position(m, prompts, p0, warmup):
+    """Reset, prefill the prompt (untimed, all positions together), decode up to
+    position p0 - warmup (untimed), then ``warmup`` untimed warm-up steps: the
+    next step runs at position p0."""
     m.reset()
-    m.prefill(prompts)          # one launch, one token per step (untimed)
-    m.warm(warmup)              # untimed warm-up steps (same program, prefill kernel)
-    torch.cuda.synchronize()
-    plan = []
-    left = steps
+    m.prefill(prompts)
+    m.warm(p0 - PROMPT - warmup)
+    m.warm(warmup)
+
+
+def chunks(steps, chunk):
+    plan, left = [], steps
     while left > 0:
-        n = min(chunk, left)
-        plan.append(n)
-        left -= n
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in plan]
+        plan.append(min(chunk, left))
+        left -= plan[-1]
+    return plan
+
+
+def _cv(xs):
+    import statistics
+    return statistics.pstdev(xs) / statistics.mean(xs) if len(xs) > 1 else 0.0
+
+
+def run_config(B, steps, warmup, chunk, repeats=REPEATS, seed=0, single=True):
+    """Decode throughput of GPT-2 small at B rows: ``repeats`` times (reset,
+    prefill, positioning and warm-up steps, untimed) ``steps`` timed steps,
+    ``chunk`` per launch (tokens fed back on the device); median and CV of
+    the repeats. With ``single``, also the reference caller's protocol: one
+    launch per step and a token copy after each (reference g0_bench.py:175-178),
+    through the same program under its own kernel symbol so kernel profiles of
+    the two legs stay apart."""
+    import statistics
+    import torch
+    tmax = bench_tmax(steps, warmup)
+    m = make_model(B, tmax, seed)
+    prompts = torch.from_numpy(bench_prompts(B)).to('cuda', torch.int32)
+    p0 = timed_start(steps, warmup)
+    plan = chunks(steps, chunk)
     tokens = torch.zeros(steps * B, dtype=torch.int32, device='cuda')
-    torch.cuda.synchronize()
-    t0 = time.perf_counter()
-    off = 0
-    for (a, b), n in zip(ev, plan):
-        a.record()
-        m.step(n, tokens[off * B:])
-        b.record()
-        off += n
-    torch.cuda.synchronize()
-    elapsed = time.perf_counter() - t0
-    kern_ms = [a.elapsed_time(b) for a, b in ev]
-    # algorithmic bytes of each launch: context grows by one per step
-    pos0 = PROMPT + warmup
-    per_launch_bytes, pos = [], pos0
-    for n in plan:
-        per_launch_bytes.append(sum(step_bytes(m, pos + k + 1) for k in range(n)))
-        pos += n
-    achieved = sum(per_launch_bytes) / (sum(kern_ms) / 1e3) / 1e9
-    out = dict(B=B, steps=steps, tok_s=B * steps / elapsed, ms_per_step=elapsed / steps * 1e3,
-               kernel_ms_per_launch=sum(kern_ms) / len(kern_ms), steps_per_launch=chunk,
-               bytes_per_step_MB=step_bytes(m, pos0 + steps // 2) / 1e6, achieved_GBps=achieved,
-               grid=m.k.grid, regs=m.k.attrs['regs'], barriers_per_step=m.low.barriers_per_launch + ('feedback visible to the next step' in m.low.src),
-               weight_MB=m.weight_bytes / 1e6, tmax=tmax, kernel=m.low.name,
-               src_sha=hashlib.sha256(m.low.src.encode()).hexdigest()[:16],
-               algorithmic_bytes_per_launch=sum(per_launch_bytes) / len(per_launch_bytes))
+    host, dev, first, same = [], [], None, True
+    for _ in range(repeats):
+        position(m, prompts, p0, warmup)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in plan]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        off = 0
+        for (a, b), n in zip(ev, plan):
+            a.record()
+            m.step(n, tokens[off * B:])
+            b.record()
+            off += n
+        torch.cuda.synchronize()
+        host.append(time.perf_counter() - t0)
+        dev.append(sum(a.elapsed_time(b) for a, b in ev) / 1e3)
+        got = tokens.cpu()
+        first = got if first is None else first
+        same = same and bool(torch.equal(got, first))
+    m.check()
+    med_host, med_dev = statistics.median(host), statistics.median(dev)
+    nbytes = sum(step_bytes(m, p0 + k + 1) for k in range(steps))
+    nflop = sum(step_flops(m, p0 + k + 1) for k in range(steps))
+    out = dict(B=B, steps=steps, tok_s=B * steps / med_host, ms_per_step=med_host / steps * 1e3,
+               cv=_cv(host), device_ms_per_step=med_dev / steps * 1e3, device_cv=_cv(dev), repeats=repeats,
+               repeats_identical_tokens=same, positions=[p0, p0 + steps - 1],
+               mean_context=p0 + (steps + 1) / 2, kernel_ms_per_launch=med_dev * 1e3 / len(plan),
+               steps_per_launch=steps / len(plan), launches=len(plan),
+               bytes_per_step_MB=nbytes / steps / 1e6, achieved_GBps=nbytes / med_dev / 1e9,
+               flop_per_step=nflop / steps, achieved_TFLOPs=nflop / med_dev / 1e12,
+               algorithmic_bytes_per_launch=nbytes / len(plan), weight_MB=m.weight_bytes / 1e6, tmax=tmax,
+               engine=m.engine)
+    if m.k is not None:
+        out.update(grid=m.k.grid, regs=m.k.attrs['regs'], kernel=m.low.name,
+                   barriers_per_step=m.low.barriers_per_launch + ('feedback visible to the next step' in m.low.src),
+                   src_sha=hashlib.sha256(m.low.src.encode()).hexdigest()[:16])
+    else:
+        out.update(grid=None, regs=None, kernel='layered', barriers_per_step=0, src_sha=None)
+    if single:
+        one = []
+        step1 = m.variant(f'vesta_step1_b{B}') if m.k is not None else None
+        for _ in range(repeats):
+            position(m, prompts, p0, warmup)
+            hist = []
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(steps):
+                if step1 is not None:
+                    step1.launch(1)
+                else:
+                    m.step()
+                hist.append(m.x.clone())
+            torch.cuda.synchronize()
+            one.append(time.perf_counter() - t0)
+        m.check()
+        med = statistics.median(one)
+        out['one_launch_per_step'] = dict(tok_s=round(B * steps / med, 1), ms_per_step=round(med / steps * 1e3, 4),
+                                          cv=round(_cv(one), 4),
+                                          tokens_equal=bool(torch.equal(torch.stack(hist).view(-1).cpu(), first)))
     del m
+    torch.cuda.empty_cache()
+    return out
+
+
+def device_bandwidth():
+    """Copy and read bandwidth of this device through PyTorch (reference
+    g0_bench.py:60-75: 512 MB fp16 buffers, best of 20)."""
+    import torch
+    n = 256 * 1024 * 1024
+    a = torch.empty(n, dtype=torch.float16, device='cuda').normal_()
+    b = torch.empty_like(a)
+    out = {}
+    for name, fn, mult in (('copy_GBs', lambda: b.copy_(a), 2), ('read_GBs', lambda: a.sum(), 1)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        ts = []
+        for _ in range(20):
+            t0 = time.perf_counter()
+            fn()
+            torch.cuda.synchronize()
+            ts.append(time.perf_counter() - t0)
+        out[name] = round(mult * n * 2 / min(ts) / 1e9, 1)
+    del a, b
     torch.cuda.empty_cache()
     return out
 
@@ -403,8 +516,10 @@ def config_line(key, steps=None, warmup=8, chunk=32, seed=0):
     b.record()
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
+    m.check()
     pos0 = prompt + warmup
     nbytes = sum(step_bytes(m, pos0 + k + 1) for k in range(steps))
+    nflop = sum(step_flops(m, pos0 + k + 1) for k in range(steps))
     dev_s = a.elapsed_time(b) / 1e3
     return {'metric': f'decode tok/s, GPT-2-{model} fp16 b{batch} (BASELINE.json configs {key})',
             'value': round(batch * steps / elapsed, 1), 'unit': 'tok/s', 'ms_per_step': round(elapsed / steps * 1e3, 3),
@@ -413,6 +528,10 @@ def config_line(key, steps=None, warmup=8, chunk=32, seed=0):
             'hbm': {'achieved': round(nbytes / dev_s / 1e9, 1), 'peak': HBM_PEAK_GBPS, 'unit': 'GB/s',
                     'frac': round(nbytes / dev_s / 1e9 / HBM_PEAK_GBPS, 4),
                     'bytes_per_step_MB': round(step_bytes(m, pos0 + steps // 2) / 1e6, 1)},
+            'mfma': {'achieved': round(nflop / dev_s / 1e12, 2), 'peak': FP16_MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+                     'frac': round(nflop / dev_s / 1e12 / FP16_MFMA_PEAK_TFLOPS, 5),
+                     'flop_per_step_G': round(nflop / steps / 1e9, 3)},
+            'storage': STORAGE,
             'data': f'synthetic: random-init GPT-2-{model} fp16 weights N(0,0.02) seed {seed}, uniform-random prompts'}
 
 
@@ -423,10 +542,10 @@ def xl_line(steps, warmup):
 
 def roofline(cfg, peak):
     """The roofline object of one configuration's kernel: algorithmic bytes
-    per launch over the launch duration (HIP events on the launch stream),
-    and the counter-measured HBM traffic per launch when profiles/traffic.json
-    holds a measurement of this exact kernel source."""
-    rec = measured_traffic(cfg['kernel'], cfg['src_sha'])
+    per launch over the launch duration (HIP events on the launch stream,
+    median repeat), and the counter-measured HBM traffic per launch when
+    profiles/traffic.json holds a measurement of this exact kernel source."""
+    rec = measured_traffic(cfg['kernel'], cfg['src_sha']) if cfg['src_sha'] else None
     return {'bound': 'hbm', 'achieved': round(cfg['achieved_GBps'], 1), 'peak': peak, 'unit': 'GB/s',
             'frac': round(cfg['achieved_GBps'] / peak, 4),
             'traffic': round(rec['traffic']) if rec else None,
@@ -438,6 +557,26 @@ def roofline(cfg, peak):
             'kernel_ms_per_launch': round(cfg['kernel_ms_per_launch'], 4)}
 
 
+def mfma_line(cfg):
+    """Matrix-core utilisation: algorithmic FLOP over the timed device time
+    against MI355X's dense fp16 peak (the products of a batched step run on
+    the fp16 matrix cores; the activations go in as two fp16 halves, so the
+    hardware does about twice the algorithmic product work)."""
+    return {'achieved': round(cfg['achieved_TFLOPs'], 2), 'peak': FP16_MFMA_PEAK_TFLOPS, 'unit': 'TFLOP/s',
+            'frac': round(cfg['achieved_TFLOPs'] / FP16_MFMA_PEAK_TFLOPS, 5),
+            'flop_per_step_G': round(cfg['flop_per_step'] / 1e9, 3)}
+
+
+def timing_line(cfg):
+    return {'repeats': cfg['repeats'], 'cv': round(cfg['cv'], 4), 'device_cv': round(cfg['device_cv'], 4),
+            'cv_ok': cfg['cv'] <= CV_MAX, 'repeats_identical_tokens': cfg['repeats_identical_tokens'],
+            'device_ms_per_step': round(cfg['device_ms_per_step'], 4)}
+
+
+STORAGE = ('f16 weights and key/value cache, f32 math; from 4 rows the products run on the fp16 matrix cores '
+           'with each activation split into two fp16 halves (22 significant bits) and f32 accumulation')
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument('--gpus', type=int, default=1)
@@ -445,7 +584,8 @@ def main():
     ap.add_argument('--warmup', type=int, default=8)
     ap.add_argument('--batch', type=int, default=8)
     ap.add_argument('--chunk', type=int, default=32)
-    ap.add_argument('--cpu-steps', type=int, default=2)
+    ap.add_argument('--repeats', type=int, default=REPEATS)
+    ap.add_argument('--cpu-steps', type=int, default=8)
     ap.add_argument('--no-cpu', action='store_true')
     ap.add_argument('--pmc-summary', nargs=3, metavar=('FETCH_CSV', 'WRITE_CSV', 'BENCH_LOG'),
                     help='summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of '
@@ -494,13 +634,14 @@ def main():
         print(json.dumps({'error': 'this build runs on one GPU: the decode step is one persistent kernel on one '
                                    'device; multi-GPU sharding is designed but not built (run with --gpus 1)'}))
         sys.exit(2)
-    if args.steps + args.warmup + PROMPT > 1024:
-        sys.exit('prompt + warmup + steps must stay within the 1024 learned positions')
+    if timed_start(args.steps, args.warmup) + args.steps > 1024:
+        sys.exit('the timed steps must stay within the 1024 learned positions')
     if args.calibrate_copy > 0:
         calibration_copy(args.calibrate_copy)
-    main_cfg = run_config(args.batch, args.steps, args.warmup, args.chunk)
-    b1 = run_config(1, args.steps, args.warmup, args.chunk)
+    main_cfg = run_config(args.batch, args.steps, args.warmup, args.chunk, args.repeats)
+    b1 = run_config(1, args.steps, args.warmup, args.chunk, args.repeats)
     peak = HBM_PEAK_GBPS
+    p0, p1 = main_cfg['positions']
     line = {
         'metric': 'decode tok/s, GPT-2-small fp16 b1/b8; HBM GB/s as % of MI355X peak',
         'value': round(main_cfg['tok_s'], 1),
@@ -514,14 +655,23 @@ def main():
         'vs_baseline': None,
         'dtype': 'f32',
         'data': 'synthetic: random-init GPT-2-small fp16 weights N(0,0.02) seed 0, uniform-random prompts',
-        'config': {'workload': f'GPT-2 small greedy decode, B={args.batch}, {PROMPT}-token prompts, '
-                               f'{args.steps} generated tokens (BASELINE.json configs[1])',
-                   'batch': args.batch, 'prompt': PROMPT, 'storage': 'f16 weights and key/value cache, f32 math',
-                   'steps_per_launch': args.chunk, 'barriers_per_step': main_cfg['barriers_per_step']},
+        'config': {'workload': f'GPT-2 small greedy decode, B={args.batch}, {PROMPT}-token prompts (BASELINE.json '
+                               f'configs[1]: 256 generated tokens, mean context {MEAN_CTX}); the {args.steps} '
+                               f'timed steps run at positions {p0}..{p1} (mean context '
+                               f'{main_cfg["mean_context"]}), after an untimed prefill and decode to position '
+                               f'{p0}; median of {args.repeats} repeats',
+                   'batch': args.batch, 'prompt': PROMPT, 'positions': [p0, p1], 'storage': STORAGE,
+                   'engine': main_cfg['engine'], 'steps_per_launch': main_cfg['steps_per_launch'],
+                   'barriers_per_step': main_cfg['barriers_per_step']},
+        'timing': timing_line(main_cfg),
         'roofline': roofline(main_cfg, peak),
+        'mfma': mfma_line(main_cfg),
+        'one_launch_per_step': main_cfg.get('one_launch_per_step'),
         'b1': {'tok_s': round(b1['tok_s'], 1), 'ms_per_step': round(b1['ms_per_step'], 4),
-               'barriers_per_step': b1['barriers_per_step'], **roofline(b1, peak)},
+               'barriers_per_step': b1['barriers_per_step'], 'timing': timing_line(b1),
+               'one_launch_per_step': b1.get('one_launch_per_step'), **roofline(b1, peak)},
     }
+    line['device_bandwidth'] = device_bandwidth()
     if not args.no_cpu:
         line['cpu_baseline'] = cpu_baseline(args.batch, args.cpu_steps)
     print(json.dumps(line), flush=True)

@@ -146,3 +146,60 @@ def test_errors_raised():
     with pytest.raises(SyntaxError):
         interp.run('residue a[i]\naxis i = 2\nz[i] = fold step k: a as c\n  y[i] = c[i]\nend\n',
                    {'a': np.ones(2, np.float32)})
+
+
+# ---------------------------------------------------------------- full-size fixtures
+CONFIG_KEYS = ('c1', 'c2', 'c3', 'c4', 'c4b1', 'c5')
+
+
+@pytest.mark.parametrize('key', CONFIG_KEYS)
+def test_config_fixture_is_consistent(key):
+    """Each fixture records the configuration it caches (tests/golden/make_configs.py)
+    and holds plausible decode output: ids inside the vocabulary, top-2
+    margins >= 0, the signature's first id the argmax (its value the largest)."""
+    import importlib.util
+    path = os.path.join(GOLD, f'config_{key}.npz')
+    if not os.path.exists(path):
+        pytest.fail(f'{path} is missing: run tests/golden/make_configs.py {key}')
+    spec = importlib.util.spec_from_file_location('make_configs', os.path.join(GOLD, 'make_configs.py'))
+    mc = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(mc)
+    g = np.load(path)
+    model, B, P, gen, rows, _ = mc.CONFIGS[key]
+    assert (str(g['model']), int(g['B']), int(g['P']), int(g['gen'])) == (model, B, P, gen)
+    assert g['rows'].tolist() == list(rows)
+    assert g['tokens'].shape == (len(rows), gen) and g['margins'].shape == (len(rows), gen)
+    assert ((g['tokens'] >= 0) & (g['tokens'] < 50257)).all() and (g['margins'] >= 0).all()
+    steps = g['sig_steps'].tolist()
+    assert steps == mc.signature_steps(gen)
+    assert g['sig_ids'].shape[:2] == (len(rows), len(steps))
+    # the first signature id of a step is its argmax, i.e. the step's token
+    for i in range(len(rows)):
+        for j, k in enumerate(steps):
+            assert g['sig_ids'][i, j, 0] == g['tokens'][i, k]
+            assert g['sig_vals'][i, j, 0] == g['sig_vals'][i, j].max()
+    assert (g['sig_ids'][..., mc.N_TOP:] == mc.fixed_ids()).all()
+
+
+def test_config1_fixture_is_row0_of_config2():
+    """Same weights and the same prompt generator: config 1's single row is
+    config 2's first."""
+    a, b = np.load(os.path.join(GOLD, 'config_c1.npz')), np.load(os.path.join(GOLD, 'config_c2.npz'))
+    assert (a['tokens'][0] == b['tokens'][0]).all() and (a['margins'][0] == b['margins'][0]).all()
+
+
+def test_config2_fixture_matches_the_live_oracle():
+    """Re-derive the start of config 2's first row with the oracle (128 prompt
+    steps and 4 generated tokens): tokens, margins and signature logits bit
+    for bit."""
+    from vesta import PROGRAMS
+    from vesta.weights import RandomGPT2
+    g = np.load(os.path.join(GOLD, 'config_c2.npz'))
+    W = decode.oracle_weights(stacked(RandomGPT2('small', 0).numpy_state(), 12))
+    text = (PROGRAMS / 'gpt2.vst').read_text()
+    prompt = random_prompts(8, 128, 50257, seed=1)[0]
+    out = decode.greedy(text, W, prompt, 4, 132, keep_logits=True)
+    assert out['tokens'].tolist() == g['tokens'][0, :4].tolist()
+    assert np.array_equal(out['margins'].astype(np.float32), g['margins'][0, :4])
+    for j in range(4):
+        assert np.array_equal(out['logits'][j][g['sig_ids'][0, j]], g['sig_vals'][0, j])

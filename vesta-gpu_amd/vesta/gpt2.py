@@ -3,6 +3,13 @@
     m = VestaGPT2(hf, dtype='f16', batch=8, tmax=1024)
     m.reset(); m.x.copy_(tok); m.t.fill_(p); m.step()     # one decode step
     m.logits(), m.next()                                    # views, no sync
+    m.check()                                               # raises if a launch failed (syncs)
+
+The object keeps a host copy of the position to refuse steps past the last
+cache row. It is known after ``reset()``, ``prefill()`` and ``seek(p)`` and
+advanced by each step; a caller that writes ``t`` itself (as above) should
+say so with ``seek(p)``, else the check is off until the next ``reset`` or
+``prefill``.
 
 With feedback on, each step writes its chosen token into x and advances t,
 so generation is back-to-back launches with nothing from the host between.
@@ -106,7 +113,9 @@ class VestaGPT2:
                                              outputs=('logit', 'next'),
                                              feedback={'x': 'next', 't': 1} if feedback else None))
         self._R, self._bps, self._timing = R, blocks_per_sm, timing
-        self.low, self.k, self._kp, self._pf = None, None, None, None
+        self.low, self.k, self._pf = None, None, None
+        self._variants = {}
+        self._pos = 0
         self.engine, self.why_layered = 'persistent', None
         from .prefill import supported
         if engine == 'layered':
@@ -148,26 +157,72 @@ class VestaGPT2:
         self.keys.zero_()
         self.vals.zero_()
         self.t.zero_()
+        self._pos = 0
+
+    def _advance(self, n, what):
+        """Keep the host's copy of the position (known after ``reset`` and
+        ``prefill``, advanced by every step this object runs; unknown after the
+        caller writes ``t`` itself until the next ``reset``/``prefill``) and
+        refuse steps past the last cache row: the engines must never be asked
+        for a position the cache does not hold."""
+        pos = getattr(self, '_pos', None)
+        if pos is not None:
+            if pos + n > self.tmax:
+                raise ValueError(f'{what}: positions {pos}..{pos + n - 1} exceed the cache (tmax {self.tmax})')
+            self._pos = pos + n
+
+    def seek(self, pos):
+        """Set the position to ``pos`` (device and host copies)."""
+        if not 0 <= pos < self.tmax:
+            raise ValueError(f'position {pos} outside the cache (tmax {self.tmax})')
+        self.t.fill_(int(pos))
+        self._pos = int(pos)
 
     def step(self, n=1, tokens=None):
         """One decode step (the reference API); ``n`` > 1 runs n steps in one
-        launch, writing each step's tokens into ``tokens`` [n, B] if given."""
-        if tokens is not None and tokens.numel() < n * self.B:
-            raise ValueError(f'tokens holds {tokens.numel()} ids, {n * self.B} needed')
+        launch, writing each step's tokens into ``tokens`` (contiguous int32,
+        e.g. [n, B]; step k at flat offsets k * B ..) if given."""
+        if tokens is not None:
+            if not (tokens.is_cuda and tokens.dtype == self.x.dtype and tokens.is_contiguous()):
+                raise TypeError('tokens must be a contiguous int32 device tensor')
+            if tokens.numel() < n * self.B:
+                raise ValueError(f'tokens holds {tokens.numel()} ids, {n * self.B} needed')
+        self._advance(n, 'step')
         if self.k is None:
             self._pf.decode(n, tokens)
             return
         self.k.launch(n, tokens)
 
-    def _prefill_kernel(self):
-        """The same program under its own symbol, for prompt feeding and
-        warm-up (so profiles of the decode kernel hold decode launches only)."""
-        if self._kp is None:
+    def check(self):
+        """Raise if an earlier launch reported a failure: a grid barrier of the
+        persistent kernel that gave up waiting, or an activation beyond the
+        fp16 range on a matrix-core product (one device synchronisation)."""
+        for k in [self.k, *self._variants.values()]:
+            if k is not None:
+                k.check()
+        if self._pf is not None:
+            self._pf.check()
+
+    def variant(self, name):
+        """The persistent kernel of this model's program under another symbol
+        (the source is otherwise the same), bound to the same residues: for
+        launches that should show apart in kernel profiles (prompt feeding,
+        warm-up, a one-launch-per-step timing). Built once per name."""
+        if self.k is None:
+            raise RuntimeError('the layered engine has no persistent kernel')
+        v = self._variants.get(name)
+        if v is None:
             text, spec, kw = self._lower_args
-            low = lower_fitted(lower, text, spec, **kw, timing=self._timing, kernel_name=f'vesta_prefill_b{self.B}')
-            self._kp = Kernel(low, blocks_per_sm=self._bps)
-            self._kp.bind(self._R)
-        return self._kp
+            low = lower_fitted(lower, text, spec, **kw, timing=self._timing, kernel_name=name)
+            v = Kernel(low, blocks_per_sm=self._bps)
+            v.bind(self._R)
+            self._variants[name] = v
+        return v
+
+    def _prefill_kernel(self):
+        """The program under its own symbol for prompt feeding and warm-up (so
+        profiles of the decode kernel hold decode launches only)."""
+        return self.variant(f'vesta_prefill_b{self.B}')
 
     def prefill(self, prompt, tokens=None, mode='auto'):
         """Feed a prompt [B, P] (int32 device tensor) at positions t .. t + P - 1;
@@ -191,9 +246,14 @@ class VestaGPT2:
         if mode == 'batched' and (tokens is not None or not fits):
             raise ValueError('batched prefill writes no per-step tokens and needs 64-wide heads and widths '
                              'that are multiples of 32')
+        if tokens is not None and not (tokens.is_cuda and tokens.dtype == self.x.dtype and tokens.is_contiguous()
+                                       and tokens.numel() >= P * self.B):
+            raise TypeError(f'tokens must be a contiguous int32 device tensor of at least {P * self.B} ids')
+        self.check()
         t0 = int(self.t.item())
         if t0 + P > self.tmax:
             raise ValueError(f'positions {t0}..{t0 + P - 1} exceed the cache (tmax {self.tmax})')
+        self._pos = t0 + P
         if mode == 'batched' or (mode == 'auto' and tokens is None and fits):
             if self._pf is None:
                 from .prefill import Prefill
@@ -202,9 +262,10 @@ class VestaGPT2:
             return
         ins = prompt.t().contiguous().to(dtype=self.x.dtype)
         if self.k is None:
+            flat = None if tokens is None else tokens.view(-1)
             for i in range(P):
                 self.x.copy_(ins[i])
-                self._pf.decode(1, None if tokens is None else tokens[i * self.B:])
+                self._pf.decode(1, None if flat is None else flat[i * self.B:(i + 1) * self.B])
             return
         self.x.copy_(ins[0])
         self._prefill_kernel().launch(P, tokens, ins)
@@ -212,6 +273,8 @@ class VestaGPT2:
 
     def warm(self, n):
         """n decode steps through the prefill kernel (untimed warm-up)."""
+        if n > 0:
+            self._advance(n, 'warm')
         if n > 0 and self.k is None:
             self._pf.decode(n)
         elif n > 0:

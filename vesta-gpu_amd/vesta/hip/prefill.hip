@@ -146,7 +146,8 @@ __device__ __forceinline__ void pf_chunk_load(PfChunk& c, const float* __restric
 }
 
 // The chunk into LDS: A rows as hi / lo fp16 halves, Wt rows as they are.
-__device__ __forceinline__ void pf_chunk_store(const PfChunk& c, vh_half* ah, vh_half* al, vh_half* wl) {
+// `bad` is raised when an A value is beyond the fp16 range (see vh_beyond_half8).
+__device__ __forceinline__ void pf_chunk_store(const PfChunk& c, vh_half* ah, vh_half* al, vh_half* wl, bool& bad) {
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -155,6 +156,7 @@ __device__ __forceinline__ void pf_chunk_store(const PfChunk& c, vh_half* ah, vh
     _Float16 h[4], l[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
+      bad |= !(__builtin_fabsf(v[j]) <= VH_HALF_MAX);
       h[j] = (_Float16)v[j];
       l[j] = (_Float16)((v[j] - (float)h[j]) * VH_LO_SCALE);
     }
@@ -179,7 +181,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm(
     const float* __restrict__ A, int lda, const vh_half* __restrict__ Wt, const vh_half* __restrict__ bias,
     int M, int N, int K, int mode, float* __restrict__ out, int ldo,
     vh_half* __restrict__ kc, vh_half* __restrict__ vc, int P, const int* __restrict__ tp, int layer, int L,
-    int tmax, int ksplit, float* __restrict__ ws) {
+    int tmax, int ksplit, float* __restrict__ ws, unsigned* __restrict__ err) {
   __shared__ __attribute__((aligned(16))) vh_half lds[2][3][PF_TILE * PF_LDA];   // [buffer][hi, lo, Wt]
   const int ntn = (N + PF_TILE - 1) / PF_TILE, ntm = (M + PF_TILE - 1) / PF_TILE;
   const int tile = blockIdx.x % (ntn * ntm), kp = blockIdx.x / (ntn * ntm);
@@ -192,9 +194,10 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm(
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = acl[j] = vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   PfChunk ch;
+  bool bad = false;
   if (c0 < c1) {
     pf_chunk_load(ch, A, lda, Wt, M, N, K, m0, n0, c0 * PF_BK);
-    pf_chunk_store(ch, lds[0][0], lds[0][1], lds[0][2]);
+    pf_chunk_store(ch, lds[0][0], lds[0][1], lds[0][2], bad);
   }
   vh_lds_sync();
   for (int c = c0; c < c1; ++c) {
@@ -212,9 +215,10 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm(
         acl[j] = vh_mfma(al, b, acl[j]);
       }
     }
-    if (c + 1 < c1) pf_chunk_store(ch, lds[cur ^ 1][0], lds[cur ^ 1][1], lds[cur ^ 1][2]);
+    if (c + 1 < c1) pf_chunk_store(ch, lds[cur ^ 1][0], lds[cur ^ 1][1], lds[cur ^ 1][2], bad);
     vh_lds_sync();
   }
+  if (bad) stc_u(err, VH_ERR_RANGE);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int n = n0 + 16 * j + r;

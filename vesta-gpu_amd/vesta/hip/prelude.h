@@ -312,6 +312,20 @@ __device__ __forceinline__ void vh_split8s(const float* v, vh_u32x4& hi, vh_u32x
   lo = __builtin_bit_cast(vh_u32x4, l);
 }
 
+// The matrix-core path carries activations as fp16 halves, so a value beyond
+// the largest fp16 (65504) cannot go in: the split would give an infinite hi
+// half. True if any of the eight values is beyond it (or is not a number);
+// callers then raise VH_ERR_RANGE in the error word, and the host (which
+// reads the word after the launch) refuses the results.
+#define VH_HALF_MAX 65504.0f
+#define VH_ERR_RANGE 2u
+__device__ __forceinline__ bool vh_beyond_half8(const float* v) {
+  bool b = false;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) b |= !(__builtin_fabsf(v[j]) <= VH_HALF_MAX);
+  return b;
+}
+
 // hi + lo / 2048 for partial sums of the two halves (see vh_split8s).
 __device__ __forceinline__ float vh_hilo(float h, float l) { return fmaf(l, 1.0f / VH_LO_SCALE, h); }
 
@@ -431,8 +445,13 @@ __device__ __forceinline__ void grid_arrive(unsigned* bar) {
 // loads issued ahead of time in flight, so its polls complete as soon as the
 // counters answer) each watch one counter. A wait that does not end within
 // VH_SPIN_LIMIT polls (seconds) gives up and raises the error word
-// bar[VH_BAR_LINE * 9 + 1] (only a broken launch configuration can get there).
+// bar[VH_BAR_ERROR] (only a launch whose blocks are not all resident can get
+// there); every other wait looks at that word once per VH_ERR_POLLS polls and
+// stops waiting once it is set, so a broken launch ends soon. The host reads
+// the word (Kernel.check) and discards the launch's results.
 #define VH_POLL_WAVE (VNWAVE - 1)
+#define VH_BAR_ERROR (VH_BAR_LINE * 9 + 1)
+#define VH_ERR_POLLS 4096u
 
 __device__ __forceinline__ void grid_wait(unsigned* bar, unsigned nblk, unsigned k) {
   if ((int)(threadIdx.x >> 6) == VH_POLL_WAVE) {
@@ -449,9 +468,10 @@ __device__ __forceinline__ void grid_wait(unsigned* bar, unsigned nblk, unsigned
       if (__all(done)) break;
       __builtin_amdgcn_s_sleep(1);
       if (++n > VH_SPIN_LIMIT) {
-        if (g == 0) stc_u(bar + VH_BAR_LINE * 9 + 1, 1u);
+        if (g == 0) stc_u(bar + VH_BAR_ERROR, 1u);
         break;
       }
+      if ((n % VH_ERR_POLLS) == 0u && __builtin_amdgcn_readfirstlane(ldc_u(bar + VH_BAR_ERROR)) != 0u) break;
     }
   }
   vh_lds_sync();

@@ -12,10 +12,13 @@ calls that need them raise.
 """
 from __future__ import annotations
 
+import atexit
 import ctypes
 import hashlib
 import os
+import sys
 import threading
+import weakref
 
 LIB_DIR = os.path.join(os.path.dirname(os.path.abspath(__file__)), '_lib')
 LIB_PATH = os.path.join(LIB_DIR, 'libvesta_hip.so')
@@ -61,6 +64,40 @@ def lib():
             L.vh_error_string.argtypes, L.vh_error_string.restype = [ctypes.c_int], ctypes.c_char_p
             _lib = L
         return _lib
+
+
+# Objects holding a loaded module. They are unloaded by an exit hook, which
+# runs while the interpreter and the HIP runtime are whole; left to garbage
+# collection at interpreter shutdown, a module can outlive the runtime's own
+# teardown (and a profiler's finalisation, which then sees a code object it
+# has already forgotten).
+_live = weakref.WeakSet()
+_hook = []
+
+
+def track(owner):
+    """Register ``owner`` (it has ``close()``) for unloading at exit."""
+    _live.add(owner)
+    if not _hook:
+        atexit.register(_close_all)
+        _hook.append(True)
+
+
+def _close_all():
+    for owner in list(_live):
+        try:
+            owner.close()
+        except Exception:
+            pass
+
+
+def unload(module_handle):
+    """Wait for the device, then unload a module (skipped once the interpreter
+    is shutting down: the exit hook has already unloaded what it could)."""
+    if sys.is_finalizing():
+        return
+    lib().vh_synchronize()                  # no launch of this module may still be running
+    lib().vh_module_unload(module_handle)
 
 
 def ok(status, what=''):
@@ -157,18 +194,39 @@ class _LazyDT(dict):
 TORCH_DT = _LazyDT()
 
 
+REFERENCE_BLOCK = 256        # the reference's default threads per block (reference launch.py:30)
+
+
+def resolve_block(block, lowered_block):
+    """The block a generated kernel runs with: its own (``lowered_block``) for
+    ``None`` or the reference default, else ``block`` if it is that one."""
+    if block in (None, REFERENCE_BLOCK):
+        return lowered_block
+    if block != lowered_block:
+        raise ValueError(f'kernel was lowered for {lowered_block} threads per block, not {block}')
+    return block
+
+
 class Kernel:
     """One generated kernel, loaded on the current device and launched
     cooperatively on torch's current stream (reference launch.py:29-73).
 
-    grid = blocks that fit per CU (occupancy at ``block`` threads and the
+    ``block``: the generated kernel fixes its own block (``lowered.block``,
+    eight waves of 64); the reference default 256 (eight 32-wide warps) and
+    ``None`` mean that block, any other value is an error.
+
+    grid = blocks that fit per CU (occupancy at the block and the
     kernel's LDS, at most the lowering's ``per_cu_max``) x CUs, optionally
     capped by ``blocks_per_sm`` and by the lowering's own grid limit. ``S`` (fp32 scratch), ``bar`` (barrier and
     reduction counters, zeroed once; the kernel leaves them zeroed) and ``TS``
     (timing sums) are allocated here.
+
+    A grid barrier that waits too long (only a launch whose blocks are not all
+    resident can get there) gives up and raises an error word in ``bar``;
+    ``check()`` reads it (one device synchronisation) and raises.
     """
 
-    def __init__(self, lowered, block=None, device=0, blocks_per_sm=None):
+    def __init__(self, lowered, block=REFERENCE_BLOCK, device=0, blocks_per_sm=None):
         torch = _torch()
         if not torch.cuda.is_available():
             raise RuntimeError('no GPU: the Vesta kernel needs a ROCm device')
@@ -178,14 +236,13 @@ class Kernel:
         self.info = device_info(device)
         if not self.info['cooperative']:
             raise RuntimeError('device does not support cooperative launch')
-        block = lowered.block if block is None else block
-        if block != lowered.block:
-            raise ValueError(f'kernel was lowered for {lowered.block} threads per block, not {block}')
+        block = resolve_block(block, lowered.block)
         self.code = compile_code(lowered.src)
         L = lib()
         mod, fn = ctypes.c_void_p(), ctypes.c_void_p()
         ok(L.vh_module_load(self.code, ctypes.byref(mod)), 'module load')
         self.mod = mod
+        track(self)
         ok(L.vh_module_get_function(mod, lowered.name.encode(), ctypes.byref(fn)), 'get function')
         self.fn = fn
         self.smem = lowered.shared_bytes
@@ -286,11 +343,24 @@ class Kernel:
         self.bind(residue)
         self.launch()
 
+    def check(self):
+        """Raise if a grid barrier of an earlier launch gave up waiting (reads
+        the error word: one device synchronisation). The barrier words are
+        cleared first, so the kernel can be launched again."""
+        from .lower import BAR_ERROR, ERR_BARRIER, ERR_RANGE
+        code = int(self.bar[BAR_ERROR].item()) if self.bar.numel() > BAR_ERROR else 0
+        if code:
+            self.bar.zero_()
+            why = {ERR_BARRIER: f'a grid barrier gave up waiting (are all {self.grid} blocks resident on the '
+                                f'device?)',
+                   ERR_RANGE: 'an activation beyond the fp16 range (65504) reached a matrix-core product'}
+            raise RuntimeError(f'{self.lowered.name}: {why.get(code, f"error word {code}")}; the launch\'s results '
+                               f'are invalid')
+
     def close(self):
         if getattr(self, 'mod', None) is not None and self.mod.value:
             try:
-                lib().vh_synchronize()          # no launch of this module may still be running
-                lib().vh_module_unload(self.mod)
+                unload(self.mod)
             finally:
                 self.mod = None
 

@@ -98,6 +98,8 @@ UNROLL = 8                    # rows (tile) / vectors (lane) whose loads are iss
 TILE_LANES = 8                # tile: lanes per row (8 x 16 bytes = one 128-byte line of a weight row)
 LINE_WORDS = 32               # one 128-byte line per counter
 BAR_WORDS = LINE_WORDS * 10   # grid barrier: 8 per-XCD arrival counters, exit counter, error word
+BAR_ERROR = LINE_WORDS * 9 + 1  # the error word (device VH_BAR_ERROR): nonzero once a launch failed
+ERR_BARRIER, ERR_RANGE = 1, 2   # ... a grid barrier gave up waiting / an activation beyond fp16 on the matrix cores
 
 FOLD_INIT = {'sum': '0.0f', 'max': '-INFINITY', 'min': 'INFINITY'}
 FOLD_OP = {'sum': 'op_sum', 'max': 'op_max', 'min': 'op_min'}

@@ -345,6 +345,7 @@ class MfmaMixin:
                      f'v_[4] = x1_.x; v_[5] = x1_.y; v_[6] = x1_.z; v_[7] = x1_.w;')
         o.append(f'{I}  vh_u32x4 h_, l_;')
         o.append(f'{I}  {"vh_split8s" if scaled else "vh_split8"}(v_, h_, l_);')
+        o.append(f'{I}  if (vh_beyond_half8(v_)) stc_u(bar + VH_BAR_ERROR, VH_ERR_RANGE);')
         o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {ah} + r_ * {SAB} + k8_ * 16) = h_;')
         o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {al} + r_ * {SAB} + k8_ * 16) = l_;')
         o.append(f'{I}}}')
@@ -507,6 +508,7 @@ class MfmaMixin:
         o.append(f'{I}  }}')
         o.append(f'{I}  vh_u32x4 h_, l_;')
         o.append(f'{I}  {"vh_split8s" if packed else "vh_split8"}(v_, h_, l_);')
+        o.append(f'{I}  if (vh_beyond_half8(v_)) stc_u(bar + VH_BAR_ERROR, VH_ERR_RANGE);')
         o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {ah} + r_ * {SAB} + k8_ * 16) = h_;')
         o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {al} + r_ * {SAB} + k8_ * 16) = l_;')
         o.append(f'{I}}}')

@@ -19,7 +19,7 @@ from __future__ import annotations
 import ctypes
 from pathlib import Path
 
-from .launch import compile_code, lib, ok
+from .launch import compile_code, lib, ok, track, unload
 
 PREFILL_SRC = Path(__file__).resolve().parent / 'hip' / 'prefill.hip'
 PRELUDE_SRC = Path(__file__).resolve().parent / 'hip' / 'prelude.h'
@@ -77,11 +77,15 @@ class Prefill:
         mod = ctypes.c_void_p()
         ok(L.vh_module_load(self.code, ctypes.byref(mod)), 'prefill module load')
         self.mod = mod
+        track(self)
         self.fn = {}
         for name in KERNELS:
             fn = ctypes.c_void_p()
             ok(L.vh_module_get_function(mod, name.encode(), ctypes.byref(fn)), name)
             self.fn[name] = fn
+        import torch
+        self.err = torch.zeros(1, dtype=torch.int32, device='cuda')   # raised by a product that met an
+                                                                     # activation beyond the fp16 range
         self._bufs = {}
         self._own = {}
         self._ws = None
@@ -90,11 +94,20 @@ class Prefill:
         self._plans = {}
         self._plan = []
 
+    def check(self):
+        """Raise if a product of an earlier launch met an activation beyond the
+        fp16 range its matrix-core path can carry (one synchronisation); the
+        word is cleared first."""
+        if int(self.err.item()):
+            self.err.zero_()
+            raise RuntimeError('layered engine: an activation beyond the fp16 range (65504) reached a matrix-core '
+                               'product; the results are invalid')
+
     def close(self):
         if getattr(self, 'mod', None) is not None and self.mod.value:
             try:
-                lib().vh_synchronize()
-                lib().vh_module_unload(self.mod)
+                self._graph = None          # a captured graph holds launches of this module
+                unload(self.mod)
             except Exception:
                 pass
             self.mod = None
@@ -141,7 +154,7 @@ class Prefill:
         ws = self._workspace(ks * M * N) if ks > 1 else None
         tail = [_p(m.keys), _p(m.vals), _i(P), _p(m.t), _i(layer), _i(m.L), _i(m.tmax)]
         self._launch('pf_gemm', tiles * ks, [_p(A), _i(lda), _p(Wt), _p(bias), _i(M), _i(N), _i(K), _i(mode),
-                                             _p(out), _i(ldo)] + tail + [_i(ks), _p(ws)])
+                                             _p(out), _i(ldo)] + tail + [_i(ks), _p(ws), _p(self.err)])
         if ks > 1:
             self._launch('pf_reduce', -(-M * N // BLOCK), [_p(ws), _i(ks), _p(bias), _i(M), _i(N), _i(mode),
                                                             _p(out), _i(ldo)] + tail)
@@ -190,9 +203,18 @@ class Prefill:
     def decode(self, n, tokens=None):
         """``n`` greedy decode steps, each one pass with P = 1 over the
         model's input ``x`` (the last pass's argmax): the layer-at-a-time
-        path for shapes the persistent kernel does not fit. ``tokens`` (int32
-        device tensor, at least n * B) receives each step's chosen tokens."""
+        path for shapes the persistent kernel does not fit. ``tokens`` (a
+        contiguous int32 device tensor of at least n * B ids, any shape, e.g.
+        [n, B]) receives each step's chosen tokens, step k at flat offsets
+        k * B .. k * B + B - 1."""
         m = self.m
+        flat = None
+        if tokens is not None:
+            if not (tokens.is_cuda and tokens.dtype == m.x.dtype and tokens.is_contiguous()):
+                raise TypeError('tokens must be a contiguous int32 device tensor')
+            if tokens.numel() < n * m.B:
+                raise ValueError(f'tokens holds {tokens.numel()} ids, {n * m.B} needed')
+            flat = tokens.view(-1)
         buf = self._buffers(m.B)
         plan = self._plan_for('decode', buf, m.B, 1, m.x)
         step = lambda: self._replay(plan)       # noqa: E731
@@ -202,8 +224,8 @@ class Prefill:
             step = self._graph[1].replay
         for k in range(n):
             step()
-            if tokens is not None:
-                tokens[k * m.B:(k + 1) * m.B].copy_(m.x)
+            if flat is not None:
+                flat[k * m.B:(k + 1) * m.B].copy_(m.x)
 
     def _capture(self, plan):
         """One decode pass recorded as a HIP graph: a step is then one graph
