@@ -36,6 +36,7 @@ extern "C" {
 #define VH_ERR_NULL_ARG 20001
 #define VH_ERR_NO_COOP 20002
 #define VH_ERR_BAD_OCCUPANCY 20003
+#define VH_ERR_SCRATCH_TOO_SMALL 20004
 
 /* Compile `src` (HIP C++) with hipRTC. `opts` are compiler options such as
  * "--offload-arch=gfx950" and "-O3". On success *code / *code_size hold the
@@ -80,6 +81,37 @@ int vh_launch_cooperative(void* fn, unsigned grid, unsigned block, unsigned dyn_
 /* One ordinary (non-cooperative) launch, same arguments. Only for kernels
  * that do not wait on other blocks. No counterpart in the reference. */
 int vh_launch(void* fn, unsigned grid, unsigned block, unsigned dyn_lds, void* stream, void** args);
+
+/* ---- Allocation-free launch. No counterpart in the reference: for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). The kernel's scratch `S`, barrier
+ * counters `bar` and timing sums `TS` (three consecutive kernel arguments)
+ * live in one static device array of VH_NOALLOC_SCRATCH_BYTES per device,
+ * held until the process ends; the caller still passes every residue. */
+#define VH_NOALLOC_SCRATCH_BYTES (8u << 20)
+#define VH_NOALLOC_MAX_ARGS 64
+
+/* Device address and size of the current device's static scratch. */
+int vh_noalloc_scratch(void** base, size_t* bytes);
+
+/* Where bar and TS start in the static scratch for buffers of these sizes (S
+ * at 0, each start 256-byte aligned); VH_ERR_SCRATCH_TOO_SMALL beyond it. */
+int vh_noalloc_layout(size_t s_bytes, size_t bar_bytes, size_t ts_bytes, size_t* bar_off, size_t* ts_off);
+
+/* Copy `bytes` of the static scratch from `offset` to device memory `dst`,
+ * ordered on `stream` (outputs a launch left in S, such as the logits). */
+int vh_noalloc_read(void* dst, size_t offset, size_t bytes, void* stream);
+
+/* vh_launch_cooperative with args[slot], args[slot + 1], args[slot + 2]
+ * replaced by the static scratch's S, bar and TS (s_bytes, bar_bytes,
+ * ts_bytes long; VH_ERR_SCRATCH_TOO_SMALL when they do not fit). Enqueues a
+ * fill kernel that zeroes bar and TS, then the launch, both on `stream`;
+ * allocates nothing. Every call on a device shares that device's array and
+ * finds the previous call's values in S: calls that overlap on one device
+ * race, so run them on one stream (or order them). */
+int vh_launch_cooperative_noalloc(void* fn, unsigned grid, unsigned block, unsigned dyn_lds, void* stream,
+                                  void* const* args, int nargs, int slot, size_t s_bytes, size_t bar_bytes,
+                                  size_t ts_bytes);
 
 /* Wait for all work on the current device. */
 int vh_synchronize(void);

@@ -55,6 +55,11 @@ def lib():
                 'vh_device_info': [ctypes.c_int, ip, ip, ip, cp, sz],
                 'vh_launch_cooperative': [vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, vp, ctypes.POINTER(vp)],
                 'vh_launch': [vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, vp, ctypes.POINTER(vp)],
+                'vh_noalloc_scratch': [ctypes.POINTER(vp), ctypes.POINTER(sz)],
+                'vh_noalloc_layout': [sz, sz, sz, ctypes.POINTER(sz), ctypes.POINTER(sz)],
+                'vh_noalloc_read': [vp, sz, sz, vp],
+                'vh_launch_cooperative_noalloc': [vp, ctypes.c_uint, ctypes.c_uint, ctypes.c_uint, vp,
+                                                  ctypes.POINTER(vp), ctypes.c_int, ctypes.c_int, sz, sz, sz],
                 'vh_synchronize': [],
             }
             for name, args in sig.items():
@@ -342,6 +347,37 @@ class Kernel:
     def __call__(self, residue):
         self.bind(residue)
         self.launch()
+
+    def launch_noalloc(self, steps=1, tokens=None, inputs=None):
+        """``launch`` through ``vh_launch_cooperative_noalloc``: S, bar and TS
+        are the library's static per-device scratch instead of this object's
+        buffers (nothing is allocated; outputs left in S are read with
+        ``read_noalloc``). Calls on one device share that scratch."""
+        if self.args is None:
+            raise RuntimeError('bind() the residues before launch_noalloc()')
+        if steps < 1:
+            raise ValueError('steps must be at least 1')
+        self._nsteps.value = int(steps)
+        self._tok.value = tokens.data_ptr() if tokens is not None else 0
+        self._tok_in.value = inputs.data_ptr() if inputs is not None else 0
+        stream = _torch().cuda.current_stream().cuda_stream
+        ok(lib().vh_launch_cooperative_noalloc(self.fn, self.grid, self.block, self.smem, ctypes.c_void_p(stream),
+                                               self.args, len(self.args), len(self.lowered.params),
+                                               self.S.numel() * 4, self.bar.numel() * 4, self.TS.numel() * 8),
+           'cooperative launch (static scratch)')
+
+    def read_noalloc(self, name, out):
+        """Copy value ``name`` (a scratch value, e.g. 'logit') from the static
+        scratch into the fp32 device tensor ``out`` (on the current stream)."""
+        off, _, shape = self.lowered.scratch[name]
+        n = 1
+        for d in shape:
+            n *= d
+        if not (out.is_cuda and out.dtype == TORCH_DT['f32'] and out.is_contiguous() and out.numel() == max(1, n)):
+            raise TypeError(f'out must be a contiguous fp32 device tensor of {max(1, n)} values')
+        stream = _torch().cuda.current_stream().cuda_stream
+        ok(lib().vh_noalloc_read(ctypes.c_void_p(out.data_ptr()), off * 4, out.numel() * 4, ctypes.c_void_p(stream)),
+           'static scratch read')
 
     def check(self):
         """Raise if a grid barrier of an earlier launch gave up waiting (reads
