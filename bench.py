@@ -276,6 +276,21 @@ def pmc_summary(fetch_csv, write_csv, bench_log, calib_mib):
         json.dump(table, fh, indent=1, sort_keys=True)
 
 
+def kernel_stats(db_path, top=12):
+    """Markdown table of the kernel dispatches a ``rocprofv3 --kernel-trace``
+    run recorded in its results database (rocpd SQLite): calls, mean and
+    total duration per kernel, longest total first."""
+    import sqlite3
+    con = sqlite3.connect(db_path)
+    rows = con.execute('select name, count(*), avg("end" - start), sum("end" - start) from kernels '
+                       'group by name order by sum("end" - start) desc').fetchall()
+    total = sum(r[3] for r in rows) or 1
+    print('| kernel | calls | mean us | total ms | share |\n|---|---|---|---|---|')
+    for name, n, mean, tot in rows[:top]:
+        short = name if len(name) < 60 else name[:57] + '...'
+        print(f'| {short} | {n} | {mean / 1e3:.3f} | {tot / 1e6:.3f} | {100 * tot / total:.1f}% |')
+
+
 def calibration_copy(mib):
     """One device-to-device copy of ``mib`` MiB (reads and writes exactly that
     many bytes): the reference point for HBM traffic counters."""
@@ -590,6 +605,9 @@ def main():
     ap.add_argument('--pmc-summary', nargs=3, metavar=('FETCH_CSV', 'WRITE_CSV', 'BENCH_LOG'),
                     help='summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of '
                          '"bench.py --calibrate-copy N" into profiles/traffic.json and exit')
+    ap.add_argument('--kernel-stats', metavar='DB',
+                    help='print per-kernel dispatch statistics of a rocprofv3 --kernel-trace results database '
+                         '(the *_results.db it writes) and exit')
     ap.add_argument('--calibrate-copy', type=int, default=0, metavar='MiB',
                     help='first run one plain device-to-device copy of this many MiB (a kernel of known '
                          'traffic, to scale rocprofv3 FETCH_SIZE / WRITE_SIZE counters)')
@@ -629,6 +647,9 @@ def main():
         return
     if args.pmc_summary:
         pmc_summary(*args.pmc_summary, calib_mib=args.calibrate_copy or 1024)
+        return
+    if args.kernel_stats:
+        kernel_stats(args.kernel_stats)
         return
     if args.gpus != 1:
         print(json.dumps({'error': 'this build runs on one GPU: the decode step is one persistent kernel on one '
