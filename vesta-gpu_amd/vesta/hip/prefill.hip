@@ -174,6 +174,24 @@ __device__ __forceinline__ void pf_chunk_store(const PfChunk& c, vh_half* ah, vh
   }
 }
 
+// One staged chunk (PF_BK deep) multiplied into wave `wave`'s row tile: the
+// hi and lo halves of A against the four column tiles of Wt.
+__device__ __forceinline__ void pf_chunk_mma(vh_half (*buf)[PF_TILE * PF_LDA], int wave, int r, int kq,
+                                             vh_f32x4* acc, vh_f32x4* acl) {
+#pragma unroll
+  for (int ks = 0; ks < PF_BK; ks += 32) {
+    const int k = ks + kq;
+    const vh_u32x4 ah = *(const vh_u32x4*)(buf[0] + (16 * wave + r) * PF_LDA + k);
+    const vh_u32x4 al = *(const vh_u32x4*)(buf[1] + (16 * wave + r) * PF_LDA + k);
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const vh_u32x4 b = *(const vh_u32x4*)(buf[2] + (16 * j + r) * PF_LDA + k);
+      acc[j] = vh_mfma(ah, b, acc[j]);
+      acl[j] = vh_mfma(al, b, acl[j]);
+    }
+  }
+}
+
 // `ksplit` > 1 splits K over blocks as well: block b makes part b / tiles of
 // the fold for tile b % tiles and stores its partial tile in ws[part][m][n];
 // pf_reduce then adds the parts in part order and applies the epilogue.
@@ -193,29 +211,28 @@ extern "C" __global__ __launch_bounds__(256) void pf_gemm(
   vh_f32x4 acc[4], acl[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = acl[j] = vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  PfChunk ch;
+  // Chunks go global -> registers -> LDS three deep: while chunk c is
+  // multiplied out of one LDS buffer, chunk c + 1 waits in registers for the
+  // other buffer and chunk c + 2 is in flight into a second register stage.
+  // (Unrolled by two so each register stage keeps its own name.)
+  PfChunk r0, r1;
   bool bad = false;
   if (c0 < c1) {
-    pf_chunk_load(ch, A, lda, Wt, M, N, K, m0, n0, c0 * PF_BK);
-    pf_chunk_store(ch, lds[0][0], lds[0][1], lds[0][2], bad);
+    pf_chunk_load(r0, A, lda, Wt, M, N, K, m0, n0, c0 * PF_BK);
+    pf_chunk_store(r0, lds[0][0], lds[0][1], lds[0][2], bad);
   }
+  if (c0 + 1 < c1) pf_chunk_load(r0, A, lda, Wt, M, N, K, m0, n0, (c0 + 1) * PF_BK);
+  if (c0 + 2 < c1) pf_chunk_load(r1, A, lda, Wt, M, N, K, m0, n0, (c0 + 2) * PF_BK);
   vh_lds_sync();
-  for (int c = c0; c < c1; ++c) {
-    const int cur = (c - c0) & 1;
-    if (c + 1 < c1) pf_chunk_load(ch, A, lda, Wt, M, N, K, m0, n0, (c + 1) * PF_BK);
-#pragma unroll
-    for (int ks = 0; ks < PF_BK; ks += 32) {
-      const int k = ks + kq;
-      const vh_u32x4 ah = *(const vh_u32x4*)(lds[cur][0] + (16 * wave + r) * PF_LDA + k);
-      const vh_u32x4 al = *(const vh_u32x4*)(lds[cur][1] + (16 * wave + r) * PF_LDA + k);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const vh_u32x4 b = *(const vh_u32x4*)(lds[cur][2] + (16 * j + r) * PF_LDA + k);
-        acc[j] = vh_mfma(ah, b, acc[j]);
-        acl[j] = vh_mfma(al, b, acl[j]);
-      }
-    }
-    if (c + 1 < c1) pf_chunk_store(ch, lds[cur ^ 1][0], lds[cur ^ 1][1], lds[cur ^ 1][2], bad);
+  for (int c = c0; c < c1; c += 2) {
+    pf_chunk_mma(lds[0], wave, r, kq, acc, acl);
+    if (c + 1 < c1) pf_chunk_store(r0, lds[1][0], lds[1][1], lds[1][2], bad);
+    if (c + 3 < c1) pf_chunk_load(r0, A, lda, Wt, M, N, K, m0, n0, (c + 3) * PF_BK);
+    vh_lds_sync();
+    if (c + 1 >= c1) break;
+    pf_chunk_mma(lds[1], wave, r, kq, acc, acl);
+    if (c + 2 < c1) pf_chunk_store(r1, lds[0][0], lds[0][1], lds[0][2], bad);
+    if (c + 4 < c1) pf_chunk_load(r1, A, lda, Wt, M, N, K, m0, n0, (c + 4) * PF_BK);
     vh_lds_sync();
   }
   if (bad) stc_u(err, VH_ERR_RANGE);
