@@ -233,19 +233,6 @@ def pmc_summary(fetch_csv, write_csv, bench_log, calib_mib):
     markdown table."""
     want = calib_mib * 1024.0
 
-    def load(path):
-        rows = list(csv.DictReader(open(path)))
-        copies = [float(r['Counter_Value']) for r in rows if 'copyBuffer' in r['Kernel_Name']
-                  or 'copy' in r['Kernel_Name'].lower()]
-        calib = max(copies)
-        per = {}
-        for r in rows:
-            if r['Kernel_Name'].startswith('vesta_step'):
-                per.setdefault(r['Kernel_Name'], []).append(float(r['Counter_Value']))
-        return calib, per
-    fc, fper = load(fetch_csv)
-    wc, wper = load(write_csv)
-    fscale, wscale = want / fc, want / wc
     line = None
     for ln in open(bench_log):
         if ln.startswith('{') and '"metric"' in ln:
@@ -253,6 +240,20 @@ def pmc_summary(fetch_csv, write_csv, bench_log, calib_mib):
     if line is None:
         raise SystemExit(f'no bench JSON line in {bench_log}')
     cfgs = {line['roofline']['kernel']: line['roofline'], line['b1']['kernel']: line['b1']}
+
+    def load(path):
+        rows = list(csv.DictReader(open(path)))
+        copies = [float(r['Counter_Value']) for r in rows if 'copyBuffer' in r['Kernel_Name']
+                  or 'copy' in r['Kernel_Name'].lower()]
+        calib = max(copies)
+        per = {}
+        for r in rows:
+            if r['Kernel_Name'] in cfgs:           # the timed kernels only (not the one-launch-per-step leg's)
+                per.setdefault(r['Kernel_Name'], []).append(float(r['Counter_Value']))
+        return calib, per
+    fc, fper = load(fetch_csv)
+    wc, wper = load(write_csv)
+    fscale, wscale = want / fc, want / wc
     table = {}
     if os.path.exists(TRAFFIC_FILE):
         table = json.load(open(TRAFFIC_FILE))
@@ -267,7 +268,9 @@ def pmc_summary(fetch_csv, write_csv, bench_log, calib_mib):
         alg = c['algorithmic_bytes_per_launch']
         table[k] = dict(src_sha=c['src_sha'], fetch_bytes=fb, write_bytes=wb, traffic=fb + wb,
                         algorithmic_bytes=alg, steps_per_launch=c['steps_per_launch'],
-                        fetch_scale=fscale, write_scale=wscale)
+                        fetch_scale=fscale, write_scale=wscale,
+                        run=f"steps {line.get('steps')}, warmup {line.get('warmup')}, positions "
+                            f"{line.get('config', {}).get('positions')}")
         print(f'| {k} | {f:.0f} | {w:.0f} | {fb / 1e6:.1f} MB | {wb / 1e6:.1f} MB | {alg / 1e6:.1f} MB | '
               f'{(fb + wb) / alg:.3f} |')
     print(f'\nscale factors (calibration copy of {calib_mib} MiB): FETCH_SIZE x{fscale:.3f}, WRITE_SIZE x{wscale:.3f}')

@@ -37,7 +37,8 @@ def test_pmc_summary_scales_counters_by_the_calibration_copy(tmp_path, monkeypat
     monkeypatch.setattr(bench, 'TRAFFIC_FILE', str(tmp_path / 'traffic.json'))
     fetch, write, log = tmp_path / 'f.csv', tmp_path / 'w.csv', tmp_path / 'bench.log'
     _counters(fetch, [('__amd_rocclr_copyBuffer', 524288.0), ('__amd_rocclr_copyBuffer', 3.0),
-                      ('vesta_step_b8', 1000.0), ('vesta_step_b8', 3000.0), ('vesta_step_b1', 500.0)])
+                      ('vesta_step_b8', 1000.0), ('vesta_step_b8', 3000.0), ('vesta_step_b1', 500.0),
+                      ('vesta_step1_b8', 99999.0)])           # the one-launch-per-step leg: not averaged in
     _counters(write, [('__amd_rocclr_copyBuffer', 1048576.0), ('vesta_step_b8', 10.0), ('vesta_step_b1', 4.0)])
     line = {'metric': 'm', 'roofline': {'kernel': 'vesta_step_b8', 'src_sha': 'aa', 'steps_per_launch': 32,
                                         'algorithmic_bytes_per_launch': 8192000.0},
