@@ -421,20 +421,40 @@ class StreamMixin:
         rpl = -(-(rows * PB) // lpp)
         J2 = I + '  '
         if qs is None:
+            # groups of PI slots, software-pipelined: the loads of the next group
+            # are in flight while the current one is multiplied and reduced (two
+            # named register buffers, the loop unrolled by two: a copy between
+            # buffers would wait for the loads it copies)
             PI = max(1, PI_STREAM // PB)
-            o.append(f'{I}for (int q0_ = 0; q0_ < {NQ}; q0_ += {PI}) {{')
-            o.append(f'{J2}{ltype} wl_[{PI}][{PB}][{pl}];')
-            for qi in range(PI):
-                o.append(f'{J2}if (q0_ + {qi} < {NQ}) {{')
-                o += [J2 + '  ' + x for x in load_lines(f'(q0_ + {qi})', f'wl_[{qi}]', None)]
-                o.append(f'{J2}}}')
-            o.append(f'{J2}#pragma unroll')
-            o.append(f'{J2}for (int qi_ = 0; qi_ < {PI}; ++qi_) {{')
-            K3 = J2 + '  '
-            o.append(f'{K3}const int q_ = q0_ + qi_;')
-            o.append(f'{K3}if (q_ >= {NQ}) break;')
-            self.slot_dot(o, K3, 'q_', 'wl_[qi_]', dt, vec, nv, lpp, pl, exact, rch, K, abase, geo)
-            self.slot_epilogue(s, c, st, fused, o, K3, 'q_', rc, rows, rpl, geo, None)
+
+            def issue(buf, q0):
+                lines = []
+                for qi in range(PI):
+                    lines.append(f'if ({q0} + {qi} < {NQ}) {{')
+                    lines += ['  ' + x for x in load_lines(f'({q0} + {qi})', f'{buf}[{qi}]', None)]
+                    lines.append('}')
+                return lines
+
+            def consume(buf, q0, ind2):
+                o.append(f'{ind2}#pragma unroll')
+                o.append(f'{ind2}for (int qi_ = 0; qi_ < {PI}; ++qi_) {{')
+                K3 = ind2 + '  '
+                o.append(f'{K3}const int q_ = {q0} + qi_;')
+                o.append(f'{K3}if (q_ >= {NQ}) break;')
+                self.slot_dot(o, K3, 'q_', f'{buf}[qi_]', dt, vec, nv, lpp, pl, exact, rch, K, abase, geo)
+                self.slot_epilogue(s, c, st, fused, o, K3, 'q_', rc, rows, rpl, geo, None)
+                o.append(f'{ind2}}}')
+            o.append(f'{I}{{')
+            o.append(f'{J2}{ltype} wl_[{PI}][{PB}][{pl}], wn_[{PI}][{PB}][{pl}];')
+            o += [J2 + x for x in issue('wl_', '0')]
+            o.append(f'{J2}for (int q0_ = 0; q0_ < {NQ}; q0_ += {2 * PI}) {{')
+            K2 = J2 + '  '
+            o += [K2 + x for x in issue('wn_', f'(q0_ + {PI})')]
+            consume('wl_', 'q0_', K2)
+            o += [K2 + x for x in issue('wl_', f'(q0_ + {2 * PI})')]
+            o.append(f'{K2}if (q0_ + {PI} < {NQ}) {{')
+            consume('wn_', f'(q0_ + {PI})', K2 + '  ')
+            o.append(f'{K2}}}')
             o.append(f'{J2}}}')
             o.append(f'{I}}}')
             return
