@@ -135,6 +135,36 @@ def test_tiny_and_medium_compile():
     assert launch.compile_code(med.src, cache=False)[:4] == b'\x7fELF'
 
 
+def test_fitted_kernels_take_the_deepest_mfma_pipeline_that_fits(monkeypatch):
+    """lower_fitted tries each prefetch budget with two k-blocks per register
+    set of an unprefetched matrix-core stream, then one, and keeps the first
+    try within SPILLS_OK; GPT-2 small B=8 keeps two at the full budget."""
+    tries = []
+
+    class Low:
+        def __init__(self, b, d):
+            self.src = (b, d)
+
+    def fake_lower(text, res, prefetch_vgprs, mfma_pipe, **kw):
+        tries.append((prefetch_vgprs, mfma_pipe))
+        return Low(prefetch_vgprs, mfma_pipe)
+    spills = {(64, 2): 30, (64, 1): 5}
+    with monkeypatch.context() as mp:
+        mp.setattr(launch, 'compile_code', lambda src: src)
+        mp.setattr(launch, 'code_spills', lambda code: spills.get(code, 99))
+        assert launch.lower_fitted(fake_lower, '', {}).src == (64, 1)
+        assert tries == [(64, 2), (64, 1)]
+        spills.clear()
+        tries.clear()
+        last = launch.lower_fitted(fake_lower, '', {}).src
+        assert tries == [(b, d) for b in launch.PREFETCH_BUDGETS for d in (2, 1)] and last == tries[-1]
+    small = launch.lower_fitted(lower, gpt2_program(12, 768, 12, 3072, 50257), gpt2_spec(8, 448),
+                                axis_max={'s': 448}, batch=8, per_token=('x', 'keys', 'vals'),
+                                outputs=('logit', 'next'), feedback={'x': 'next', 't': 1})
+    assert re.search(r'wb0_\[\d+\]\[2\]', small.src)
+    assert small.src == lower_gpt2(8, 448, prefetch_vgprs=launch.PREFETCH_BUDGETS[0], mfma_pipe=2).src
+
+
 def test_errors():
     with pytest.raises(NameError):
         lower('residue q[i]\naxis i = 2\ny[i] = q[i]\n', {}, {})

@@ -164,12 +164,15 @@ def code_spills(code: bytes) -> int:
 
 
 def lower_fitted(lower_fn, text, res, **kw):
-    """``lower_fn(text, res, **kw)`` with the largest prefetch register budget
-    whose kernel spills at most SPILLS_OK registers (compiling each try; the
-    code objects are cached, so the chosen one is not compiled again)."""
-    for budget in PREFETCH_BUDGETS:
-        low = lower_fn(text, res, prefetch_vgprs=budget, **kw)
-        if budget == PREFETCH_BUDGETS[-1] or code_spills(compile_code(low.src)) <= SPILLS_OK:
+    """``lower_fn(text, res, **kw)`` with the largest prefetch register budget,
+    and at it the deepest unprefetched MFMA pipeline (``MFMA_PIPES``), whose
+    kernel spills at most SPILLS_OK registers (compiling each try; the code
+    objects are cached, so the chosen one is not compiled again)."""
+    from .mfma import MFMA_PIPES
+    tries = [(b, d) for b in PREFETCH_BUDGETS for d in MFMA_PIPES]
+    for budget, pipe in tries:
+        low = lower_fn(text, res, prefetch_vgprs=budget, mfma_pipe=pipe, **kw)
+        if (budget, pipe) == tries[-1] or code_spills(compile_code(low.src)) <= SPILLS_OK:
             return low
 
 

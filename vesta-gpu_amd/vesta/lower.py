@@ -68,7 +68,7 @@ from .analysis import (BIG, PRIV_SIZE, PRIV_WORK, STAGE_MAX, Analysis, LowerErro
 from .attn import AttnMixin
 from .ir import defined_names, is_node, stmt_exprs, transform, walk
 from .stream import StreamMixin, PREFETCH_VGPRS
-from .mfma import MfmaMixin
+from .mfma import MFMA_PIPES, MfmaMixin
 
 PRELUDE_PATH = Path(__file__).resolve().parent / 'hip' / 'prelude.h'
 
@@ -203,7 +203,8 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
     nodes_of = staticmethod(nodes)
     rebuild_expr = staticmethod(rebuild)
 
-    def __init__(self, stmts, res, axis_max, outputs, batch, timing=False, grid=None, prefetch_vgprs=None):
+    def __init__(self, stmts, res, axis_max, outputs, batch, timing=False, grid=None, prefetch_vgprs=None,
+                 mfma_pipe=None):
         self.res = {n: (tuple(int(x) for x in shp), dt) for n, (shp, dt) in res.items()}
         self.axis_max = dict(axis_max or {})
         self.outputs = set(outputs)
@@ -231,6 +232,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
         self.grid_wide = GRID_WIDE
         self.proj_wider = False       # an attention projection would get its replicas on GRID_WIDE blocks
         self.pf_budget = int(prefetch_vgprs or PREFETCH_VGPRS)   # registers per lane a site may prefetch into
+        self.mfma_pipe = int(mfma_pipe or MFMA_PIPES[0])     # k-blocks per register set of an unprefetched MFMA stream
         self.packs = {}           # transposed copy -> the residue it is made from
         self.decls = []           # kernel-scope declarations (prefetch registers)
         self.pf_slots = []        # prefetch code per grid barrier
@@ -2574,7 +2576,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
 
 
 def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None, timing=False,
-          kernel_name='vesta_step', grid=None, prefetch_vgprs=None):
+          kernel_name='vesta_step', grid=None, prefetch_vgprs=None, mfma_pipe=None):
     """Program text -> Lowered: HIP source of one persistent kernel.
 
     Kernel ABI: ``<kernel_name>(R_<residue>... in spec order, float* S,
@@ -2591,18 +2593,19 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
     the first launch and is left consistent by every launch.
     """
     args = (text, res, axis_max, batch, per_token, outputs, feedback, timing, kernel_name)
-    out, low = _lower(*args, grid, prefetch_vgprs)
+    out, low = _lower(*args, grid, prefetch_vgprs, mfma_pipe)
     if low.grid_auto and low.grid != GRID_WIDE and (low.proj_wider or out.shared_bytes > LDS_BYTES):
         # the default grid is too small for replicated attention projections, or leaves streams so
         # many points per block that their staged rows overflow LDS; the full grid may not
-        out, low = _lower(*args, GRID_WIDE, prefetch_vgprs)
+        out, low = _lower(*args, GRID_WIDE, prefetch_vgprs, mfma_pipe)
     return out
 
 
-def _lower(text, res, axis_max, batch, per_token, outputs, feedback, timing, kernel_name, grid, prefetch_vgprs):
+def _lower(text, res, axis_max, batch, per_token, outputs, feedback, timing, kernel_name, grid, prefetch_vgprs,
+           mfma_pipe):
     """One lowering on one grid: (Lowered, the Lowering that made it)."""
     stmts = batch_lift(parse(text), batch, set(per_token))
-    low = Lowering(stmts, res, axis_max, outputs, batch, timing, grid, prefetch_vgprs)
+    low = Lowering(stmts, res, axis_max, outputs, batch, timing, grid, prefetch_vgprs, mfma_pipe)
     for o in outputs:
         if o not in low.axes_of:
             raise NameError(f'output {o} is not a value of the program')

@@ -24,14 +24,16 @@ fewer, KW waves share a tile, each over its own range of the fold, and the
 partial tiles are added through LDS in wave order (a fixed order, so results
 do not depend on timing). The weights of a wave's share are loaded at the
 barrier before the site when they fit in the prefetch register budget, else
-streamed through two register sets of MFMA_PIPE k-blocks each.
+streamed through two register sets of ``mfma_pipe`` k-blocks each.
 """
 from __future__ import annotations
 
 MFMA_ROWS_MIN = 4            # rows from which a stream runs on the matrix cores
-MFMA_PIPE = 1                # k-blocks of weights per register set when not prefetched (two sets: the
-                             # next set's loads are in flight while one is used; B=8 315 us per step at 3,
-                             # 312.5 at 2, 311.5 at 1, 326 at 4)
+MFMA_PIPES = (2, 1)          # k-blocks of weights per register set when not prefetched (two sets: the
+                             # next set's loads are in flight while one is used), tried in turn at each
+                             # prefetch budget; GPT-2 small B=8, same box, alternating order: 321 us per
+                             # step at 2, 324.6 at 1, equal tokens and logits; 3 spills 57 registers at
+                             # the full budget
 MFMA_POINTS_MIN = 8          # points a block must make (of a tile's 16 columns)
 
 
@@ -188,7 +190,7 @@ class MfmaMixin:
                 o.append(f'{J}if (mk0_ + {j} < mk1_)')
                 o += kstep(str(j), lambda i, j=j: f'{wm}[{i}][{j}]', J + '  ')
         else:
-            D = MFMA_PIPE
+            D = self.mfma_pipe
             o.append(f'{J}vh_u32x4 wb0_[{TPW}][{D}], wb1_[{TPW}][{D}];')
             for i in range(TPW):
                 for d in range(D):
