@@ -62,14 +62,18 @@ def _nodes(e):
 def test_gpt2_small_b1_plan():
     low = lower_gpt2(1)
     p = placements(low)
-    # three projections stream rows of a transposed weight copy, no split-K; the
+    # two projections stream rows of a transposed weight copy, no split-K; the
     # attention's blocks do the out-projection (12 of the 144 blocks per head) and add it
     # into z1, a fixed-point sum whose base z + ob is stored in the phase before
-    for name in ('qkv', 'u', 'z2'):
+    for name in ('qkv', 'u'):
         assert p[name].startswith('stream (transposed copy)'), (name, p[name])
     assert p['oo'] == 'attention[bt, h] projection x12'
     assert p['z1'].startswith('fixed-point sum')
-    assert low.packs == {'qkvw__t': 'qkvw', 'ow__t': 'ow', 'fcw__t': 'fcw', 'pw__t': 'pw'}
+    # the down-projection folds each block's own 22 widened values in the widening's
+    # phase, from pw's rows in their own layout, into z kept in 8 fixed-point copies
+    assert p['z2'] == 'local fold over the points of u (22 per block), fixed-point sum in 8 copies'
+    assert low.packs == {'qkvw__t': 'qkvw', 'ow__t': 'ow', 'fcw__t': 'fcw'}
+    assert 'stage_fxc<8>' in low.src and 'clear the copies of z' in low.src
     # attention: scores, softmax statistics and weighted values in one block per (bt, h)
     assert p['sc'] == p['mx'] == p['_h1'] == p['o'] == 'attention[bt, h]'
     assert p['logit'] == 'stream'
@@ -82,10 +86,10 @@ def test_gpt2_small_b1_plan():
     assert p['g'] == 'epilogue of u'
     # softmax denominator hoisted, q / ex / w inlined
     assert '_h1' in p and 'q' not in p and 'w' not in p and 'ex' not in p
-    assert low.barriers_per_launch == 4 * 12 + 1
+    assert low.barriers_per_launch == 3 * 12 + 1
     assert set(low.scratch) >= {'logit', 'next'} and low.scratch['logit'][2] == (1, 50257)
-    # fixed-point and elided values are not host-visible
-    assert not {'z1', 'oo', 'o'} & set(low.scratch)
+    # fixed-point, block-local and elided values are not host-visible
+    assert not {'z1', 'oo', 'o', 'g', 'z'} & set(low.scratch)
 
 
 def test_gpt2_small_b8_plan():
@@ -106,7 +110,8 @@ def test_params_and_abi():
     low = lower_gpt2(1)
     names = [n for n, _, _ in low.params]
     spec = list(gpt2_spec(1, 384))
-    assert names[:len(spec)] == spec and sorted(names[len(spec):]) == ['fcw__t', 'ow__t', 'pw__t', 'qkvw__t']
+    # transposed copies for the streams (the down-projection's local fold reads pw as it is)
+    assert names[:len(spec)] == spec and sorted(names[len(spec):]) == ['fcw__t', 'ow__t', 'qkvw__t']
     written = {n for n, _, w in low.params if w}
     assert written == {'x', 't', 'keys', 'vals'}
     sig = re.search(r'vesta_step\((.*?)\) \{', low.src).group(1)
@@ -252,7 +257,7 @@ def test_weight_cache_policy(monkeypatch):
         streamed = set(_re.findall(r'ldg16_nt\(mk_rsrc\((R_\w+)', src))
         assert not got & streamed, (B, got & streamed)
         return got
-    assert policy(1) == {'R_qkvw__t', 'R_ow__t', 'R_fcw__t', 'R_pw__t', 'R_wte'}
+    assert policy(1) == {'R_qkvw__t', 'R_ow__t', 'R_fcw__t', 'R_pw', 'R_wte'}
     assert policy(8) == {'R_pw__t', 'R_wte', 'R_ow__t'}
     assert policy(8, (24, 1024, 16, 4096, 50257)) == {'R_pw__t', 'R_wte', 'R_ow__t'}
     monkeypatch.setattr(stream, 'PROJ_KEPT_BYTES', 12 * 768 * 768 * 2 - 1)

@@ -366,6 +366,39 @@ __device__ __forceinline__ void stage_fx(float* dst, vh_rsrc S, unsigned off, in
   }
 }
 
+// A fixed-point sum kept in C copies, cs floats apart (adders spread over the
+// copies; the value is the exact integer sum of the copies): element i, and n
+// elements at float index off into LDS floats.
+template <int C>
+__device__ __forceinline__ float fxld_c(vh_rsrc r, unsigned i, unsigned cs) {
+  long long a = 0;
+#pragma unroll
+  for (int c = 0; c < C; ++c) a += ldfx_raw(r, i + (unsigned)c * cs);
+  return vh_fx2f(a);
+}
+template <int C>
+__device__ __forceinline__ void stage_fxc(float* dst, vh_rsrc S, unsigned off, int n, unsigned cs) {
+  const int nv = (n + 1) >> 1;
+  for (int base = threadIdx.x; base < nv; base += VBLOCK) {
+    vh_u32x4 v[C];
+#pragma unroll
+    for (int c = 0; c < C; ++c)
+      v[c] = __builtin_amdgcn_raw_buffer_load_b128(S, (off + (unsigned)c * cs + 4u * (unsigned)base) * 4u, 0, VH_SC1);
+    long long a = 0, b = 0;
+#pragma unroll
+    for (int c = 0; c < C; ++c) {
+      a += __builtin_bit_cast(long long, vh_u32x2{v[c].x, v[c].y});
+      b += __builtin_bit_cast(long long, vh_u32x2{v[c].z, v[c].w});
+    }
+    dst[2 * base] = vh_fx2f(a);
+    if (2 * base + 1 < n) dst[2 * base + 1] = vh_fx2f(b);
+  }
+}
+// 16 zero bytes at float index i of a buffer (agent-coherent store).
+__device__ __forceinline__ void stz4(vh_rsrc r, unsigned i) {
+  __builtin_amdgcn_raw_buffer_store_b128(vh_u32x4{0u, 0u, 0u, 0u}, r, i * 4u, 0, VH_SC1);
+}
+
 // Wait until every memory operation this wave issued has completed. The
 // signal fences keep the compiler from moving memory operations across it.
 __device__ __forceinline__ void drain() {

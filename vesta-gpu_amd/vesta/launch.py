@@ -111,16 +111,33 @@ def ok(status, what=''):
         raise RuntimeError(f'{what}: {msg} (status {status})' if what else f'{msg} (status {status})')
 
 
-def compile_code(src: str, arch: str = ARCH, opts=RTC_OPTS, cache: bool = True) -> bytes:
-    """HIP C++ -> gfx950 code object through hipRTC (replaces NVRTC, reference
-    launch.py:17-27). Failures raise RuntimeError carrying the compile log.
-    Code objects are cached on disk by a hash of source, arch and options."""
-    full = [f'--offload-arch={arch}', *opts]
-    key = hashlib.sha256((src + '\0' + '\0'.join(full)).encode()).hexdigest()[:32]
-    path = os.path.join(CACHE_DIR, key + '.co')
-    if cache and os.path.exists(path):
-        with open(path, 'rb') as fh:
-            return fh.read()
+ROCM_DIR = os.path.realpath(os.environ.get('ROCM_PATH', '/opt/rocm'))
+
+
+def rtc_version() -> str:
+    """The ROCm release whose hipRTC compiles the kernels (the image's own)."""
+    try:
+        with open(os.path.join(ROCM_DIR, '.info', 'version')) as fh:
+            return fh.read().strip()
+    except OSError:
+        return 'unknown'
+
+
+def _rtc_in_process() -> bool:
+    """Is the hipRTC this process has mapped the image's own? torch ships its
+    own hipRTC and compiler (an older ROCm, which allocates registers
+    differently); once torch is loaded first, the shim binds to that copy."""
+    L = lib()
+    del L
+    try:
+        with open('/proc/self/maps') as fh:
+            paths = {ln.split()[-1] for ln in fh if 'libhiprtc' in ln or 'libamd_comgr' in ln}
+    except OSError:
+        return 'torch' not in sys.modules
+    return all(os.path.realpath(p).startswith(ROCM_DIR + os.sep) for p in paths)
+
+
+def _compile_here(src: str, full) -> bytes:
     L = lib()
     arr = (ctypes.c_char_p * len(full))(*[o.encode() for o in full])
     code, size, log = ctypes.c_void_p(), ctypes.c_size_t(), ctypes.c_void_p()
@@ -133,6 +150,55 @@ def compile_code(src: str, arch: str = ARCH, opts=RTC_OPTS, cache: bool = True) 
         raise RuntimeError(f'hipRTC failed ({L.vh_error_string(st).decode()}):\n{text}')
     blob = ctypes.string_at(code.value, size.value)
     L.vh_free(code)
+    return blob
+
+
+def _compile_file(src_path: str, out_path: str, full) -> None:
+    """Child-process side of ``compile_code``: no torch loaded, so the shim's
+    hipRTC is the image's."""
+    with open(src_path) as fh:
+        src = fh.read()
+    try:
+        blob = _compile_here(src, list(full))
+    except RuntimeError as e:
+        sys.stderr.write(str(e))
+        sys.exit(3)
+    with open(out_path, 'wb') as fh:
+        fh.write(blob)
+
+
+def _compile_child(src: str, full) -> bytes:
+    import subprocess
+    import tempfile
+    pkg = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    with tempfile.TemporaryDirectory(prefix='vesta_rtc_') as d:
+        sp, op = os.path.join(d, 'k.hip'), os.path.join(d, 'k.co')
+        with open(sp, 'w') as fh:
+            fh.write(src)
+        code = (f'import sys; sys.path.insert(0, {pkg!r}); from vesta import launch; '
+                f'launch._compile_file({sp!r}, {op!r}, {list(full)!r})')
+        r = subprocess.run([sys.executable, '-c', code], capture_output=True, text=True)
+        if r.returncode == 3:
+            raise RuntimeError(r.stderr)
+        if r.returncode != 0 or not os.path.exists(op):
+            raise RuntimeError(f'the hipRTC compile process failed (status {r.returncode}):\n{r.stderr[-4000:]}')
+        with open(op, 'rb') as fh:
+            return fh.read()
+
+
+def compile_code(src: str, arch: str = ARCH, opts=RTC_OPTS, cache: bool = True) -> bytes:
+    """HIP C++ -> gfx950 code object through hipRTC (replaces NVRTC, reference
+    launch.py:17-27). Failures raise RuntimeError carrying the compile log.
+    Always the image's ROCm hipRTC: in a process where torch's copy is the one
+    mapped, the compile runs in a child process. Code objects are cached on
+    disk by a hash of source, arch, options and that ROCm release."""
+    full = [f'--offload-arch={arch}', *opts]
+    key = hashlib.sha256((src + '\0' + '\0'.join(full) + '\0rocm ' + rtc_version()).encode()).hexdigest()[:32]
+    path = os.path.join(CACHE_DIR, key + '.co')
+    if cache and os.path.exists(path):
+        with open(path, 'rb') as fh:
+            return fh.read()
+    blob = _compile_here(src, full) if _rtc_in_process() else _compile_child(src, full)
     if cache:
         os.makedirs(CACHE_DIR, exist_ok=True)
         tmp = f'{path}.{os.getpid()}.tmp'

@@ -66,6 +66,7 @@ from .interp import parse
 from .analysis import (BIG, PRIV_SIZE, PRIV_WORK, STAGE_MAX, Analysis, LowerError, batch_lift, replace_node,
                        top_folds)
 from .attn import AttnMixin
+from .chain import ChainError, ChainMixin
 from .ir import defined_names, is_node, stmt_exprs, transform, walk
 from .stream import StreamMixin, PREFETCH_VGPRS
 from .mfma import MFMA_PIPES, MfmaMixin
@@ -197,14 +198,14 @@ class Contraction:
 
 
 
-class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
+class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
     NWAVE, BLOCK, REG_MAX = NWAVE, BLOCK, REG_MAX
     show_stmt = staticmethod(show_stmt)
     nodes_of = staticmethod(nodes)
     rebuild_expr = staticmethod(rebuild)
 
     def __init__(self, stmts, res, axis_max, outputs, batch, timing=False, grid=None, prefetch_vgprs=None,
-                 mfma_pipe=None):
+                 mfma_pipe=None, local_folds=True):
         self.res = {n: (tuple(int(x) for x in shp), dt) for n, (shp, dt) in res.items()}
         self.axis_max = dict(axis_max or {})
         self.outputs = set(outputs)
@@ -268,6 +269,13 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
         self.find_peels(stmts)
         self.splits = {}              # id(stream statement) -> geometry of its fold split over blocks
         self.find_splits(stmts)
+        self.chains = {}              # id(statement) -> a local fold: its fold over the points its block made
+        self.chain_src = {}           # id(the stream making those points) -> the same
+        self.chain_local = set()      # values kept only in the LDS of the block that made them
+        self.chain_lds = {}           # such a value -> (LDS base, points/block, rows) of the site just made
+        self.fx_copies = {}           # fixed-point sum -> copies its adders spread over
+        if local_folds:
+            self.find_chains(stmts)
         self.layout(stmts)
 
     # ------------------------------------------------------------ rewrites
@@ -620,7 +628,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
             if r in self.private or r in self.g or n in self.inlined or r in self.elided_vals:
                 continue
             self.g[r] = self.goff
-            words = max(1, self.size(self.axes_of[r])) * (2 if r in self.fx else 1)
+            words = self.fx_words(r) if r in self.fx else max(1, self.size(self.axes_of[r]))
             self.goff += -(-words // LINE_WORDS) * LINE_WORDS
         self.counters = BAR_WORDS
         self.staged = {}
@@ -879,6 +887,10 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
             off, plen = self.glocal[r]
             return self.lds_read(f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}]')
         pv = self.peel_value(r, ix)
+        if r in self.fx_copies:
+            i = f'{self.g[r]} + 2u * ({a})'
+            v = f'fxld_c<{self.fx_copies[r]}>(rb_S, {i}, {self.fx_copy_stride(r)}u)'
+            return f'({pv[0]} == 0 ? {pv[1]} : {v})' if pv is not None else self.captured(v, 'float', r)
         if r in self.fx:
             i = f'{self.g[r]} + 2u * ({a})'
             if pv is not None:
@@ -896,6 +908,8 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
         if r in self.glocal:
             off, plen = self.glocal[r]
             return f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}] = {self.as_float(v, t)};'
+        if r in self.fx_copies:
+            raise LowerError(f'{r} is a fixed-point sum in copies: only atomic adds go into it')
         if r in self.fx:
             return f'fxst(rb_S, {self.g[r]} + 2u * ({a}), {self.as_float(v, t)});'
         return f'stcs(rb_S, {self.g[r]} + {a}, {self.as_float(v, t)});'
@@ -947,6 +961,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
         self.readers |= gl_reads
 
     def barrier(self, out, ind, what='', pre_wait=()):
+        out.append(f'{ind}/*@PZ{len(self.pf_slots)}@*/')   # code that must end before the arrival
         out.append(f'{ind}bk_ += 1u; grid_arrive(bar);' + (f'  // before {what}' if what else ''))
         self.mark(out, ind, f'arrive before {what}')
         if self.timing:
@@ -954,7 +969,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
             out.append(f'{ind}if (tid == 0 && st_ + 1 == nsteps && bk_ - bk0_ <= {BTRACE}u) '
                        f'TS[TSB_ + (bk_ - bk0_ - 1u) * 2u * nblk + blockIdx.x] = vh_clock();')
         out += [ind + x for x in pre_wait]
-        self.pf_open(out, ind, self.dirty)
+        self.pf_open(out, ind, self.dirty, self.readers)
         out.append(f'{ind}grid_wait(bar, nblk, bk_);')
         if self.timing:
             out.append(f'{ind}if (tid == 0 && st_ + 1 == nsteps && bk_ - bk0_ <= {BTRACE}u) '
@@ -1018,6 +1033,10 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
                     run.append(ss[i + len(run)])
                 self.gen_private(run, out, ind, self.base_after(ss, i + len(run)))
                 i += len(run)
+                continue
+            if id(s) in self.chains:
+                self.gen_chain(s, self.chains[id(s)], out, ind)
+                i += 1
                 continue
             if id(s) in self.splits:
                 self.gen_stream_split(s, self.splits[id(s)], out, ind)
@@ -1200,6 +1219,8 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
             row = self.addr([env[a][0] for a in reg], self.strides(reg)) if reg else '0'
             pt = self.addr([env[a][0] for a in pts], self.strides(pts))
             return f'sh_f[{base} + ({row}) * {PPB} + ({pt}) - (int)blockIdx.x * {PPB}] = {cur};'
+        if name in self.chain_local:
+            return None                 # the early-load pass over an epilogue: no store to make
         return self.store(name, [env[a][0] for a in axes], cur, 'float')
 
     def epilogue_emit(self, t_, inv, env, made, out, ind):
@@ -1662,6 +1683,9 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
             if id(t) in self.splits:
                 sk = self.splits[id(t)]
                 return None, self.root(t[1]), list(t[2]), sk['base'], sk
+            if id(t) in self.chains:
+                ch = self.chains[id(t)]
+                return None, ch['z'], list(t[2]), ch['base'], ch
             if t[0] == 'emit' or (t[0] == 'let' and self.place.get(id(t)) in ('tile', 'lane', 'epilogue')
                                   and id(t) not in self.groups):
                 continue
@@ -1701,6 +1725,10 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
                 if off - base + size <= STAGE_MAX:
                     staged[r] = off
                     fn = 'stage_fx' if r in self.fx else 'stage_ldc4'
+                    call = f'{fn}(sh_f + {off}, rb_S, {self.g[r]}, {size});'
+                    if r in self.fx_copies:
+                        call = (f'stage_fxc<{self.fx_copies[r]}>(sh_f + {off}, rb_S, {self.g[r]}, {size}, '
+                                f'{self.fx_copy_stride(r)}u);')
                     if r in self.peel_active:
                         lv, zs = self.peel_active[r]
                         out.append(f'{ind}if ({lv} == 0) {{  // {r} starts as {zs[1]}: made here')
@@ -1712,10 +1740,10 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
                         out.append(f'{ind}    sh_f[{off} + e_] = {val};')
                         out.append(f'{ind}  }}')
                         out.append(f'{ind}}} else {{')
-                        out.append(f'{ind}  {fn}(sh_f + {off}, rb_S, {self.g[r]}, {size});  // stage {r}')
+                        out.append(f'{ind}  {call}  // stage {r}')
                         out.append(f'{ind}}}')
                     else:
-                        out.append(f'{ind}{fn}(sh_f + {off}, rb_S, {self.g[r]}, {size});  // stage {r}')
+                        out.append(f'{ind}{call}  // stage {r}')
                     off += -(-size // 4) * 4
         self.stage_floats = max(self.stage_floats, off - base)
         self.priv_stage_end = off - base
@@ -1773,7 +1801,10 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin):
             shown, z, axes, bexpr, info = fx_base
             if (z not in self.readers and z not in self.dirty
                     and not (self.root_reads([bexpr]) & self.dirty)):
-                self.emit_base(shown, z, axes, bexpr, out, ind, sync=False)
+                if info.get('y') is not None and id(info['y']) in self.chains:
+                    self.chain_base(info, out, ind)
+                else:
+                    self.emit_base(shown, z, axes, bexpr, out, ind, sync=False)
                 info['base_done'] = True
         out.append(f'{ind}vh_lds_sync();')
         self.staged = {}
@@ -2603,9 +2634,21 @@ def lower(text, res, axis_max, batch=1, per_token=(), outputs=(), feedback=None,
 
 def _lower(text, res, axis_max, batch, per_token, outputs, feedback, timing, kernel_name, grid, prefetch_vgprs,
            mfma_pipe):
-    """One lowering on one grid: (Lowered, the Lowering that made it)."""
+    """One lowering on one grid: (Lowered, the Lowering that made it); again
+    without local folds when one cannot be kept."""
+    args = (text, res, axis_max, batch, per_token, outputs, feedback, timing, kernel_name, grid, prefetch_vgprs,
+            mfma_pipe)
+    try:
+        return _lower_once(*args, local_folds=True)
+    except ChainError:
+        return _lower_once(*args, local_folds=False)
+
+
+def _lower_once(text, res, axis_max, batch, per_token, outputs, feedback, timing, kernel_name, grid,
+                prefetch_vgprs, mfma_pipe, local_folds):
     stmts = batch_lift(parse(text), batch, set(per_token))
-    low = Lowering(stmts, res, axis_max, outputs, batch, timing, grid, prefetch_vgprs, mfma_pipe)
+    low = Lowering(stmts, dict(res), axis_max, outputs, batch, timing, grid, prefetch_vgprs, mfma_pipe,
+                   local_folds)
     for o in outputs:
         if o not in low.axes_of:
             raise NameError(f'output {o} is not a value of the program')
@@ -2620,6 +2663,11 @@ def _lower(text, res, axis_max, batch, per_token, outputs, feedback, timing, ker
         if t.startswith('/*@PF') and t.endswith('@*/'):
             slot = low.pf_slots[int(t[5:-3])]
             filled += [slot['ind'] + x for x in slot['lines']]
+        elif t.startswith('/*@PZ') and t.endswith('@*/'):
+            k = int(t[5:-3])
+            if k < len(low.pf_slots):
+                slot = low.pf_slots[k]
+                filled += [slot['ind'] + x for x in slot['pre']]
         else:
             filled.append(line)
     body = filled

@@ -96,12 +96,15 @@ class StreamMixin:
         return Stream(pack, pack or W, K, c0, rowlen, prefix, pts, vec)
 
     # ------------------------------------------------------------ prefetch slots
-    def pf_open(self, out, ind, dirty=()):
-        """A place for prefetch code between grid_arrive and grid_wait.
-        ``dirty``: values written since the previous barrier (other blocks'
-        writes of them are not yet visible there)."""
+    def pf_open(self, out, ind, dirty=(), readers=()):
+        """A place for prefetch code between grid_arrive and grid_wait (and
+        one before grid_arrive, ``pre``, for code that must end before the
+        block arrives). ``dirty`` / ``readers``: values written / read since
+        the previous barrier (other blocks' writes of them are not yet
+        visible there)."""
         k = len(self.pf_slots)
-        self.pf_slots.append({'lines': [], 'loop': self.loop_id(), 'ind': ind, 'dirty': set(dirty)})
+        self.pf_slots.append({'lines': [], 'pre': [], 'loop': self.loop_id(), 'ind': ind, 'dirty': set(dirty),
+                              'readers': set(readers)})
         out.append(f'/*@PF{k}@*/')
         self.last_pf = k
 
@@ -162,7 +165,13 @@ class StreamMixin:
         if self.mfma_ok(c, st):
             return self.gen_stream_mfma(s, c, st, fused, out, ind)
         name = s[1]
+        ch = self.chain_src.get(id(s))
+        if ch is not None and [(k, id(t)) for k, t, _ in fused] != [('let', id(ch['gs']))]:
+            from .chain import ChainError
+            raise ChainError(f'local fold {ch["y"][1]}: {ch["g"]} is not the epilogue of {name}')
         reads, writes = self.site_io(s, c, fused)
+        if ch is not None:
+            writes.discard(ch['g'])           # kept in the block's LDS only
         self.sync(reads, writes, out, ind, name)
         self.plan.append((self.show_stmt(s), 'stream' + (' (transposed copy)' if st.pack else '')
                           + (f' +{len(fused)} fused' if fused else '')))
@@ -307,10 +316,12 @@ class StreamMixin:
             qs = [str(q) for q in range(NQ)] if prefetch else None
             self.stream_body(s, c, st, fused, o, I, rc, rch, R, K, abase, dt, vec, nv, lpp, pl, exact,
                              NQ, qs, wq, ltype, geo, load_lines, sid, unsafe if prefetch else None)
-        if self.out_stage:
+        if any(n not in self.chain_local for n in self.out_stage):
             self.write_out(P, PPB, R, o, I)
             self.mark(o, I, f'stream {name}: write out')
         self.stream_lds = {self.root(n): (base, PPB, R) for n, (base, _, _, _) in self.out_stage.items()}
+        self.chain_lds = {n: (base, PPB, R) for n, (base, _, _, _) in self.out_stage.items()
+                          if n in self.chain_local}
         self.skip_store, self.out_stage = set(), {}
         o.append(f'{ind}}}')
         self.note(reads, writes)
@@ -325,6 +336,8 @@ class StreamMixin:
         o.append(f'{I}    const int r_ = e_ / {PPB}, i_ = e_ - r_ * {PPB};')
         o.append(f'{I}    if (p0_ + i_ < {P}) {{')
         for n, (base, _, _, _) in self.out_stage.items():
+            if n in self.chain_local:
+                continue
             o.append(f'{I}      stcs(rb_S, {self.g[self.root(n)]} + r_ * {P} + p0_ + i_, sh_f[{base} + e_]);')
         o.append(f'{I}    }}')
         o.append(f'{I}  }}')
@@ -343,6 +356,8 @@ class StreamMixin:
         (several rows per point, or the argmax that reads it next)?"""
         n = t[1]
         r = self.root(n)
+        if n in self.chain_local:
+            return list(t[2]) == list(reg) + list(pts)
         if r in self.private or r in self.fx or r not in self.g or list(self.axes_of[r]) != list(t[2]):
             return False
         if list(t[2]) != list(reg) + list(pts) or R * PPB > STAGE_OUT_MAX:
