@@ -167,13 +167,14 @@ class ChainMixin:
         atomic add: other blocks' partials may already be in)."""
         z, reg, d = ch['z'], ch['reg'], ch['d']
         axes = reg + [d]
+        early = self.early_spread_loads(axes, ch['base'], out, ind)
         I = ind + '  '
         out.append(f'{ind}{{ const unsigned cz_ = {self.fx_copy_base(z)};')
         out.append(f'{ind}for (int p_ = (int)blockIdx.x + (int)nblk * tid; p_ < {self.count_c(axes)}; '
                    f'p_ += nthr) {{  // {z} base')
         env = self.decode('p_', axes, out, I)
         pre = []
-        v, t = self.expr(ch['base'], env, pre, I)
+        v, t = self.spread_value(ch['base'], env, pre, I, early)
         out += pre
         out.append(f'{I}fxadd(S, {self.g[z]}u + cz_ + 2u * (unsigned)p_, {self.as_float(v, t)});')
         out.append(f'{ind}}} }}')
