@@ -143,7 +143,7 @@ def test_tiny_and_medium_compile():
 def test_fitted_kernels_take_the_deepest_mfma_pipeline_that_fits(monkeypatch):
     """lower_fitted tries each prefetch budget with two k-blocks per register
     set of an unprefetched matrix-core stream, then one, and keeps the first
-    try within SPILLS_OK; GPT-2 small B=8 keeps two at the full budget."""
+    try within SPILLS_OK."""
     tries = []
 
     class Low:
@@ -163,11 +163,18 @@ def test_fitted_kernels_take_the_deepest_mfma_pipeline_that_fits(monkeypatch):
         tries.clear()
         last = launch.lower_fitted(fake_lower, '', {}).src
         assert tries == [(b, d) for b in launch.PREFETCH_BUDGETS for d in (2, 1)] and last == tries[-1]
+    # GPT-2 small B=8: the first try within the limit, every earlier one beyond it
     small = launch.lower_fitted(lower, gpt2_program(12, 768, 12, 3072, 50257), gpt2_spec(8, 448),
                                 axis_max={'s': 448}, batch=8, per_token=('x', 'keys', 'vals'),
                                 outputs=('logit', 'next'), feedback={'x': 'next', 't': 1})
-    assert re.search(r'wb0_\[\d+\]\[2\]', small.src)
-    assert small.src == lower_gpt2(8, 448, prefetch_vgprs=launch.PREFETCH_BUDGETS[0], mfma_pipe=2).src
+    for b, d in [(b, d) for b in launch.PREFETCH_BUDGETS for d in (2, 1)]:
+        src = lower_gpt2(8, 448, prefetch_vgprs=b, mfma_pipe=d).src
+        if src == small.src:
+            assert launch.code_spills(launch.compile_code(src)) <= launch.SPILLS_OK
+            break
+        assert launch.code_spills(launch.compile_code(src)) > launch.SPILLS_OK, (b, d)
+    else:
+        raise AssertionError('the fitted kernel is none of the tries')
 
 
 def test_errors():

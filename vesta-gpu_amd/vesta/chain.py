@@ -151,8 +151,8 @@ class ChainMixin:
         That barrier must not be the first of its loop body, and neither the
         phase it closes nor this one may touch z before here."""
         k, loop = self.last_pf, self.loop_id()
-        if k is None:
-            raise ChainError(f'local fold into {z}: no barrier before its phase')
+        if k is None or self.pf_slots[k].get('ready'):
+            raise ChainError(f'local fold into {z}: no grid barrier right before its phase')
         slot = self.pf_slots[k]
         if slot['loop'] != loop or not any(self.pf_slots[j]['loop'] == loop for j in range(k)):
             raise ChainError(f'local fold into {z}: its phase is the first of a loop body')
@@ -165,8 +165,8 @@ class ChainMixin:
     def chain_base(self, ch, out, ind):
         """BASE into y's fixed-point sum, once per element over all blocks (an
         atomic add: other blocks' partials may already be in)."""
-        z, reg, d = ch['z'], ch['reg'], ch['d']
-        axes = reg + [d]
+        z = ch['z']
+        axes = list(ch['axes']) if 'axes' in ch else ch['reg'] + [ch['d']]
         early = self.early_spread_loads(axes, ch['base'], out, ind)
         I = ind + '  '
         out.append(f'{ind}{{ const unsigned cz_ = {self.fx_copy_base(z)};')

@@ -527,6 +527,55 @@ __device__ __forceinline__ void grid_exit(unsigned* bar, unsigned nblk) {
   }
 }
 
+// Readiness flags, for a set of producer blocks feeding a set of consumer
+// blocks without a grid barrier: block b publishes in flag line b (one
+// 128-byte line each, from `flags`) how many producer points of this launch it
+// has passed, once everything it stored before is complete; a consumer waits
+// only for the producers it reads from. Flags only grow during a launch;
+// grid_exit_flags() lets the last block out zero them.
+__device__ __forceinline__ void flag_publish(unsigned* flags, unsigned k) {
+  drain();
+  vh_lds_sync();
+  if (threadIdx.x == 0) stc_u(flags + VH_BAR_LINE * blockIdx.x, k);
+}
+// Until blocks p0 .. p0 + np - 1 (np <= 64) have published k: lane g of the
+// polling wave watches producer p0 + g, with grid_wait's spin limit and
+// error-word checks.
+__device__ __forceinline__ void flag_wait(unsigned* bar, const unsigned* flags, int p0, int np, unsigned k) {
+  if ((int)(threadIdx.x >> 6) == VH_POLL_WAVE) {
+    const int g = (int)(threadIdx.x & 63u);
+    bool done = g >= np;
+    const unsigned* cp = flags + VH_BAR_LINE * (done ? 0 : p0 + g);
+    unsigned n = 0;
+    while (true) {
+      if (!done) done = ldc_u(cp) >= k;
+      if (__all(done)) break;
+      __builtin_amdgcn_s_sleep(1);
+      if (++n > VH_SPIN_LIMIT) {
+        if (g == 0) stc_u(bar + VH_BAR_ERROR, 1u);
+        break;
+      }
+      if ((n % VH_ERR_POLLS) == 0u && __builtin_amdgcn_readfirstlane(ldc_u(bar + VH_BAR_ERROR)) != 0u) break;
+    }
+  }
+  vh_lds_sync();
+}
+// grid_exit() for a kernel with readiness flags: a block's flag stores are
+// complete before it counts itself out, and the last block out zeroes the
+// nblk flag lines too.
+__device__ __forceinline__ void grid_exit_flags(unsigned* bar, unsigned nblk, unsigned* flags) {
+  drain();
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    unsigned* ex = bar + VH_BAR_LINE * VH_BAR_GROUPS;
+    if (__hip_atomic_fetch_add(ex, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == nblk - 1u) {
+      for (unsigned g = 0; g < VH_BAR_GROUPS; ++g) stc_u(bar + VH_BAR_LINE * g, 0u);
+      for (unsigned b = 0; b < nblk; ++b) stc_u(flags + VH_BAR_LINE * b, 0u);
+      stc_u(ex, 0u);
+    }
+  }
+}
+
 // Split reductions: after storing its partial (coherent stores), a block
 // arrives on counter *cnt; the block that brings it to `total` is the last
 // and gets true; it then reads the other partials with coherent loads. The

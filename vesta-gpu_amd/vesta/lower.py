@@ -268,12 +268,14 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
         self.peel_active = {}         # carry root -> (loop variable, that statement) inside the loop
         self.find_peels(stmts)
         self.splits = {}              # id(stream statement) -> geometry of its fold split over blocks
+        self.local_folds = local_folds
         self.find_splits(stmts)
         self.chains = {}              # id(statement) -> a local fold: its fold over the points its block made
         self.chain_src = {}           # id(the stream making those points) -> the same
         self.chain_local = set()      # values kept only in the LDS of the block that made them
         self.chain_lds = {}           # such a value -> (LDS base, points/block, rows) of the site just made
         self.fx_copies = {}           # fixed-point sum -> copies its adders spread over
+        self.flags_off = None         # readiness flag lines in bar (one per block), when a split uses them
         if local_folds:
             self.find_chains(stmts)
         self.layout(stmts)
@@ -1861,7 +1863,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
             shown, z, axes, bexpr, info = fx_base
             if (z not in self.readers and z not in self.dirty
                     and not (self.root_reads([bexpr]) & self.dirty)):
-                if info.get('y') is not None and id(info['y']) in self.chains:
+                if (info.get('y') is not None and id(info['y']) in self.chains) or info.get('p2p'):
                     self.chain_base(info, out, ind)
                 else:
                     self.emit_base(shown, z, axes, bexpr, out, ind, sync=False)
@@ -2789,6 +2791,7 @@ def _lower_once(text, res, axis_max, batch, per_token, outputs, feedback, timing
            + f'  const int nthr = {low.grid} * {BLOCK};\n'
            + f'  const unsigned nblk = {low.grid}u;  // the launch grid (checked at launch)\n'
            + '  unsigned bk_ = 0u;  // grid barriers passed in this launch\n'
+           + '  unsigned pk_ = 0u;  // readiness flags published in this launch\n'
            + ''.join(f'  {d}\n' for d in low.decls)
            + (f'  __shared__ unsigned long long ts_sh[{max(1, len(low.sites))}];\n'
               f'  for (int i_ = tid; i_ < {max(1, len(low.sites))}; i_ += {BLOCK}) ts_sh[i_] = 0ull;\n'
@@ -2810,7 +2813,8 @@ def _lower_once(text, res, axis_max, batch, per_token, outputs, feedback, timing
            + ('  __syncthreads();\n'
               f'  for (int i_ = tid; i_ < {len(low.sites)}; i_ += {BLOCK}) TS[i_ * nblk + blockIdx.x] += ts_sh[i_];\n'
               if timing is True else '')
-           + '  grid_exit(bar, nblk);\n}\n')
+           + ('  grid_exit(bar, nblk);\n}\n' if low.flags_off is None
+              else f'  grid_exit_flags(bar, nblk, bar + {low.flags_off}u);\n}}\n'))
     scratch = {}
     for n in low.axes_of:
         r = low.root(n)

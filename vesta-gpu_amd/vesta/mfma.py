@@ -28,6 +28,8 @@ streamed through two register sets of ``mfma_pipe`` k-blocks each.
 """
 from __future__ import annotations
 
+from .analysis import top_folds
+
 MFMA_ROWS_MIN = 4            # rows from which a stream runs on the matrix cores
 MFMA_PIPES = (2, 1)          # k-blocks of weights per register set when not prefetched (two sets: the
                              # next set's loads are in flight while one is used), tried in turn at each
@@ -400,10 +402,11 @@ class MfmaMixin:
             return None
         _, NTS, NPG, KS, KSL = best
         base = self.rebuild_expr(c.epi, lambda n: ('num', 0.0) if n == ('name', '__acc') else n)
-        return dict(c=c, st=st, NTS=NTS, NPG=NPG, KS=KS, KSL=KSL, PG=16 * NTS, base=base)
+        return dict(c=c, st=st, NTS=NTS, NPG=NPG, KS=KS, KSL=KSL, PG=16 * NTS, base=base,
+                    z=self.root(name), axes=list(s[2]))
 
     def find_splits(self, ss):
-        for s in ss:
+        for i, s in enumerate(ss):
             if s[0] == 'step':
                 self.find_splits(s[6])
                 continue
@@ -411,6 +414,62 @@ class MfmaMixin:
             if sk is not None:
                 self.splits[id(s)] = sk
                 self.fx.add(self.root(s[1]))
+                if self.local_folds:
+                    sk['p2p'] = self.split_producer(ss, i, s, sk)
+
+    def split_producer(self, ss, i, s, sk):
+        """A split whose other factor is the epilogue value g of the stream
+        just before it (u; g = EPI(u) at u's points; the split reads g at its
+        own points and nothing else reads g): the blocks of a fold slice then
+        wait for the blocks that made that slice of g (readiness flags)
+        instead of a grid barrier. Returns u's points per block, or None."""
+        if i < 2:
+            return None
+        u, t, c = ss[i - 2], ss[i - 1], sk['c']
+        if u[0] != 'let' or t[0] != 'let' or self.place.get(id(u)) not in ('tile', 'lane'):
+            return None
+        if id(u) in self.splits or id(u) in self.groups or id(u) in self.elided:
+            return None
+        cu = self.info.get(id(u))
+        if getattr(cu, 'kind', None) not in ('tile', 'lane'):
+            return None
+        stu = self.stream_of(cu)
+        if stu is None or len(stu.pts) != 1 or list(stu.pts) != list(c.fold_axes):
+            return None
+        g = t[1]
+        if list(t[2]) != list(u[2]) or top_folds(t[3]) or self.root(g) != g or g in self.private:
+            return None
+        if g in self.outputs or self.readers_of.get(g, set()) != {id(s)}:
+            return None
+        if c.A[0] != 'idx' or c.A[1] != g or list(c.A[2]) != [('name', a) for a in t[2]]:
+            return None
+        P = self.size(stu.pts)
+        PPB = -(-P // self.grid)
+        NKB, KS = sk['st'].K // 32, sk['KS']
+        most = max(((q + 1) * NKB // KS * 32 - 1) // PPB - (q * NKB // KS * 32) // PPB + 1 for q in range(KS))
+        if most > 64:
+            return None
+        return dict(g=g, PPB=PPB)
+
+    def ready_point(self, pp, sk, out, ind, name):
+        """Every block publishes that its part of g is stored; a block of
+        fold slice q then waits for the blocks that made g's points of that
+        slice (u's block b made points [b * PPB, (b + 1) * PPB)). Between the
+        two, the split's weights are issued (a prefetch slot, as between a
+        grid barrier's arrival and wait)."""
+        if self.flags_off is None:
+            self.flags_off = self.alloc_counters(self.grid)
+        F, PPB = self.flags_off, pp['PPB']
+        NKB, KS, NPG = sk['st'].K // 32, sk['KS'], sk['NPG']
+        out.append(f'{ind}pk_ += 1u; flag_publish(bar + {F}u, pk_);  // {pp["g"]} stored: {name} waits for its makers')
+        self.mark(out, ind, f'publish before {name}')
+        self.pf_open(out, ind, self.dirty, self.readers)
+        self.pf_slots[-1]['ready'] = True
+        out.append(f'{ind}{{ const int q_ = (int)blockIdx.x % {KS};')
+        out.append(f'{ind}  const int p0_ = (q_ * {NKB} / {KS}) * 32 / {PPB}, '
+                   f'p1_ = min((((q_ + 1) * {NKB} / {KS}) * 32 - 1) / {PPB}, (int)nblk - 1);')
+        out.append(f'{ind}  flag_wait(bar, bar + {F}u, p0_, (int)blockIdx.x < {NPG * KS} ? p1_ - p0_ + 1 : 0, pk_); }}')
+        self.mark(out, ind, f'wait before {name}')
 
     def gen_stream_split(self, s, sk, out, ind):
         c, st = sk['c'], sk['st']
@@ -426,12 +485,25 @@ class MfmaMixin:
         KBW = -(-KSL // KW)
         # the base, everywhere, in the phase before
         self.plan.append((self.show_stmt(s), f'stream (transposed copy) mfma, fold in {KS} slices, '
-                          'fixed-point sum: base in the phase before'))
-        if not sk.get('base_done'):
-            self.emit_base(None, z, list(s[2]), sk['base'], out, ind, sync=True)
+                          + ('fixed-point sum cleared in the phase before, each slice waiting for the blocks '
+                             'that made it' if sk.get('p2p') else 'fixed-point sum: base in the phase before')))
+        pp = sk.get('p2p')
         I = ind + '  '
         reads = self.root_reads([c.A]) | {n for n in self.root_reads([s[3]]) if n != z}
-        self.sync(reads, {z}, out, ind, name)
+        if pp is not None:
+            # no grid barrier: z was cleared in the phase before, its base goes
+            # in by atomic adds, and each block waits for the makers of its slice
+            from .chain import ChainError
+            if ((reads - {pp['g']}) & self.dirty) or z in self.readers:
+                raise ChainError(f'split {name}: its phase would need a barrier after all')
+            self.chain_clear(z)
+            if not sk.get('base_done'):
+                self.chain_base(sk, out, ind)
+            self.ready_point(pp, sk, out, ind, name)
+        else:
+            if not sk.get('base_done'):
+                self.emit_base(None, z, list(s[2]), sk['base'], out, ind, sync=True)
+            self.sync(reads, {z}, out, ind, name)
         sid = self.fresh('k')
         rr, rs = self.rsrc(st.src), self.res_strides(st.src)
         role = [f'const int sg_ = (int)blockIdx.x / {KS}, ss_ = (int)blockIdx.x % {KS};',
