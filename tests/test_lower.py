@@ -86,10 +86,28 @@ def test_gpt2_small_b1_plan():
     assert p['g'] == 'epilogue of u'
     # softmax denominator hoisted, q / ex / w inlined
     assert '_h1' in p and 'q' not in p and 'w' not in p and 'ex' not in p
+    # three grid barriers per layer: the down-projection folds in the widening's phase
     assert low.barriers_per_launch == 3 * 12 + 1
     assert set(low.scratch) >= {'logit', 'next'} and low.scratch['logit'][2] == (1, 50257)
     # fixed-point, block-local and elided values are not host-visible
     assert not {'z1', 'oo', 'o', 'g', 'z'} & set(low.scratch)
+
+
+def test_attention_readiness_flags_lower_to_two_barriers_per_layer(monkeypatch):
+    """With READY_ATTN the attention waits for the blocks that made its query,
+    key and value rows instead of a grid barrier: two grid barriers per layer
+    at B=1 and B=8; the projection's sum and the layer carry alternate
+    between two buffers (cleared once a launch, then a layer ahead). Off by
+    default (slower on the MI355X); it must still lower and compile."""
+    from vesta import attn
+    monkeypatch.setattr(attn, 'READY_ATTN', True)
+    for B in (1, 8):
+        low = lower_gpt2(B, 448)
+        assert low.barriers_per_launch == 2 * 12 + 1, B
+        assert low.src.count('flag_publish(bar') == (1 if B == 1 else 2)
+        assert 'both layer buffers of z1, cleared once a launch' in low.src
+        assert "clear the next layer's z1" in low.src and 'clear the buffer of z read before' in low.src
+        assert launch.code_spills(launch.compile_code(low.src)) <= 16
 
 
 def test_gpt2_small_b8_plan():

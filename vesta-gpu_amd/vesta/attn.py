@@ -32,6 +32,10 @@ ATTN_PREFETCH_SLOTS = 8      # cache rows per lane issued early (K and V each)
 ATTN_CHUNK = 4               # longer contexts: slots per chunk of the running (online) softmax
 PROJ_MIN_REPLICAS = 2        # fuse the out-projection only if every leading point gets this many blocks
 PROJ_EARLY_SLOTS = 8         # projection weights issued at the barrier when a lane needs at most this many loads
+READY_ATTN = False           # attention waits for the blocks that made its rows (readiness flags) instead of
+                             # a grid barrier, its projection's sum in two layer buffers: two grid barriers
+                             # per GPT-2 layer, but slower (same box: B=8 306-312 us per step against 299,
+                             # B=1 212-218 against 205-208, equal tokens and logits), so off
                              # (B=8: 7 loads; early, with the prefetch budget cut to fit, 316 -> 307 us per step)
 
 
@@ -214,11 +218,163 @@ class AttnMixin:
 
     def gen_proj_base(self, pj, out, ind):
         """z1 = BASE at every point, spread over all blocks (a few threads
-        each), unless a private run before did it."""
+        each), unless a private run before did it (by atomic adds when the
+        group waits on readiness flags: other blocks' projections may be in
+        already)."""
         sz = pj['sz']
         if pj.get('base_done'):
             return
+        if pj.get('ready') is not None:
+            self.chain_base(pj, out, ind)
+            return
         self.emit_base(sz, sz[1], list(sz[2]), pj['base'], out, ind, sync=True)
+
+    # ------------------------------------------------------------ readiness flags
+    def find_ready_attn(self, ss, step=None):
+        """Attention groups with a projection whose dirty inputs all come from
+        the stream right before them (its values, and cache rows its fused
+        emits store): the group's blocks then wait for the blocks that made
+        their rows instead of a grid barrier (``attn_ready``). The projection's
+        fixed-point sum is then kept in two buffers by layer parity: a layer's
+        adds go into one while the other, read by the layer before, is
+        cleared for the next."""
+        if not READY_ATTN:
+            return
+        for i, s in enumerate(ss):
+            if s[0] == 'step':
+                self.find_ready_attn(s[6], s)
+                continue
+            pj = self.proj.get(id(s))
+            if pj is None or step is None:
+                continue
+            lead, members = self.groups[id(s)]
+            rd = self.attn_ready(ss, i, self.attn_of(lead, members), pj)
+            if rd is None:
+                continue
+            z1 = self.root(pj['sz'][1])
+            if z1 in self.fx_copies or z1 in self.fx_parity:
+                continue
+            pj.update(ready=rd, p2p=True, z=z1, axes=list(pj['sz'][2]))
+            var = step[3]
+            self.fx_parity[z1] = (f'l_{var}', var, self.static[var], 'layer')
+            # the loop's carry, added into by a local fold or a split in the same
+            # body, can no longer be cleared in the phase before theirs (it is read
+            # there now): it alternates between two buffers as well
+            ids = {id(t) for t in step[6]}
+            for sid_, sk in list(self.chains.items()) + list(self.splits.items()):
+                if sid_ in ids and (sk is not None and (sid_ in self.chains or sk.get('p2p'))):
+                    self.fx_parity[sk['z']] = (f'l_{var}', var, self.static[var], 'carry')
+
+    def attn_ready(self, ss, i, at, pj):
+        """The producers of group ``at`` (statement ss[i]): the stream u before
+        it and the emits fused into u between them. Returns (u, points per
+        block of u, [(const, {axis: coef}), ..]: u's point index of each read
+        the group makes of u's values or of the rows the emits store, affine in
+        the group's leading axes and free axes), or None."""
+        j, emits = i - 1, {}
+        while j >= 0 and ss[j][0] == 'emit':
+            emits[ss[j][1]] = ss[j]
+            j -= 1
+        if j < 0 or ss[j][0] != 'let':
+            return None
+        u = ss[j]
+        if self.place.get(id(u)) not in ('tile', 'lane') or id(u) in self.splits or id(u) in self.groups:
+            return None
+        cu = self.info.get(id(u))
+        st = self.stream_of(cu) if getattr(cu, 'kind', None) in ('tile', 'lane') else None
+        if st is None or len(st.pts) != 1:
+            return None
+        U, reg = self.root(u[1]), list(cu.reg_axes)
+        if list(u[2]) != reg + list(st.pts) or any(a not in at['lead'] for a in reg):
+            return None
+        deps = []
+
+        def u_index(n):
+            if list(n[2][:len(reg)]) != [('name', a) for a in reg]:
+                return None
+            return self.affine(n[2][-1])
+        for t in at['t']:
+            for n in self.nodes_of(t[3]):
+                if n[0] != 'idx':
+                    continue
+                if n[1] in self.axes_of and self.root(n[1]) == U:
+                    aff = u_index(n)
+                elif n[1] in emits:
+                    e = emits[n[1]]
+                    # the emit's row index must name the group's leading axes where the read does
+                    if len(e[2]) != len(n[2]) or any(x[0] == 'name' and x[1] in at['lead'] and y != x
+                                                     for x, y in zip(n[2], e[2])):
+                        return None
+                    vals = [m for m in self.nodes_of(e[3]) if m[0] == 'idx' and m[1] in self.axes_of
+                            and self.root(m[1]) == U]
+                    aff = u_index(vals[0]) if len(vals) == 1 else None
+                else:
+                    continue
+                if aff is None or any(a not in self.static for a in aff[1]):
+                    return None
+                if aff not in deps:
+                    deps.append(aff)
+        if not deps:
+            return None
+        P = self.size(st.pts)
+        PPB = -(-P // self.grid)
+        lead = at['lead']
+        # at most 64 producers per consumer, over every leading point
+        ext = [self.static[a] for a in lead]
+        for flat in range(math.prod(ext)):
+            vals, r = {}, flat
+            for a, n in zip(reversed(lead), reversed(ext)):
+                vals[a] = r % n
+                r //= n
+            total = 0
+            for const, coefs in deps:
+                lo, hi = self.dep_range(const, coefs, vals)
+                total += hi // PPB - lo // PPB + 1
+            if total > 64:
+                return None
+        return dict(u=u, U=U, PPB=PPB, deps=deps, emits=set(emits))
+
+    def attn_ready_point(self, at, pj, rd, reads, writes, out, ind):
+        """In place of the grid barrier before the group: the next layer's
+        buffer of the projection's sum is cleared, then every block publishes
+        and the group's blocks wait for the makers of their rows."""
+        from .chain import ChainError
+        t1, lead = at['t'][0], at['lead']
+        z1 = pj['z']
+        if (reads - {rd['U']} - rd['emits']) & self.dirty or (writes - {z1}) & (self.readers | self.dirty) \
+                or z1 in self.readers:
+            raise ChainError(f'attention {t1[1]}: its phase would need a barrier after all')
+        n4 = self.fx_words(z1) // 4
+        out.append(f'{ind}for (int e_ = (int)blockIdx.x + (int)nblk * tid; e_ < {n4}; e_ += nthr) '
+                   f'stz4(rb_S, {self.gofs(z1, ahead=1)} + 4u * (unsigned)e_);  // clear the next layer\'s {z1}')
+        G = self.size(lead)
+        setup = []
+        env = self.decode(f'((int)blockIdx.x % {G})', lead, setup, '', prefix='rl_')
+        vals = {a: env[a][0] for a in lead}
+        PPB = rd['PPB']
+        ranges = []
+        for const, coefs in rd['deps']:
+            lo, hi = self.dep_range(const, coefs, vals)
+            ranges.append((f'({lo}) / {PPB}', f'({hi}) / {PPB}'))
+        self.ready_point(t1[1], ranges, f'(int)blockIdx.x < {G * pj["R"]}', out, ind, rd['u'][1], setup)
+
+    def dep_range(self, const, coefs, lead_vals):
+        """(lowest, highest) point of an affine index with the leading axes
+        given (all numbers, or all C expressions) and every other axis over
+        its extent."""
+        num = all(isinstance(v, int) for v in lead_vals.values())
+        lo, hi = [const], [const]
+        for a, k in coefs.items():
+            if a in lead_vals:
+                term = k * lead_vals[a] if num else f'{k} * ({lead_vals[a]})'
+                lo.append(term)
+                hi.append(term)
+            else:
+                span = k * (self.static[a] - 1)
+                (lo if span < 0 else hi).append(span)
+        if num:
+            return sum(lo), sum(hi)
+        return ' + '.join(map(str, lo)), ' + '.join(map(str, hi))
 
     def _reads_at(self, e, allowed):
         """Does e read group values only at the given index lists (and no folds)?"""
@@ -245,7 +401,11 @@ class AttnMixin:
         writes = {self.root(t[1]) for t in at['t'] if t[1] not in local}
         if pj is not None:
             writes = (writes - {t4[1]}) | {pj['sz'][1]}
-        self.sync(reads, writes, out, ind, t1[1])
+        rd = pj.get('ready') if pj is not None else None
+        if rd is not None:
+            self.attn_ready_point(at, pj, rd, reads, writes, out, ind)
+        else:
+            self.sync(reads, writes, out, ind, t1[1])
         for t in at['t']:
             self.plan.append((self.show_stmt(t), f'attention[{", ".join(lead)}]'))
         if pj is not None:
@@ -532,7 +692,7 @@ class AttnMixin:
             o.append(f'{J}  for (int v_ = 0; v_ < 8; ++v_) a_ = fmaf(ol_[v_], wf_[v_], a_);')
             o.append(f'{J}  a_ = group_red_sum(a_, {LPE});')
             o.append(f'{J}  if (wave < {NW} && cl_ == 0 && dl_ < {DPR} && d_ < {D}) '
-                     f'fxadd(S, {self.g[z1]}u + 2u * (unsigned)({za}), a_);')
+                     f'fxadd(S, {self.gadd(z1)} + 2u * (unsigned)({za}), a_);')
             o.append(f'{J}}}')
         o.append(f'{I}}}')
         self.mark(o, I, 'attention: projection')

@@ -131,6 +131,34 @@ class ChainMixin:
         base = self.rebuild_expr(c2.epi, lambda n: ('num', 0.0) if n == ('name', '__acc') else n)
         return dict(u=s, gs=t, y=y, c=c2, g=g, z=z, f=f, d=d, P=P, PPB=PPB, R=R, D=D, reg=reg, base=base)
 
+    # ------------------------------------------------------------ readiness flags
+    def ready_point(self, what, ranges, active, out, ind, made, setup=()):
+        """Instead of a grid barrier before ``what``: every block publishes
+        that what it stored so far is complete, then waits only for the blocks
+        it reads from: ``ranges`` is a list of (first, last) C expressions of
+        producer blocks (clamped to the grid), ``active`` a C condition (a
+        block that is not active waits for none). Between the two, a prefetch
+        slot takes the loads issued early for the next sites, as between a
+        grid barrier's arrival and wait."""
+        if self.flags_off is None:
+            self.flags_off = self.alloc_counters(self.grid)
+        F = self.flags_off
+        out.append(f'{ind}pk_ += 1u; flag_publish(bar + {F}u, pk_);  // {made} stored: {what} waits for its makers')
+        self.mark(out, ind, f'publish before {what}')
+        self.pf_open(out, ind, self.dirty, self.readers)
+        self.pf_slots[-1]['ready'] = True
+        if len(ranges) > 4:
+            raise ChainError(f'{what}: more than four producer ranges')
+        I = ind + '  '
+        out.append(f'{ind}{{')
+        out += [I + x for x in setup]
+        args = []
+        for q, (lo, hi) in enumerate(ranges):
+            out.append(f'{I}const int a{q}_ = {lo}, n{q}_ = ({active}) ? min({hi}, (int)nblk - 1) - a{q}_ + 1 : 0;')
+            args += [f'a{q}_', f'n{q}_']
+        out.append(f'{I}flag_wait(bar, bar + {F}u, pk_, {", ".join(args)}); }}')
+        self.mark(out, ind, f'wait before {what}')
+
     # ------------------------------------------------------------ storage
     def fx_copy_stride(self, z):
         """Floats between copies of fixed-point sum z (16-byte aligned)."""
@@ -140,16 +168,44 @@ class ChainMixin:
         """Floats of global scratch fixed-point sum z takes (all its copies)."""
         return self.fx_copy_stride(z) * self.fx_copies.get(z, 1)
 
+    def gofs(self, r, ahead=0):
+        """C expression: the float offset of fixed-point sum r in global
+        scratch. A sum kept in two buffers by layer parity (``fx_parity``;
+        layers counted across the steps of a launch, st_ * n + l) has the
+        buffer of the current layer (``ahead`` 1: of the next one); after its
+        layer loop, the buffer the loop's last layer left."""
+        if r not in self.fx_parity:
+            return f'{self.g[r]}u'
+        lv, var, n, _ = self.fx_parity[r]
+        layer = lv if any(lp['var'] == var for lp in self.loops) else str(n)
+        return f'({self.g[r]}u + (unsigned)((st_ * {n} + {layer} + {ahead}) & 1) * {self.fx_words(r)}u)'
+
+    def gadd(self, r):
+        """C expression: the offset the current layer's atomic adds into r go
+        to: the current buffer, or for a layer loop's carry (read as the
+        previous layer left it, added into for the next layer) the next one."""
+        carry = r in self.fx_parity and self.fx_parity[r][3] == 'carry'
+        return self.gofs(r, ahead=1 if carry else 0)
+
     def fx_copy_base(self, z):
         """C expression: float offset of the copy the current block adds into."""
         C = self.fx_copies.get(z, 1)
         return f'(unsigned)(blockIdx.x % {C}u) * {self.fx_copy_stride(z)}u' if C > 1 else '0u'
 
     # ------------------------------------------------------------ code generation
-    def chain_clear(self, z):
+    def chain_clear(self, z, out, ind):
         """Clear z's copies right before the barrier that opened this phase.
         That barrier must not be the first of its loop body, and neither the
-        phase it closes nor this one may touch z before here."""
+        phase it closes nor this one may touch z before here. A layer loop's
+        carry in parity buffers is cleared here instead: the buffer this
+        layer's reads took (in an earlier phase), which the next layer's adds
+        will use."""
+        if z in self.fx_parity and self.fx_parity[z][3] == 'carry':
+            n4 = self.fx_words(z) // 4
+            out.append(f'{ind}for (int e_ = (int)blockIdx.x + (int)nblk * tid; e_ < {n4}; e_ += nthr) '
+                       f'stz4(rb_S, {self.gofs(z)} + 4u * (unsigned)e_);  // clear the buffer of {z} read '
+                       f'before, for the next layer')
+            return
         k, loop = self.last_pf, self.loop_id()
         if k is None or self.pf_slots[k].get('ready'):
             raise ChainError(f'local fold into {z}: no grid barrier right before its phase')
@@ -167,6 +223,9 @@ class ChainMixin:
         atomic add: other blocks' partials may already be in)."""
         z = ch['z']
         axes = list(ch['axes']) if 'axes' in ch else ch['reg'] + [ch['d']]
+        if 'sz' in ch:
+            self.plan.append((self.show_stmt(ch['sz']), 'fixed-point sum in two layer buffers: base and '
+                              'projection added'))
         early = self.early_spread_loads(axes, ch['base'], out, ind)
         I = ind + '  '
         out.append(f'{ind}{{ const unsigned cz_ = {self.fx_copy_base(z)};')
@@ -176,7 +235,7 @@ class ChainMixin:
         pre = []
         v, t = self.spread_value(ch['base'], env, pre, I, early)
         out += pre
-        out.append(f'{I}fxadd(S, {self.g[z]}u + cz_ + 2u * (unsigned)p_, {self.as_float(v, t)});')
+        out.append(f'{I}fxadd(S, {self.gadd(z)} + cz_ + 2u * (unsigned)p_, {self.as_float(v, t)});')
         out.append(f'{ind}}} }}')
         ch['base_done'] = True
         self.mark(out, ind, f'{z} base')
@@ -193,7 +252,7 @@ class ChainMixin:
         self.sync(reads, {z}, out, ind, y[1])
         if self.barriers != nb:
             raise ChainError(f'local fold {y[1]}: its phase would need a barrier after {ch["u"][1]}')
-        self.chain_clear(z)
+        self.chain_clear(z, out, ind)
         self.plan.append((self.show_stmt(y), f'local fold over the points of {ch["u"][1]} '
                           f'({PPB} per block), fixed-point sum in {self.fx_copies[z]} copies'))
         NW = self.NWAVE - 1
@@ -284,7 +343,7 @@ class ChainMixin:
         o.append(f'{I}    float v_ = sh_f[{red} + e_];')
         for q in range(1, RG):
             o.append(f'{I}    v_ += sh_f[{red} + {q * R * D} + e_];')
-        o.append(f'{I}    fxadd(S, {self.g[z]}u + cz_ + 2u * (unsigned)e_, v_);')
+        o.append(f'{I}    fxadd(S, {self.gadd(z)} + cz_ + 2u * (unsigned)e_, v_);')
         o.append(f'{I}  }}')
         o.append(f'{I}}}')
         o.append(f'{ind}}}')

@@ -538,14 +538,20 @@ __device__ __forceinline__ void flag_publish(unsigned* flags, unsigned k) {
   vh_lds_sync();
   if (threadIdx.x == 0) stc_u(flags + VH_BAR_LINE * blockIdx.x, k);
 }
-// Until blocks p0 .. p0 + np - 1 (np <= 64) have published k: lane g of the
-// polling wave watches producer p0 + g, with grid_wait's spin limit and
-// error-word checks.
-__device__ __forceinline__ void flag_wait(unsigned* bar, const unsigned* flags, int p0, int np, unsigned k) {
+// Until blocks a0 .. a0 + n0 - 1, a1 .. a1 + n1 - 1, .. (at most 4 ranges, at
+// most 64 blocks in all; the bounds are the same for every thread of the
+// block) have published k: lane g of the polling wave watches the g-th of
+// them, with grid_wait's spin limit and error-word checks.
+__device__ __forceinline__ void flag_wait(unsigned* bar, const unsigned* flags, unsigned k, int a0, int n0,
+                                          int a1 = 0, int n1 = 0, int a2 = 0, int n2 = 0, int a3 = 0, int n3 = 0) {
   if ((int)(threadIdx.x >> 6) == VH_POLL_WAVE) {
     const int g = (int)(threadIdx.x & 63u);
-    bool done = g >= np;
-    const unsigned* cp = flags + VH_BAR_LINE * (done ? 0 : p0 + g);
+    const int pid = g < n0 ? a0 + g
+                  : g < n0 + n1 ? a1 + g - n0
+                  : g < n0 + n1 + n2 ? a2 + g - n0 - n1
+                  : g < n0 + n1 + n2 + n3 ? a3 + g - n0 - n1 - n2 : -1;
+    bool done = pid < 0;
+    const unsigned* cp = flags + VH_BAR_LINE * (done ? 0 : pid);
     unsigned n = 0;
     while (true) {
       if (!done) done = ldc_u(cp) >= k;

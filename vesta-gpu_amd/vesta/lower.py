@@ -275,9 +275,11 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
         self.chain_local = set()      # values kept only in the LDS of the block that made them
         self.chain_lds = {}           # such a value -> (LDS base, points/block, rows) of the site just made
         self.fx_copies = {}           # fixed-point sum -> copies its adders spread over
-        self.flags_off = None         # readiness flag lines in bar (one per block), when a split uses them
+        self.flags_off = None         # readiness flag lines in bar (one per block), when a site uses them
+        self.fx_parity = {}           # fixed-point sum -> (layer loop variable, its extent): two buffers
         if local_folds:
             self.find_chains(stmts)
+            self.find_ready_attn(stmts)
         self.layout(stmts)
 
     # ------------------------------------------------------------ rewrites
@@ -630,7 +632,8 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
             if r in self.private or r in self.g or n in self.inlined or r in self.elided_vals:
                 continue
             self.g[r] = self.goff
-            words = self.fx_words(r) if r in self.fx else max(1, self.size(self.axes_of[r]))
+            words = (self.fx_words(r) * (2 if r in self.fx_parity else 1) if r in self.fx
+                     else max(1, self.size(self.axes_of[r])))
             self.goff += -(-words // LINE_WORDS) * LINE_WORDS
         self.counters = BAR_WORDS
         self.staged = {}
@@ -890,11 +893,11 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
             return self.lds_read(f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}]')
         pv = self.peel_value(r, ix)
         if r in self.fx_copies:
-            i = f'{self.g[r]} + 2u * ({a})'
+            i = f'{self.gofs(r)} + 2u * ({a})'
             v = f'fxld_c<{self.fx_copies[r]}>(rb_S, {i}, {self.fx_copy_stride(r)}u)'
             return f'({pv[0]} == 0 ? {pv[1]} : {v})' if pv is not None else self.captured(v, 'float', r)
         if r in self.fx:
-            i = f'{self.g[r]} + 2u * ({a})'
+            i = f'{self.gofs(r)} + 2u * ({a})'
             if pv is not None:
                 return f'({pv[0]} == 0 ? {pv[1]} : fxld(rb_S, {i}))'
             return self.captured(f'fxld(rb_S, {i})', 'float', r, raw=(f'ldfx_raw(rb_S, {i})', 'long long', 'vh_fx2f'))
@@ -910,8 +913,8 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
         if r in self.glocal:
             off, plen = self.glocal[r]
             return f'sh_f[{off} + {self.addr(ix[plen:], self.strides(self.axes_of[r][plen:]))}] = {self.as_float(v, t)};'
-        if r in self.fx_copies:
-            raise LowerError(f'{r} is a fixed-point sum in copies: only atomic adds go into it')
+        if r in self.fx_copies or r in self.fx_parity:
+            raise LowerError(f'{r} is a fixed-point sum in copies or parity buffers: only atomic adds go into it')
         if r in self.fx:
             return f'fxst(rb_S, {self.g[r]} + 2u * ({a}), {self.as_float(v, t)});'
         return f'stcs(rb_S, {self.g[r]} + {a}, {self.as_float(v, t)});'
@@ -1787,9 +1790,9 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
                 if off - base + size <= STAGE_MAX:
                     staged[r] = off
                     fn = 'stage_fx' if r in self.fx else 'stage_ldc4'
-                    call = f'{fn}(sh_f + {off}, rb_S, {self.g[r]}, {size});'
+                    call = f'{fn}(sh_f + {off}, rb_S, {self.gofs(r) if r in self.fx else self.g[r]}, {size});'
                     if r in self.fx_copies:
-                        call = (f'stage_fxc<{self.fx_copies[r]}>(sh_f + {off}, rb_S, {self.g[r]}, {size}, '
+                        call = (f'stage_fxc<{self.fx_copies[r]}>(sh_f + {off}, rb_S, {self.gofs(r)}, {size}, '
                                 f'{self.fx_copy_stride(r)}u);')
                     if r in self.peel_active:
                         lv, zs = self.peel_active[r]
@@ -2802,6 +2805,10 @@ def _lower_once(text, res, axis_max, batch, per_token, outputs, feedback, timing
            + ''.join(fb_init)
            + (f'  const unsigned TSB_ = {len(low.sites)}u * nblk;  // barrier trace after the site table\n'
               if timing else '')
+           + ''.join(f'  for (int e_ = gtid; e_ < {low.fx_words(r) // 2}; e_ += nthr) stz4(rb_S, {low.g[r]}u + 4u * '
+                     f'(unsigned)e_);  // both layer buffers of {r}, cleared once a launch\n'
+                     for r in sorted(low.fx_parity))
+           + ('  grid_sync(bar, nblk, bk_);\n' if low.fx_parity else '')
            + '  for (int st_ = 0; st_ < nsteps; ++st_) {\n'
            + '    const int tid = vh_opaque(tid_k_), lane = tid & 63, wave = tid >> 6;\n'
            + ('    const unsigned bk0_ = bk_;\n' if timing else '')

@@ -451,26 +451,6 @@ class MfmaMixin:
             return None
         return dict(g=g, PPB=PPB)
 
-    def ready_point(self, pp, sk, out, ind, name):
-        """Every block publishes that its part of g is stored; a block of
-        fold slice q then waits for the blocks that made g's points of that
-        slice (u's block b made points [b * PPB, (b + 1) * PPB)). Between the
-        two, the split's weights are issued (a prefetch slot, as between a
-        grid barrier's arrival and wait)."""
-        if self.flags_off is None:
-            self.flags_off = self.alloc_counters(self.grid)
-        F, PPB = self.flags_off, pp['PPB']
-        NKB, KS, NPG = sk['st'].K // 32, sk['KS'], sk['NPG']
-        out.append(f'{ind}pk_ += 1u; flag_publish(bar + {F}u, pk_);  // {pp["g"]} stored: {name} waits for its makers')
-        self.mark(out, ind, f'publish before {name}')
-        self.pf_open(out, ind, self.dirty, self.readers)
-        self.pf_slots[-1]['ready'] = True
-        out.append(f'{ind}{{ const int q_ = (int)blockIdx.x % {KS};')
-        out.append(f'{ind}  const int p0_ = (q_ * {NKB} / {KS}) * 32 / {PPB}, '
-                   f'p1_ = min((((q_ + 1) * {NKB} / {KS}) * 32 - 1) / {PPB}, (int)nblk - 1);')
-        out.append(f'{ind}  flag_wait(bar, bar + {F}u, p0_, (int)blockIdx.x < {NPG * KS} ? p1_ - p0_ + 1 : 0, pk_); }}')
-        self.mark(out, ind, f'wait before {name}')
-
     def gen_stream_split(self, s, sk, out, ind):
         c, st = sk['c'], sk['st']
         name, z = s[1], self.root(s[1])
@@ -496,10 +476,13 @@ class MfmaMixin:
             from .chain import ChainError
             if ((reads - {pp['g']}) & self.dirty) or z in self.readers:
                 raise ChainError(f'split {name}: its phase would need a barrier after all')
-            self.chain_clear(z)
+            self.chain_clear(z, out, ind)
             if not sk.get('base_done'):
                 self.chain_base(sk, out, ind)
-            self.ready_point(pp, sk, out, ind, name)
+            PPB, NKB, KS = pp['PPB'], sk['st'].K // 32, sk['KS']
+            self.ready_point(name, [(f'((int)blockIdx.x % {KS} * {NKB} / {KS}) * 32 / {PPB}',
+                                     f'(((int)blockIdx.x % {KS} + 1) * {NKB} / {KS} * 32 - 1) / {PPB}')],
+                             f'(int)blockIdx.x < {sk["NPG"] * KS}', out, ind, pp['g'])
         else:
             if not sk.get('base_done'):
                 self.emit_base(None, z, list(s[2]), sk['base'], out, ind, sync=True)
@@ -627,7 +610,7 @@ class MfmaMixin:
             o.append(f'{I}      #pragma unroll')
             o.append(f'{I}      for (int v_ = 0; v_ < 4; ++v_) {{')
             o.append(f'{I}        const int r_ = (lane >> 4) * 4 + v_;')
-            o.append(f'{I}        if (r_ < {R}) fxadd(S, {self.g[z]}u + 2u * (unsigned)(r_ * {P} + p_), acc_[{i}][v_]);')
+            o.append(f'{I}        if (r_ < {R}) fxadd(S, {self.gadd(z)} + 2u * (unsigned)(r_ * {P} + p_), acc_[{i}][v_]);')
             o.append(f'{I}      }}')
             o.append(f'{I}    }}')
             o.append(f'{I}  }}')
