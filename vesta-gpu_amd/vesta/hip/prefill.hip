@@ -267,6 +267,70 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce(
   pf_epi(mode, m, n, c, bias, N, out, ldo, kc, vc, P, tp, layer, L, tmax);
 }
 
+// A split residual product's parts added (pf_reduce, mode 1: Z[m, n] =
+// (Z[m, n] + C) + bias[n]) and the LayerNorm that reads Z next (pf_ln into
+// Y), in one launch: one block per row, the row kept in registers between
+// the two. The same sums in the same order as the two launches it replaces,
+// so the same bits.
+extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
+    const float* __restrict__ ws, int ksplit, const vh_half* __restrict__ bias, int M, int D,
+    float* __restrict__ Z, const vh_half* __restrict__ w, const vh_half* __restrict__ b, float* __restrict__ Y) {
+  __shared__ float red[VNWAVE];
+  const int m = blockIdx.x;
+  float* z = Z + (size_t)m * D;
+  float* y = Y + (size_t)m * D;
+  const float fd = (float)D;
+  // the parts of the thread's 8 values, eight parts' loads in flight at once,
+  // added in part order
+  float v[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = threadIdx.x + j * 256;
+    v[j] = i < D ? ws[(size_t)m * D + i] : 0.0f;
+  }
+  for (int k0 = 1; k0 < ksplit; k0 += 8) {
+    float p[8][8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int i = threadIdx.x + j * 256;
+        p[u][j] = (k0 + u < ksplit && i < D) ? ws[((size_t)(k0 + u) * M + m) * D + i] : 0.0f;
+      }
+#pragma unroll
+    for (int u = 0; u < 8; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (k0 + u < ksplit) v[j] += p[u][j];
+  }
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = threadIdx.x + j * 256;
+    if (i < D) {
+      const float bn = bias ? h2f(bias[i]) : 0.0f;
+      v[j] = (z[i] + v[j]) + bn;
+      z[i] = v[j];
+      s += v[j] / fd;
+    }
+  }
+  const float mean = block_red_sum(s, red);
+  float q = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = threadIdx.x + j * 256;
+    if (i < D) q += (v[j] - mean) * (v[j] - mean) / fd;
+  }
+  vh_lds_sync();
+  const float var = block_red_sum(q, red);
+  const float sd = sqrtf(var + 0.00001f);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    const int i = threadIdx.x + j * 256;
+    if (i < D) y[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
+  }
+}
+
 // ---------------------------------------------------------------- attention
 // One wave per (row m, head h): scores of the query against cache positions
 // 0 .. t0 + p (gpt2.vst Q5: dot over e, divided by 8; a lane per position),

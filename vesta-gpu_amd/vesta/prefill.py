@@ -27,11 +27,15 @@ BLOCK = 256
 TILE = 64
 CHUNK = 64                    # fold depth one product step stages in LDS
 HEAD = 64
-KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_attn', 'pf_attn1', 'pf_argmax_part', 'pf_argmax')
+KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_reduce_ln', 'pf_attn', 'pf_attn1', 'pf_argmax_part',
+           'pf_argmax')
 ARGMAX_SPLIT = 16             # blocks per row of the output-head argmax
 SPLIT_BLOCKS = 384            # a product with fewer output tiles than this splits its fold over blocks ...
                               # (XL B=64 decode: 4.95 ms per step at 320-384, 5.18 at 256, 5.42 at 512)
 SPLIT_MIN_CHUNKS = 4          # ... into parts of at least this many 64-deep chunks
+FUSE_REDUCE_LN = True         # a split residual product's reduction makes the LayerNorm that follows (one
+                              # launch instead of two; same box: GPT-2 small B=32 1.073 -> 1.055 ms per step,
+                              # XL B=64 5.194 -> 5.212: one block per row reads all the parts of its row)
 MODE_PLAIN, MODE_RESID, MODE_GELU, MODE_QKV = 0, 1, 2, 3
 
 
@@ -144,10 +148,13 @@ class Prefill:
                 self.m.W[name[:-3]].transpose(-1, -2).contiguous()
         return self._own[name]
 
-    def _gemm(self, A, lda, Wt, bias, M, N, K, mode, out, ldo, layer=0, P=1):
+    def _gemm(self, A, lda, Wt, bias, M, N, K, mode, out, ldo, layer=0, P=1, ln=None):
         """One product launch; with few output tiles, or a long fold, the fold
         is split over blocks too (partial tiles into a workspace, then
-        ``pf_reduce`` adds them in order and applies the epilogue)."""
+        ``pf_reduce`` adds them in order and applies the epilogue). ``ln``
+        (w, b, Y) for a residual product: the LayerNorm of all M rows of
+        ``out`` into Y that comes next; a split product then does it in the
+        launch that adds its parts (``pf_reduce_ln``). Returns whether it did."""
         m = self.m
         tiles = -(-M // TILE) * -(-N // TILE)
         ks = max(1, min(-(-SPLIT_BLOCKS // tiles), (K // CHUNK) // SPLIT_MIN_CHUNKS))
@@ -155,9 +162,14 @@ class Prefill:
         tail = [_p(m.keys), _p(m.vals), _i(P), _p(m.t), _i(layer), _i(m.L), _i(m.tmax)]
         self._launch('pf_gemm', tiles * ks, [_p(A), _i(lda), _p(Wt), _p(bias), _i(M), _i(N), _i(K), _i(mode),
                                              _p(out), _i(ldo)] + tail + [_i(ks), _p(ws), _p(self.err)])
+        if FUSE_REDUCE_LN and ks > 1 and ln is not None and mode == MODE_RESID and ldo == N:
+            w, b, Y = ln
+            self._launch('pf_reduce_ln', M, [_p(ws), _i(ks), _p(bias), _i(M), _i(N), _p(out), _p(w), _p(b), _p(Y)])
+            return True
         if ks > 1:
             self._launch('pf_reduce', -(-M * N // BLOCK), [_p(ws), _i(ks), _p(bias), _i(M), _i(N), _i(mode),
                                                             _p(out), _i(ldo)] + tail)
+        return False
 
     def _workspace(self, n):
         """Partial tiles of split products: one buffer, grown to the largest
@@ -247,13 +259,15 @@ class Prefill:
         Z, A, Q, G, C = buf['Z'], buf['A'], buf['Q'], buf['G'], buf['C']
         self._launch('pf_embed', M, [_p(tok), _i(P), _p(m.t), _p(W['wte']), _p(W['wpe']), _p(Z), _i(D), _i(V),
                                      _i(W['wpe'].shape[0])])
+        normed = False                  # A holds LN1 of Z already (made by the last product's reduction)
         for layer in range(L):
-            def lw(name):
+            def lw(name, layer=layer):
                 return W[name][layer]
 
             def lt(name):
                 return self._transposed(name)[layer]
-            self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln1w')), _p(lw('ln1b')), _p(A), _i(D)])
+            if not normed:
+                self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln1w')), _p(lw('ln1b')), _p(A), _i(D)])
             self._gemm(A, D, lt('qkvw__t'), lw('qkvb'), M, 3 * D, D, MODE_QKV, Q, D, layer, P)
             if P == 1:      # a decode pass: a block per (row, head) (GPT-2 small, 32 rows, 1024
                             # positions: 1.32 -> 1.07 ms per step against a wave per (row, head))
@@ -263,11 +277,17 @@ class Prefill:
                 self._launch('pf_attn', -(-M * H // (BLOCK // 64)),
                              [_p(Q), _p(m.keys), _p(m.vals), _p(A), _i(M), _i(P), _p(m.t), _i(layer), _i(L),
                               _i(m.tmax), _i(H)])
-            self._gemm(A, D, lt('ow__t'), lw('ob'), M, D, D, MODE_RESID, Z, D)
-            self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln2w')), _p(lw('ln2b')), _p(A), _i(D)])
+            if not self._gemm(A, D, lt('ow__t'), lw('ob'), M, D, D, MODE_RESID, Z, D,
+                              ln=(lw('ln2w'), lw('ln2b'), A)):
+                self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln2w')), _p(lw('ln2b')), _p(A), _i(D)])
             self._gemm(A, D, lt('fcw__t'), lw('fcb'), M, F, D, MODE_GELU, G, F)
-            self._gemm(G, F, lt('pw__t'), lw('pb'), M, D, F, MODE_RESID, Z, D)
-        self._launch('pf_ln', B, [_p(Z), _i(P - 1), _i(P), _p(W['lnfw']), _p(W['lnfb']), _p(C), _i(D)])
+            if layer + 1 < L:
+                nxt = (lw('ln1w', layer + 1), lw('ln1b', layer + 1), A)
+            else:
+                nxt = (W['lnfw'], W['lnfb'], C) if P == 1 else None   # the final norm: each row's last position
+            normed = self._gemm(G, F, lt('pw__t'), lw('pb'), M, D, F, MODE_RESID, Z, D, ln=nxt)
+        if not normed:
+            self._launch('pf_ln', B, [_p(Z), _i(P - 1), _i(P), _p(W['lnfw']), _p(W['lnfb']), _p(C), _i(D)])
         logit, nxt = m.logits(), m.next()
         self._gemm(C, D, W['wte'], None, B, V, D, MODE_PLAIN, logit, V)
         self._launch('pf_argmax_part', B * ARGMAX_SPLIT, [_p(logit), _i(V), _i(ARGMAX_SPLIT), _p(buf['apv']),
