@@ -39,14 +39,40 @@ extern "C" __global__ __launch_bounds__(256) void pf_embed(const int* __restrict
     Z[(size_t)m * D + i] = h2f(wte[(size_t)x * D + i]) + h2f(wpe[(size_t)pos * D + i]);
 }
 
+// ---------------------------------------------------------------- fragment order
+// The decode products (pf_mgemm*, at most 64 rows) read both operands in the
+// order the matrix cores take them (v_mfma_f32_16x16x32_f16: lane l = 16 q + r
+// holds row r, fold positions 8 q .. 8 q + 7 of a 16 x 32 operand tile), so
+// that each operand load of a wave is one contiguous kilobyte:
+//   weights      Wf[n-tile][k-step][lane][8]         n = 16 n-tile + r
+//   activations  Af[plane][m-tile][k-step][lane][8]  m = 16 m-tile + r
+// with k = 32 k-step + 8 q + e; plane 0 holds the nearest fp16 (hi), plane 1
+// the remainder scaled by 2^11 (vh_split8s). MT m-tiles, KT k-steps; rows
+// past the last real one are never written and only reach discarded outputs.
+// A producer of an activation row stores eight values k8 .. k8 + 7 (k8 a
+// multiple of 8) of row m at once; `bad` is raised for a value beyond the
+// fp16 range.
+__device__ __forceinline__ void pf_frag_put8(vh_half* __restrict__ F, int MT, int KT, int m, int k8, const float* v,
+                                             bool& bad) {
+  bad |= vh_beyond_half8(v);
+  vh_u32x4 hi, lo;
+  vh_split8s(v, hi, lo);
+  const size_t at = (((size_t)(m >> 4) * KT + (k8 >> 5)) * 64 + ((k8 >> 3) & 3) * 16 + (m & 15)) * 8;
+  *(vh_u32x4*)(F + at) = hi;
+  *(vh_u32x4*)(F + (size_t)MT * KT * 512 + at) = lo;
+}
+
 // ---------------------------------------------------------------- layer norm
 // Y[i] = (X[r] - mean) / sqrt(var + 1e-5) * w + b for r = row0 + i * rstride
 // (biased variance; mean and variance as sums of x / D and (x - mean)^2 / D,
-// as gpt2.vst Q2 writes them). One block per output row; D <= 8 * 256.
+// as gpt2.vst Q2 writes them). One block per output row; D <= 8 * 256. With
+// F set the row goes to F in fragment order (MT m-tiles) instead of Y.
 extern "C" __global__ __launch_bounds__(256) void pf_ln(const float* __restrict__ X, int row0, int rstride,
                                                          const vh_half* __restrict__ w, const vh_half* __restrict__ b,
-                                                         float* __restrict__ Y, int D) {
+                                                         float* __restrict__ Y, int D, vh_half* __restrict__ F, int MT,
+                                                         unsigned* __restrict__ err) {
   __shared__ float red[VNWAVE];
+  __shared__ __attribute__((aligned(16))) float out[8 * 256];
   const float* x = X + (size_t)(row0 + (size_t)blockIdx.x * rstride) * D;
   float* y = Y + (size_t)blockIdx.x * D;
   const float fd = (float)D;
@@ -68,11 +94,23 @@ extern "C" __global__ __launch_bounds__(256) void pf_ln(const float* __restrict_
   vh_lds_sync();
   const float var = block_red_sum(q, red);
   const float sd = sqrtf(var + 0.00001f);
+  if (F == nullptr) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = threadIdx.x + j * 256;
+      if (i < D) y[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int i = threadIdx.x + j * 256;
-    if (i < D) y[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
+    if (i < D) out[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
   }
+  __syncthreads();
+  bool bad = false;
+  if (8 * (int)threadIdx.x < D) pf_frag_put8(F, MT, D / 32, blockIdx.x, 8 * threadIdx.x, out + 8 * threadIdx.x, bad);
+  if (bad) stc_u(err, VH_ERR_RANGE);
 }
 
 // ---------------------------------------------------------------- products
@@ -271,11 +309,14 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce(
 // (Z[m, n] + C) + bias[n]) and the LayerNorm that reads Z next (pf_ln into
 // Y), in one launch: one block per row, the row kept in registers between
 // the two. The same sums in the same order as the two launches it replaces,
-// so the same bits.
+// so the same bits. With F set the normalised row goes to F in fragment order
+// (MT m-tiles) instead of Y.
 extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
     const float* __restrict__ ws, int ksplit, const vh_half* __restrict__ bias, int M, int D,
-    float* __restrict__ Z, const vh_half* __restrict__ w, const vh_half* __restrict__ b, float* __restrict__ Y) {
+    float* __restrict__ Z, const vh_half* __restrict__ w, const vh_half* __restrict__ b, float* __restrict__ Y,
+    vh_half* __restrict__ F, int MT, unsigned* __restrict__ err) {
   __shared__ float red[VNWAVE];
+  __shared__ __attribute__((aligned(16))) float out[8 * 256];
   const int m = blockIdx.x;
   float* z = Z + (size_t)m * D;
   float* y = Y + (size_t)m * D;
@@ -324,11 +365,169 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
   vh_lds_sync();
   const float var = block_red_sum(q, red);
   const float sd = sqrtf(var + 0.00001f);
+  if (F == nullptr) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int i = threadIdx.x + j * 256;
+      if (i < D) y[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
+    }
+    return;
+  }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int i = threadIdx.x + j * 256;
-    if (i < D) y[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
+    if (i < D) out[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
   }
+  __syncthreads();
+  bool bad = false;
+  if (8 * (int)threadIdx.x < D) pf_frag_put8(F, MT, D / 32, m, 8 * threadIdx.x, out + 8 * threadIdx.x, bad);
+  if (bad) stc_u(err, VH_ERR_RANGE);
+}
+
+// ---------------------------------------------------------------- decode products
+// C = A W over K for M <= 16 MT rows, both operands in fragment order (above):
+// the weights streamed from memory straight into the matrix cores' registers,
+// the activations read as they are (hi and lo planes, each multiplied into
+// its own accumulator and combined at the end). A block is PF_MW waves on the
+// same PF_MN n-tiles (32 columns); block b takes n-tile pair b / ks and fold
+// part b % ks of ks, and its waves split that part's k-steps into PF_MW
+// consecutive runs, each wave keeping the next k-step's operands in flight
+// while it multiplies the current one. The waves' partial tiles are added in
+// LDS in wave order. Then either the part is stored (ks > 1: ws[part][m][n],
+// added by pf_reduce / pf_reduce_ln / pf_reduce_frag), or the epilogue of
+// `mode` is applied: 0, 1 and 3 as pf_epi (one position per row); 2 (GELU)
+// writes the result in fragment order into F, as the activation of the next
+// product (N / 32 k-steps).
+#define PF_MW 8
+#define PF_MN 2
+template <int MT>
+__device__ __forceinline__ void pf_mgemm_body(
+    const vh_u32x4* __restrict__ Af, const vh_u32x4* __restrict__ Wf, int KT, int NT, int ks,
+    const vh_half* __restrict__ bias, int M, int N, int mode, float* __restrict__ out, int ldo,
+    vh_half* __restrict__ kc, vh_half* __restrict__ vc, const int* __restrict__ tp, int layer, int L, int tmax,
+    float* __restrict__ ws, vh_half* __restrict__ F, unsigned* __restrict__ err) {
+  __shared__ __attribute__((aligned(16))) vh_f32x4 red[PF_MW][PF_MN * MT * 64];
+  __shared__ __attribute__((aligned(16))) float tile[16 * MT][16 * PF_MN + 4];
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int part = blockIdx.x % ks, nt0 = (blockIdx.x / ks) * PF_MN;
+  const int ka = part * KT / ks, kb = (part + 1) * KT / ks;
+  const int k0 = ka + (kb - ka) * wave / PF_MW, k1 = ka + (kb - ka) * (wave + 1) / PF_MW;
+  vh_f32x4 acc[PF_MN][MT], acl[PF_MN][MT];
+#pragma unroll
+  for (int t = 0; t < PF_MN; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = acl[t][mt] = vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const size_t plane = (size_t)MT * KT * 64;
+  vh_u32x4 wa[PF_MN], aa[2][MT], wb[PF_MN], ab[2][MT];
+  auto load = [&](vh_u32x4 (&w)[PF_MN], vh_u32x4 (&a)[2][MT], int k) {
+    const bool in = k < k1;
+#pragma unroll
+    for (int t = 0; t < PF_MN; ++t)
+      w[t] = in && nt0 + t < NT ? Wf[((size_t)(nt0 + t) * KT + k) * 64 + lane] : vh_u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        a[p][mt] = in ? Af[p * plane + ((size_t)mt * KT + k) * 64 + lane] : vh_u32x4{0u, 0u, 0u, 0u};
+  };
+  auto mma = [&](const vh_u32x4 (&w)[PF_MN], const vh_u32x4 (&a)[2][MT]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < PF_MN; ++t) {
+        acc[t][mt] = vh_mfma(a[0][mt], w[t], acc[t][mt]);
+        acl[t][mt] = vh_mfma(a[1][mt], w[t], acl[t][mt]);
+      }
+  };
+  load(wa, aa, k0);
+  for (int k = k0; k < k1; k += 2) {
+    load(wb, ab, k + 1);
+    mma(wa, aa);
+    if (k + 1 >= k1) break;
+    load(wa, aa, k + 2);
+    mma(wb, ab);
+  }
+#pragma unroll
+  for (int t = 0; t < PF_MN; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const vh_f32x4 h = acc[t][mt], l = acl[t][mt];
+      red[wave][(t * MT + mt) * 64 + lane] =
+          vh_f32x4{vh_hilo(h[0], l[0]), vh_hilo(h[1], l[1]), vh_hilo(h[2], l[2]), vh_hilo(h[3], l[3])};
+    }
+  __syncthreads();
+  for (int i = threadIdx.x; i < PF_MN * MT * 64; i += PF_MW * 64) {
+    vh_f32x4 s = red[0][i];
+#pragma unroll
+    for (int w = 1; w < PF_MW; ++w) {
+      const vh_f32x4 o = red[w][i];
+      s = vh_f32x4{s[0] + o[0], s[1] + o[1], s[2] + o[2], s[3] + o[3]};
+    }
+    const int l = i & 63, tm = i >> 6, mt = tm % MT, t = tm / MT;
+#pragma unroll
+    for (int v = 0; v < 4; ++v) tile[16 * mt + 4 * (l >> 4) + v][16 * t + (l & 15)] = s[v];
+  }
+  __syncthreads();
+  const int n0 = 16 * nt0;
+  if (ks == 1 && mode == 2) {
+    bool bad = false;
+    for (int e = threadIdx.x; e < 16 * MT * 2 * PF_MN; e += PF_MW * 64) {
+      const int m = e / (2 * PF_MN), c8 = 8 * (e % (2 * PF_MN));
+      if (m >= M || n0 + c8 >= N) continue;
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = pf_gelu(tile[m][c8 + j] + h2f(bias[n0 + c8 + j]));
+      pf_frag_put8(F, MT, N / 32, m, n0 + c8, v, bad);
+    }
+    if (bad) stc_u(err, VH_ERR_RANGE);
+    return;
+  }
+  for (int e = threadIdx.x; e < 16 * MT * 16 * PF_MN; e += PF_MW * 64) {
+    const int m = e / (16 * PF_MN), c = e % (16 * PF_MN), n = n0 + c;
+    if (m >= M || n >= N) continue;
+    if (ks > 1)
+      ws[((size_t)part * M + m) * N + n] = tile[m][c];
+    else
+      pf_epi(mode, m, n, tile[m][c], bias, N, out, ldo, kc, vc, 1, tp, layer, L, tmax);
+  }
+}
+
+#define PF_MGEMM(name, MT)                                                                                         \
+  extern "C" __global__ __launch_bounds__(PF_MW * 64) void name(                                                  \
+      const vh_u32x4* __restrict__ Af, const vh_u32x4* __restrict__ Wf, int KT, int NT, int ks,                    \
+      const vh_half* __restrict__ bias, int M, int N, int mode, float* __restrict__ out, int ldo,                 \
+      vh_half* __restrict__ kc, vh_half* __restrict__ vc, const int* __restrict__ tp, int layer, int L, int tmax, \
+      float* __restrict__ ws, vh_half* __restrict__ F, unsigned* __restrict__ err) {                              \
+    pf_mgemm_body<MT>(Af, Wf, KT, NT, ks, bias, M, N, mode, out, ldo, kc, vc, tp, layer, L, tmax, ws, F, err);   \
+  }
+PF_MGEMM(pf_mgemm1, 1)
+PF_MGEMM(pf_mgemm2, 2)
+PF_MGEMM(pf_mgemm4, 4)
+
+// The parts of a split GELU product (ws[part][m][n], part order) with the
+// bias and GELU, written in fragment order into F like pf_mgemm's mode 2: one
+// thread per eight consecutive columns of a row.
+extern "C" __global__ __launch_bounds__(256) void pf_reduce_frag(const float* __restrict__ ws, int ksplit,
+                                                                  const vh_half* __restrict__ bias, int M, int N,
+                                                                  vh_half* __restrict__ F, int MT,
+                                                                  unsigned* __restrict__ err) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= M * (N / 8)) return;
+  const int m = e / (N / 8), n8 = 8 * (e % (N / 8));
+  float v[8];
+  const float* p = ws + (size_t)m * N + n8;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = p[j];
+  for (int k = 1; k < ksplit; ++k) {
+    const float* q = p + (size_t)k * M * N;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] += q[j];
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = pf_gelu(v[j] + h2f(bias[n8 + j]));
+  bool bad = false;
+  pf_frag_put8(F, MT, N / 32, m, n8, v, bad);
+  if (bad) stc_u(err, VH_ERR_RANGE);
 }
 
 // ---------------------------------------------------------------- attention
@@ -433,7 +632,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restric
 extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restrict__ Q, const vh_half* __restrict__ kc,
                                                             const vh_half* __restrict__ vc, float* __restrict__ O,
                                                             const int* __restrict__ tp, int layer, int L, int tmax,
-                                                            int H) {
+                                                            int H, vh_half* __restrict__ F, int MT,
+                                                            unsigned* __restrict__ err) {
   __shared__ float qs[PF_E];
   __shared__ float ws[PF_TMAX];
   __shared__ float red[VNWAVE];
@@ -517,7 +717,16 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restri
     float r = part[0][tid];
 #pragma unroll
     for (int w = 1; w < VNWAVE; ++w) r += part[w][tid];
-    O[(size_t)m * D + h * PF_E + tid] = r;
+    if (F == nullptr)
+      O[(size_t)m * D + h * PF_E + tid] = r;
+    else
+      qs[tid] = r;
+  }
+  if (F != nullptr) {       // the head's 64 outputs in fragment order, eight per thread
+    __syncthreads();
+    bool bad = false;
+    if (tid < PF_E / 8) pf_frag_put8(F, MT, D / 32, m, h * PF_E + 8 * tid, qs + 8 * tid, bad);
+    if (bad) stc_u(err, VH_ERR_RANGE);
   }
 }
 

@@ -28,7 +28,7 @@ TILE = 64
 CHUNK = 64                    # fold depth one product step stages in LDS
 HEAD = 64
 KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_reduce_ln', 'pf_attn', 'pf_attn1', 'pf_argmax_part',
-           'pf_argmax')
+           'pf_argmax', 'pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_reduce_frag')
 ARGMAX_SPLIT = 16             # blocks per row of the output-head argmax
 SPLIT_BLOCKS = 384            # a product with fewer output tiles than this splits its fold over blocks ...
                               # (XL B=64 decode: 4.95 ms per step at 320-384, 5.18 at 256, 5.42 at 512)
@@ -37,12 +37,24 @@ FUSE_REDUCE_LN = True         # a split residual product's reduction makes the L
                               # launch instead of two; same box: GPT-2 small B=32 1.073 -> 1.055 ms per step,
                               # XL B=64 5.194 -> 5.212: one block per row reads all the parts of its row)
 MODE_PLAIN, MODE_RESID, MODE_GELU, MODE_QKV = 0, 1, 2, 3
+DECODE_ROWS = 64              # decode passes of up to this many rows run the fragment-order products (pf_mgemm*)
+MG_WAVES = 8                  # waves of a pf_mgemm block ...
+MG_TILES = 2                  # ... and the 16-column tiles it makes
+MG_BLOCKS = 200               # a decode product splits its fold so that it has about this many blocks, ...
+MG_MIN_STEPS = 16             # ... each part at least this many 32-deep k-steps (two per wave)
+FRAG_DECODE = True            # decode passes on the fragment-order products (else the prefill products)
 
 
 def supported(D, H, F):
     """Shapes the prefill kernels take: 64-wide heads and products whose fold
     lengths are multiples of the 64-deep chunk a product stages at a time."""
     return H * HEAD == D and D % CHUNK == 0 and F % CHUNK == 0 and D <= 8 * BLOCK
+
+
+def _mtiles(rows: int) -> int:
+    """16-row tiles of a decode product's kernel (pf_mgemm1 / 2 / 4)."""
+    t = -(-rows // 16)
+    return 1 if t <= 1 else 2 if t == 2 else 4
 
 
 def prefill_source(tmax: int) -> str:
@@ -119,9 +131,9 @@ class Prefill:
     def __del__(self):
         self.close()
 
-    def _launch(self, name, grid, vals):
+    def _launch(self, name, grid, vals, block=BLOCK):
         """Record one launch of the plan being built."""
-        self._plan.append((name, self.fn[name], int(grid), _Args(vals)))
+        self._plan.append((name, self.fn[name], int(grid), _Args(vals), int(block)))
 
     def _buffers(self, M):
         """Activation buffers for M rows (one set per row count, kept)."""
@@ -137,6 +149,120 @@ class Prefill:
                                  apv=torch.empty(m.B * ARGMAX_SPLIT, **f32),
                                  api=torch.empty(m.B * ARGMAX_SPLIT, dtype=torch.int32, device='cuda'))
         return self._bufs[M]
+
+    def _decode_buffers(self, B):
+        """Fragment-order activations of a decode pass of B rows: AF for the
+        products over d (LayerNorm and attention outputs), GF for the one over
+        the feed-forward width (GELU outputs). Zeroed once: rows past B are
+        never written."""
+        import torch
+        key = ('frag', B)
+        if key not in self._bufs:
+            m = self.m
+            rows = 16 * _mtiles(B)
+            F = m.W['fcw'].shape[2]
+            h16 = dict(dtype=torch.float16, device='cuda')
+            self._bufs[key] = dict(AF=torch.zeros(2 * rows * m.D, **h16), GF=torch.zeros(2 * rows * F, **h16))
+        return self._bufs[key]
+
+    def _frag(self, name):
+        """Weight ``name`` in the decode products' fragment order
+        ([L,] n-tile, k-step, lane, 8; see hip/prefill.hip), made on first use
+        and held. Layer weights are stored [L, in, out]; the output head
+        ``wte`` [V, d] is already [out, in] and gets zero rows up to a
+        multiple of 16."""
+        import torch
+        key = name + '__f'
+        if key not in self._own:
+            W = self.m.W[name]
+            if name == 'wte':
+                V, K = W.shape
+                Vp = -(-V // 16) * 16
+                Wt = torch.zeros(Vp, K, dtype=W.dtype, device=W.device)
+                Wt[:V] = W
+                f = Wt.reshape(Vp // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4)
+            else:
+                Lr, K, N = W.shape
+                f = W.transpose(1, 2).reshape(Lr, N // 16, 16, K // 32, 4, 8).permute(0, 1, 3, 4, 2, 5)
+            self._own[key] = f.contiguous()
+        return self._own[key]
+
+    def _mgemm(self, Af, K, wname, layer, N, mode, bias=None, out=None, ldo=0, F=None, ln=None, M=1):
+        """One decode product (``pf_mgemm*``) over M rows: A in fragment order
+        (Af), weights ``wname`` (layer ``layer``) in fragment order. With a
+        split fold the parts are added by a second launch: ``pf_reduce_ln``
+        for a residual product followed by the LayerNorm ``ln`` = (w, b, F_out)
+        (returns True: that LayerNorm is done), ``pf_reduce_frag`` for the
+        GELU product, ``pf_reduce`` otherwise."""
+        m = self.m
+        KT, NT = K // 32, -(-N // 16)
+        nb = -(-NT // MG_TILES)
+        ks = max(1, min(round(MG_BLOCKS / nb), KT // MG_MIN_STEPS))
+        ws = self._workspace(ks * M * N) if ks > 1 else None
+        Wf = self._frag(wname)
+        Wf = Wf[layer] if layer is not None else Wf
+        mt = _mtiles(M)
+        t_args = [_p(m.keys), _p(m.vals), _p(m.t), _i(layer or 0), _i(m.L), _i(m.tmax)]
+        self._launch(f'pf_mgemm{mt}', nb * ks,
+                     [_p(Af), _p(Wf), _i(KT), _i(NT), _i(ks), _p(bias), _i(M), _i(N), _i(mode), _p(out), _i(ldo)]
+                     + t_args + [_p(ws), _p(F), _p(self.err)], block=MG_WAVES * 64)
+        if ks == 1:
+            return False
+        if mode == MODE_RESID and ln is not None:
+            w, b, Fo = ln
+            self._launch('pf_reduce_ln', M, [_p(ws), _i(ks), _p(bias), _i(M), _i(N), _p(out), _p(w), _p(b), _p(None),
+                                             _p(Fo), _i(mt), _p(self.err)])
+            return True
+        if mode == MODE_GELU:
+            self._launch('pf_reduce_frag', -(-M * (N // 8) // BLOCK), [_p(ws), _i(ks), _p(bias), _i(M), _i(N), _p(F),
+                                                                       _i(mt), _p(self.err)])
+        else:
+            self._launch('pf_reduce', -(-M * N // BLOCK), [_p(ws), _i(ks), _p(bias), _i(M), _i(N), _i(mode), _p(out),
+                                                            _i(ldo), _p(m.keys), _p(m.vals), _i(1), _p(m.t),
+                                                            _i(layer or 0), _i(m.L), _i(m.tmax)])
+        return False
+
+    def _build_decode(self, buf, B, tok):
+        """One decode pass (one position per row, B <= DECODE_ROWS) on the
+        fragment-order products: LayerNorm and attention write their outputs
+        as the next product's fragment-order activations, the widening
+        product writes its GELU outputs as the narrowing one's."""
+        m = self.m
+        D, H, L = m.D, m.H, m.L
+        F = m.W['fcw'].shape[2]
+        V = m.W['wte'].shape[0]
+        W = m.W
+        mt = _mtiles(B)
+        Z, Q = buf['Z'], buf['Q']
+        fb = self._decode_buffers(B)
+        AF, GF = fb['AF'], fb['GF']
+        err = self.err
+        self._launch('pf_embed', B, [_p(tok), _i(1), _p(m.t), _p(W['wte']), _p(W['wpe']), _p(Z), _i(D), _i(V),
+                                     _i(W['wpe'].shape[0])])
+        self._launch('pf_ln', B, [_p(Z), _i(0), _i(1), _p(W['ln1w'][0]), _p(W['ln1b'][0]), _p(None), _i(D), _p(AF),
+                                  _i(mt), _p(err)])
+        for layer in range(L):
+            def lw(name, layer=layer):
+                return W[name][layer]
+            self._mgemm(AF, D, 'qkvw', layer, 3 * D, MODE_QKV, bias=lw('qkvb'), out=Q, ldo=D, M=B)
+            self._launch('pf_attn1', B * H, [_p(Q), _p(m.keys), _p(m.vals), _p(None), _p(m.t), _i(layer), _i(L),
+                                             _i(m.tmax), _i(H), _p(AF), _i(mt), _p(err)])
+            if not self._mgemm(AF, D, 'ow', layer, D, MODE_RESID, bias=lw('ob'), out=Z, ldo=D,
+                               ln=(lw('ln2w'), lw('ln2b'), AF), M=B):
+                self._launch('pf_ln', B, [_p(Z), _i(0), _i(1), _p(lw('ln2w')), _p(lw('ln2b')), _p(None), _i(D),
+                                          _p(AF), _i(mt), _p(err)])
+            self._mgemm(AF, D, 'fcw', layer, F, MODE_GELU, bias=lw('fcb'), F=GF, M=B)
+            nw, nb_ = (lw('ln1w', layer + 1), lw('ln1b', layer + 1)) if layer + 1 < L else (W['lnfw'], W['lnfb'])
+            if not self._mgemm(GF, F, 'pw', layer, D, MODE_RESID, bias=lw('pb'), out=Z, ldo=D, ln=(nw, nb_, AF),
+                               M=B):
+                self._launch('pf_ln', B, [_p(Z), _i(0), _i(1), _p(nw), _p(nb_), _p(None), _i(D), _p(AF), _i(mt),
+                                          _p(err)])
+        logit, nxt = m.logits(), m.next()
+        self._mgemm(AF, D, 'wte', None, V, MODE_PLAIN, out=logit, ldo=V, M=B)
+        self._launch('pf_argmax_part', B * ARGMAX_SPLIT, [_p(logit), _i(V), _i(ARGMAX_SPLIT), _p(buf['apv']),
+                                                           _p(buf['api'])])
+        self._launch('pf_argmax', B, [_p(buf['apv']), _p(buf['api']), _i(ARGMAX_SPLIT), _p(m.x), _p(nxt), _p(m.t),
+                                      _i(1)])
 
     def _transposed(self, name):
         """The weight copy ``name`` (``<w>__t``: [L, out, in]); the decode
@@ -164,7 +290,8 @@ class Prefill:
                                              _p(out), _i(ldo)] + tail + [_i(ks), _p(ws), _p(self.err)])
         if FUSE_REDUCE_LN and ks > 1 and ln is not None and mode == MODE_RESID and ldo == N:
             w, b, Y = ln
-            self._launch('pf_reduce_ln', M, [_p(ws), _i(ks), _p(bias), _i(M), _i(N), _p(out), _p(w), _p(b), _p(Y)])
+            self._launch('pf_reduce_ln', M, [_p(ws), _i(ks), _p(bias), _i(M), _i(N), _p(out), _p(w), _p(b), _p(Y),
+                                             _p(None), _i(0), _p(self.err)])
             return True
         if ks > 1:
             self._launch('pf_reduce', -(-M * N // BLOCK), [_p(ws), _i(ks), _p(bias), _i(M), _i(N), _i(mode),
@@ -197,8 +324,8 @@ class Prefill:
         import torch
         stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
         L = lib()
-        for name, fn, grid, a in plan:
-            ok(L.vh_launch(fn, grid, BLOCK, 0, stream, a.array), name)
+        for name, fn, grid, a, block in plan:
+            ok(L.vh_launch(fn, grid, block, 0, stream, a.array), name)
 
     def run(self, prompt):
         """Prefill ``prompt`` (int32 device tensor [B, P]) at positions t .. t + P - 1
@@ -251,6 +378,8 @@ class Prefill:
         return g
 
     def _build(self, buf, B, P, tok):
+        if P == 1 and B <= DECODE_ROWS and FRAG_DECODE:
+            return self._build_decode(buf, B, tok)
         m = self.m
         M, D, H, L = B * P, m.D, m.H, m.L
         F = m.W['fcw'].shape[2]
@@ -267,19 +396,21 @@ class Prefill:
             def lt(name):
                 return self._transposed(name)[layer]
             if not normed:
-                self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln1w')), _p(lw('ln1b')), _p(A), _i(D)])
+                self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln1w')), _p(lw('ln1b')), _p(A), _i(D),
+                                          _p(None), _i(0), _p(self.err)])
             self._gemm(A, D, lt('qkvw__t'), lw('qkvb'), M, 3 * D, D, MODE_QKV, Q, D, layer, P)
             if P == 1:      # a decode pass: a block per (row, head) (GPT-2 small, 32 rows, 1024
                             # positions: 1.32 -> 1.07 ms per step against a wave per (row, head))
                 self._launch('pf_attn1', M * H, [_p(Q), _p(m.keys), _p(m.vals), _p(A), _p(m.t), _i(layer), _i(L),
-                                                 _i(m.tmax), _i(H)])
+                                                 _i(m.tmax), _i(H), _p(None), _i(0), _p(self.err)])
             else:
                 self._launch('pf_attn', -(-M * H // (BLOCK // 64)),
                              [_p(Q), _p(m.keys), _p(m.vals), _p(A), _i(M), _i(P), _p(m.t), _i(layer), _i(L),
                               _i(m.tmax), _i(H)])
             if not self._gemm(A, D, lt('ow__t'), lw('ob'), M, D, D, MODE_RESID, Z, D,
                               ln=(lw('ln2w'), lw('ln2b'), A)):
-                self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln2w')), _p(lw('ln2b')), _p(A), _i(D)])
+                self._launch('pf_ln', M, [_p(Z), _i(0), _i(1), _p(lw('ln2w')), _p(lw('ln2b')), _p(A), _i(D),
+                                          _p(None), _i(0), _p(self.err)])
             self._gemm(A, D, lt('fcw__t'), lw('fcb'), M, F, D, MODE_GELU, G, F)
             if layer + 1 < L:
                 nxt = (lw('ln1w', layer + 1), lw('ln1b', layer + 1), A)
@@ -287,7 +418,8 @@ class Prefill:
                 nxt = (W['lnfw'], W['lnfb'], C) if P == 1 else None   # the final norm: each row's last position
             normed = self._gemm(G, F, lt('pw__t'), lw('pb'), M, D, F, MODE_RESID, Z, D, ln=nxt)
         if not normed:
-            self._launch('pf_ln', B, [_p(Z), _i(P - 1), _i(P), _p(W['lnfw']), _p(W['lnfb']), _p(C), _i(D)])
+            self._launch('pf_ln', B, [_p(Z), _i(P - 1), _i(P), _p(W['lnfw']), _p(W['lnfb']), _p(C), _i(D),
+                                      _p(None), _i(0), _p(self.err)])
         logit, nxt = m.logits(), m.next()
         self._gemm(C, D, W['wte'], None, B, V, D, MODE_PLAIN, logit, V)
         self._launch('pf_argmax_part', B * ARGMAX_SPLIT, [_p(logit), _i(V), _i(ARGMAX_SPLIT), _p(buf['apv']),
