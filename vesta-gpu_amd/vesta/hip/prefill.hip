@@ -76,12 +76,14 @@ extern "C" __global__ __launch_bounds__(256) void pf_ln(const float* __restrict_
   const float* x = X + (size_t)(row0 + (size_t)blockIdx.x * rstride) * D;
   float* y = Y + (size_t)blockIdx.x * D;
   const float fd = (float)D;
-  float v[8];
+  float v[8], wv[8], bv[8];
   float s = 0.0f;
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int i = threadIdx.x + j * 256;
     v[j] = i < D ? x[i] : 0.0f;
+    wv[j] = i < D ? h2f(w[i]) : 0.0f;
+    bv[j] = i < D ? h2f(b[i]) : 0.0f;
     if (i < D) s += v[j] / fd;
   }
   const float mean = block_red_sum(s, red);
@@ -98,14 +100,14 @@ extern "C" __global__ __launch_bounds__(256) void pf_ln(const float* __restrict_
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int i = threadIdx.x + j * 256;
-      if (i < D) y[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
+      if (i < D) y[i] = (v[j] - mean) / sd * wv[j] + bv[j];
     }
     return;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int i = threadIdx.x + j * 256;
-    if (i < D) out[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
+    if (i < D) out[i] = (v[j] - mean) / sd * wv[j] + bv[j];
   }
   __syncthreads();
   bool bad = false;
@@ -322,12 +324,18 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
   float* y = Y + (size_t)m * D;
   const float fd = (float)D;
   // the parts of the thread's 8 values, eight parts' loads in flight at once,
-  // added in part order
-  float v[8];
+  // added in part order; the residual row, bias and LayerNorm weights are
+  // loaded with the first parts
+  float v[8], zr[8], bn[8], wv[8], bv[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int i = threadIdx.x + j * 256;
-    v[j] = i < D ? ws[(size_t)m * D + i] : 0.0f;
+    const bool in = i < D;
+    v[j] = in ? ws[(size_t)m * D + i] : 0.0f;
+    zr[j] = in ? z[i] : 0.0f;
+    bn[j] = in && bias ? h2f(bias[i]) : 0.0f;
+    wv[j] = in ? h2f(w[i]) : 0.0f;
+    bv[j] = in ? h2f(b[i]) : 0.0f;
   }
   for (int k0 = 1; k0 < ksplit; k0 += 8) {
     float p[8][8];
@@ -349,8 +357,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
   for (int j = 0; j < 8; ++j) {
     const int i = threadIdx.x + j * 256;
     if (i < D) {
-      const float bn = bias ? h2f(bias[i]) : 0.0f;
-      v[j] = (z[i] + v[j]) + bn;
+      v[j] = (zr[j] + v[j]) + bn[j];
       z[i] = v[j];
       s += v[j] / fd;
     }
@@ -369,14 +376,14 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
       const int i = threadIdx.x + j * 256;
-      if (i < D) y[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
+      if (i < D) y[i] = (v[j] - mean) / sd * wv[j] + bv[j];
     }
     return;
   }
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     const int i = threadIdx.x + j * 256;
-    if (i < D) out[i] = (v[j] - mean) / sd * h2f(w[i]) + h2f(b[i]);
+    if (i < D) out[i] = (v[j] - mean) / sd * wv[j] + bv[j];
   }
   __syncthreads();
   bool bad = false;
@@ -389,8 +396,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
 // the weights streamed from memory straight into the matrix cores' registers,
 // the activations read as they are (hi and lo planes, each multiplied into
 // its own accumulator and combined at the end). A block is PF_MW waves on the
-// same PF_MN n-tiles (32 columns); block b takes n-tile pair b / ks and fold
-// part b % ks of ks, and its waves split that part's k-steps into PF_MW
+// same PF_MN n-tiles (32 columns); block vb takes n-tile pair vb / ks and fold
+// part vb % ks of ks, and its waves split that part's k-steps into PF_MW
 // consecutive runs, each wave keeping the next k-step's operands in flight
 // while it multiplies the current one. The waves' partial tiles are added in
 // LDS in wave order. Then either the part is stored (ks > 1: ws[part][m][n],
@@ -402,14 +409,14 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
 #define PF_MN 2
 template <int MT>
 __device__ __forceinline__ void pf_mgemm_body(
-    const vh_u32x4* __restrict__ Af, const vh_u32x4* __restrict__ Wf, int KT, int NT, int ks,
+    int vb, const vh_u32x4* __restrict__ Af, const vh_u32x4* __restrict__ Wf, int KT, int NT, int ks,
     const vh_half* __restrict__ bias, int M, int N, int mode, float* __restrict__ out, int ldo,
     vh_half* __restrict__ kc, vh_half* __restrict__ vc, const int* __restrict__ tp, int layer, int L, int tmax,
     float* __restrict__ ws, vh_half* __restrict__ F, unsigned* __restrict__ err) {
   __shared__ __attribute__((aligned(16))) vh_f32x4 red[PF_MW][PF_MN * MT * 64];
   __shared__ __attribute__((aligned(16))) float tile[16 * MT][16 * PF_MN + 4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int part = blockIdx.x % ks, nt0 = (blockIdx.x / ks) * PF_MN;
+  const int part = vb % ks, nt0 = (vb / ks) * PF_MN;
   const int ka = part * KT / ks, kb = (part + 1) * KT / ks;
   const int k0 = ka + (kb - ka) * wave / PF_MW, k1 = ka + (kb - ka) * (wave + 1) / PF_MW;
   vh_f32x4 acc[PF_MN][MT], acl[PF_MN][MT];
@@ -498,7 +505,8 @@ __device__ __forceinline__ void pf_mgemm_body(
       const vh_half* __restrict__ bias, int M, int N, int mode, float* __restrict__ out, int ldo,                 \
       vh_half* __restrict__ kc, vh_half* __restrict__ vc, const int* __restrict__ tp, int layer, int L, int tmax, \
       float* __restrict__ ws, vh_half* __restrict__ F, unsigned* __restrict__ err) {                              \
-    pf_mgemm_body<MT>(Af, Wf, KT, NT, ks, bias, M, N, mode, out, ldo, kc, vc, tp, layer, L, tmax, ws, F, err);   \
+    pf_mgemm_body<MT>(blockIdx.x, Af, Wf, KT, NT, ks, bias, M, N, mode, out, ldo, kc, vc, tp, layer, L, tmax, ws, \
+                      F, err);                                                                                    \
   }
 PF_MGEMM(pf_mgemm1, 1)
 PF_MGEMM(pf_mgemm2, 2)
