@@ -504,6 +504,40 @@ CONFIGS = {3: ('small', 32, 768, 256, 1024), 4: ('medium', 8, 256, 256, 512), '4
            5: ('xl', 64, 128, 128, 256)}
 
 
+def engines_line(shapes, steps=64, warmup=8, seed=0):
+    """Both decode engines forced at each shape (model, rows, prompt, cache):
+    ms per step of ``steps`` steps in one call after the batched prefill and
+    ``warmup`` steps (the data behind ``gpt2.LAYERED_ROWS``)."""
+    import torch
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import RandomGPT2, random_prompts
+    out = []
+    for model, B, P, tmax in shapes:
+        hf = RandomGPT2(model, seed)
+        prompts = torch.from_numpy(random_prompts(B, P, 50257, seed=1)).to('cuda', torch.int32)
+        row = dict(model=model, rows=B, prompt=P, tmax=tmax)
+        for engine in ('persistent', 'layered'):
+            try:
+                m = VestaGPT2(hf, batch=B, tmax=tmax, engine=engine)
+            except (RuntimeError, ValueError) as e:
+                row[engine] = f'does not fit: {e}'[:120]
+                continue
+            m.reset()
+            m.prefill(prompts)
+            m.step(warmup)
+            toks = torch.zeros(steps * B, dtype=torch.int32, device='cuda')
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            m.step(steps, toks)
+            torch.cuda.synchronize()
+            row[engine] = round((time.perf_counter() - t0) / steps * 1e3, 3)
+            m.check()
+            del m
+            torch.cuda.empty_cache()
+        out.append(row)
+    return dict(metric='decode ms per step, both engines forced', unit='ms', rows=out)
+
+
 def config_line(key, steps=None, warmup=8, chunk=32, seed=0):
     """Greedy decode throughput of one of BASELINE.json's other configurations
     (random-init weights of that model, uniform-random prompts fed by the
@@ -626,7 +660,14 @@ def main():
     ap.add_argument('--config', default='', metavar='KEY',
                     help='instead of the benchmark line, measure decode of another configuration: 3 (small, '
                          'B=32, 768-token prompts), 4 / 4b1 (medium, B=8 / B=1), 5 (XL, B=64)')
+    ap.add_argument('--engines', default='', metavar='MODEL:B:P:T,...',
+                    help='instead of the benchmark line, time both decode engines forced at these shapes '
+                         '(model, rows, prompt length, cache positions), e.g. small:16:128:448')
     args = ap.parse_args()
+    if args.engines:
+        shapes = [(m, int(b), int(p), int(t)) for m, b, p, t in (x.split(':') for x in args.engines.split(',') if x)]
+        print(json.dumps(engines_line(shapes, args.steps if '--steps' in sys.argv else 64, args.warmup)), flush=True)
+        return
     if args.config:
         key = int(args.config) if args.config.isdigit() else args.config
         if key not in CONFIGS:

@@ -31,9 +31,10 @@ from .lower import lower
 
 LDS_PER_CU = 160 * 1024      # bytes of LDS one block of the persistent kernel may use
 SPILLS_LAYERED = 64          # spilled registers beyond which 'auto' takes the layered engine
-LAYERED_ROWS = 32            # rows from which 'auto' takes the layered engine (GPT-2 small, 32 rows,
-                             # 1024-position cache: 1.39 ms per step layered, 1.50 persistent; 16 rows:
-                             # 0.93 layered, 0.58 persistent)
+LAYERED_ROWS = {768: 12}      # rows from which 'auto' takes the layered engine, by model width (same box, ms
+LAYERED_ROWS_OTHER = 32       # per step, persistent / layered: GPT-2 small 8 rows 0.291 / 0.499, 12 rows
+                              # 0.563 / 0.504, 16 rows 0.620 / 0.519, 32 rows with a 1024-position cache 1.549 /
+                              # 0.790; medium 8 rows 0.859 / 1.287, 16 rows 1.233 / 1.326)
 
 SHAPE_PROGRAMS = {(12, 768, 12): 'gpt2.vst', (24, 1024, 16): 'gpt2_medium.vst', (48, 1600, 25): 'gpt2_xl.vst'}
 
@@ -76,7 +77,8 @@ class VestaGPT2:
         per launch (the reference design); 'layered' runs each step as a
         sequence of ordinary per-layer launches (``vesta.prefill``: the
         multi-token prefill kernels with one position per row); 'auto' takes
-        the layered engine from ``LAYERED_ROWS`` rows (where it is faster) and
+        the layered engine from ``LAYERED_ROWS[d]`` rows (``LAYERED_ROWS_OTHER``
+        for widths not listed; where it is faster) and
         the persistent kernel below, unless that does not fit the device (LDS
         beyond a CU's 160 KB, or more than ``SPILLS_LAYERED`` spilled
         registers), as for GPT-2 XL at 64 rows. With the layered engine ``low`` and ``k``
@@ -120,8 +122,8 @@ class VestaGPT2:
         from .prefill import supported
         if engine == 'layered':
             self.why_layered = 'asked for'
-        elif engine == 'auto' and batch >= LAYERED_ROWS and supported(D, H, F):
-            self.why_layered = f'{batch} rows (layered is faster from {LAYERED_ROWS} rows)'
+        elif engine == 'auto' and batch >= (rows := LAYERED_ROWS.get(D, LAYERED_ROWS_OTHER)) and supported(D, H, F):
+            self.why_layered = f'{batch} rows (layered is faster from {rows} rows)'
         else:
             self.why_layered = self._persistent(text, spec, batch, timing, blocks_per_sm, strict=engine == 'persistent')
         if self.k is None:
