@@ -57,6 +57,30 @@ def _mtiles(rows: int) -> int:
     return 1 if t <= 1 else 2 if t == 2 else 4
 
 
+def frag_weights(Wt):
+    """Weights [.., N, K] (row n: output n's K weights) in the decode
+    products' fragment order [.., N/16, K/32, 64, 8]: element (n, k) at
+    n-tile n // 16, k-step k // 32, lane 16 * ((k % 32) // 8) + n % 16,
+    position k % 8 (the B operand of v_mfma_f32_16x16x32_f16 as a lane
+    holds it). N is padded with zero rows to a multiple of 16."""
+    import torch
+    *lead, N, K = Wt.shape
+    Np = -(-N // 16) * 16
+    if Np != N:
+        Wt = torch.cat([Wt, Wt.new_zeros(*lead, Np - N, K)], dim=-2)
+    f = Wt.reshape(*lead, Np // 16, 16, K // 32, 4, 8)
+    n = len(lead)
+    return f.permute(*range(n), n, n + 2, n + 3, n + 1, n + 4).reshape(*lead, Np // 16, K // 32, 64, 8)
+
+
+def frag_offset(M16: int, K: int, plane: int, m: int, k: int) -> int:
+    """Half index of activation element (m, k) in fragment order (the
+    layout pf_frag_put8 writes: plane, m-tile, k-step, lane, 8; M16 rows in
+    16-row tiles)."""
+    MT, KT = M16 // 16, K // 32
+    return (((plane * MT + m // 16) * KT + k // 32) * 64 + ((k % 32) // 8) * 16 + m % 16) * 8 + k % 8
+
+
 def prefill_source(tmax: int) -> str:
     return (f'#define VBLOCK {BLOCK}\n#define PF_TMAX {tmax}\n' + PRELUDE_SRC.read_text() + '\n'
             + PREFILL_SRC.read_text())
@@ -171,20 +195,10 @@ class Prefill:
         and held. Layer weights are stored [L, in, out]; the output head
         ``wte`` [V, d] is already [out, in] and gets zero rows up to a
         multiple of 16."""
-        import torch
         key = name + '__f'
         if key not in self._own:
             W = self.m.W[name]
-            if name == 'wte':
-                V, K = W.shape
-                Vp = -(-V // 16) * 16
-                Wt = torch.zeros(Vp, K, dtype=W.dtype, device=W.device)
-                Wt[:V] = W
-                f = Wt.reshape(Vp // 16, 16, K // 32, 4, 8).permute(0, 2, 3, 1, 4)
-            else:
-                Lr, K, N = W.shape
-                f = W.transpose(1, 2).reshape(Lr, N // 16, 16, K // 32, 4, 8).permute(0, 1, 3, 4, 2, 5)
-            self._own[key] = f.contiguous()
+            self._own[key] = frag_weights(W) if name == 'wte' else frag_weights(W.transpose(1, 2))
         return self._own[key]
 
     def _mgemm(self, Af, K, wname, layer, N, mode, bias=None, out=None, ldo=0, F=None, ln=None, M=1):
@@ -202,6 +216,15 @@ class Prefill:
         Wf = self._frag(wname)
         Wf = Wf[layer] if layer is not None else Wf
         mt = _mtiles(M)
+        # the extents pf_mgemm* indexes, checked before the launch is recorded
+        if K % 32 or M > 16 * mt or mt > 4:
+            raise ValueError(f'decode product: K={K} must be a multiple of 32 and M={M} at most 64')
+        if Af.numel() < 2 * 16 * mt * K or Wf.numel() < NT * KT * 512:
+            raise ValueError(f'decode product {wname}: operands smaller than {M}x{K} activations / {N}x{K} weights')
+        if mode == MODE_GELU and (N % 32 or F is None or F.numel() < 2 * 16 * mt * N):
+            raise ValueError(f'decode product {wname}: GELU output needs a fragment buffer of {M}x{N}, N % 32 == 0')
+        if mode in (MODE_PLAIN, MODE_RESID, MODE_QKV) and out.numel() < M * ldo:
+            raise ValueError(f'decode product {wname}: output smaller than {M} rows of {ldo}')
         t_args = [_p(m.keys), _p(m.vals), _p(m.t), _i(layer or 0), _i(m.L), _i(m.tmax)]
         self._launch(f'pf_mgemm{mt}', nb * ks,
                      [_p(Af), _p(Wf), _i(KT), _i(NT), _i(ks), _p(bias), _i(M), _i(N), _i(mode), _p(out), _i(ldo)]
