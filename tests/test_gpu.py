@@ -26,6 +26,18 @@ def _torch():
     return torch
 
 
+def _tokens_match(label, got, want, margins, err):
+    """Greedy tokens against the oracle's: a token may differ only at a step
+    whose oracle top-2 margin is below twice the measured logit error `err`
+    (a near-tie the tolerance itself allows); prints how many were waived."""
+    got, want, margins = np.asarray(got), np.asarray(want), np.asarray(margins)
+    diff = [k for k in range(len(want)) if got[k] != want[k]]
+    waived = [(k, float(margins[k])) for k in diff if margins[k] < 2 * err]
+    bad = [(k, float(margins[k])) for k in diff if margins[k] >= 2 * err]
+    print(f'{label}: {len(want)} tokens, logit error {err:.2e}, {len(waived)} near-tie steps waived {waived}')
+    assert not bad, f'{label}: tokens differ from the oracle at (step, margin) {bad}'
+
+
 @pytest.fixture(scope='module')
 def small():
     from oracle import decode
@@ -109,8 +121,9 @@ def test_local_checkpoint_matches_oracle(tmp_path):
     text = gpt2_program(2, 16, 4, 64, 37, 'tiny')
     for r in range(2):
         onx, olog, marg = decode.teacher_forced(text, W, ins[:, r], 16)
-        assert np.abs(lg[:, r] - olog).max() < 1e-3, r
-        assert all(a == b or mg < 1e-3 for a, b, mg in zip(nx[:, r], onx, marg)), r
+        err = np.abs(lg[:, r] - olog).max()
+        assert err < 1e-3, r
+        _tokens_match(f'local checkpoint row {r}', nx[:, r], onx, marg, err)
 
 
 def test_batch8_rows_match_oracle(small):
@@ -125,8 +138,9 @@ def test_batch8_rows_match_oracle(small):
     ins, lg, nx = _run_steps(m, [pr[:, i] for i in range(P)], P + G - 1)
     for r in (0, 5):
         onx, olog, marg = decode.teacher_forced(text, W, ins[:, r], 64)
-        assert np.abs(lg[:, r] - olog).max() < LOGIT_TOL, r
-        assert (nx[:, r] == onx).all() or all(mg < 1e-3 for a, b, mg in zip(nx[:, r], onx, marg) if a != b)
+        err = np.abs(lg[:, r] - olog).max()
+        assert err < LOGIT_TOL, r
+        _tokens_match(f'B=8 row {r}', nx[:, r], onx, marg, err)
 
 
 @pytest.mark.parametrize('B', [4, 8])
@@ -156,10 +170,9 @@ def test_matrix_core_rows_long_context_match_oracle(small, B):
     for r in range(B):
         inputs = np.concatenate([pr[r], gen[:-1, r]])                             # what step i saw
         onx, olog, marg = decode.teacher_forced(text, W, inputs, T)
-        assert np.abs(last[r] - olog[-1]).max() < LOGIT_TOL, r
-        want = onx[P - 1:]
-        bad = [k for k in range(G) if gen[k, r] != want[k] and marg[P - 1 + k] >= 1e-3]
-        assert not bad, (r, bad)
+        err = np.abs(last[r] - olog[-1]).max()
+        assert err < LOGIT_TOL, r
+        _tokens_match(f'B={B} long context row {r}', gen[:, r], onx[P - 1:], marg[P - 1:], err)
 
 
 def _prefill_and_generate(m, pr, G):
@@ -183,9 +196,9 @@ def _check_rows(text, W, pr, gen, last, T, rows):
     for r in rows:
         inputs = np.concatenate([pr[r], gen[:-1, r]])
         onx, olog, marg = decode.teacher_forced(text, W, inputs, T)
-        assert np.abs(last[r] - olog[-1]).max() < LOGIT_TOL, r
-        bad = [k for k in range(G) if gen[k, r] != onx[P - 1 + k] and marg[P - 1 + k] >= 1e-3]
-        assert not bad, (r, bad)
+        err = np.abs(last[r] - olog[-1]).max()
+        assert err < LOGIT_TOL, r
+        _tokens_match(f'row {r}', gen[:, r], onx[P - 1:P - 1 + G], marg[P - 1:P - 1 + G], err)
 
 
 @pytest.mark.slow
@@ -337,10 +350,10 @@ def test_batched_prefill_matches_oracle_and_continues(small):
         seq = np.concatenate([pr[r], [ins[k][r] for k in range(G)]])
         onx, olog, marg = decode.teacher_forced(text, W, seq, 32)
         got = np.stack([lg[k][r] for k in range(G + 1)])
-        assert np.abs(got - olog[P1 + P2 - 1:]).max() < LOGIT_TOL, r
+        err = np.abs(got - olog[P1 + P2 - 1:]).max()
+        assert err < LOGIT_TOL, r
         nxt = np.array([ins[k][r] for k in range(G + 1)])
-        want = onx[P1 + P2 - 1:]
-        assert all(a == b or mg < 1e-3 for a, b, mg in zip(nxt, want, marg[P1 + P2 - 1:])), r
+        _tokens_match(f'prefill continued row {r}', nxt, onx[P1 + P2 - 1:], marg[P1 + P2 - 1:], err)
         keys = m.keys[r].float().cpu().numpy()
         row = decode.Row(text, W, 32)
         for i, tok in enumerate(seq[:P1 + P2]):
@@ -445,9 +458,10 @@ def test_xl_widths_match_oracle(B, engine):
         seq = np.concatenate([pr[r], [ins[k][r] for k in range(G)]])
         onx, olog, marg = decode.teacher_forced(text, W, seq, 16)
         got = np.stack([lg[k][r] for k in range(G + 1)])
-        assert np.abs(got - olog[P - 1:]).max() < LOGIT_TOL, r
+        err = np.abs(got - olog[P - 1:]).max()
+        assert err < LOGIT_TOL, r
         nxt = np.array([ins[k][r] for k in range(G + 1)])
-        assert all(a == b or mg < 1e-3 for a, b, mg in zip(nxt, onx[P - 1:], marg[P - 1:])), r
+        _tokens_match(f'XL widths B={B} row {r}', nxt, onx[P - 1:], marg[P - 1:], err)
 
 
 def _grammar_cases():
