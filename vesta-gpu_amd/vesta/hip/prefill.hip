@@ -632,11 +632,14 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restric
 
 // One position per row (a decode step): one block per (row m, head h), every
 // thread of the block on the positions 0 .. t0, so that a step's cache rows
-// are read with a block's worth of loads in flight instead of a wave's. The
-// same arithmetic as pf_attn: each score a dot over e in order, / 8; the
-// max-subtracted softmax (block-wide maximum and sum); the weighted values
-// with wave w, lane 8a + b on positions s = 8w + a (mod 32), dims 8b..8b+7,
-// the four waves' partial outputs added in order through LDS.
+// are read with a block's worth of loads in flight instead of a wave's. Each
+// score is read by eight lanes, one 16-byte piece of the position's key row
+// each (so a wave's load covers eight whole rows), the eight partial dots
+// added across the lanes, / 8; the max-subtracted softmax (block-wide maximum
+// and sum); the weighted values with wave w, lane 8a + b on positions
+// s = 8w + a (mod 32), dims 8b..8b+7, the four waves' partial outputs added
+// in order through LDS. (Keys read a row per lane, eight 16-byte loads of it,
+// measured slower: XL B=64 decode 4.32 against 4.06 ms per step.)
 extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restrict__ Q, const vh_half* __restrict__ kc,
                                                             const vh_half* __restrict__ vc, float* __restrict__ O,
                                                             const int* __restrict__ tp, int layer, int L, int tmax,
@@ -652,23 +655,44 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restri
   const int at = *tp;
   const int pos = at < tmax ? at : tmax - 1;
   const size_t base = (size_t)(m * L + layer) * tmax * D + (size_t)h * PF_E;
-  if (tid < PF_E) qs[tid] = Q[(size_t)m * D + h * PF_E + tid];
-  __syncthreads();
-  float mx = -INFINITY;
-  for (int s = tid; s <= pos; s += VBLOCK) {
-    const vh_half* kr = kc + base + (size_t)s * D;
-    float acc = 0.0f;
-#pragma unroll
-    for (int e = 0; e < PF_E; e += 8) {
-      float kv[8];
-      unpack8(ld16(kr + e), kv);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc = fmaf(qs[e + j], kv[j], acc);
-    }
-    const float sc = acc * 0.125f;      // / 8, exact
-    ws[s] = sc;
-    mx = fmaxf(mx, sc);
+  // scores: eight lanes per position (lane 8g + b holds dims 8b .. 8b + 7, one
+  // 16-byte load), positions g, g + 32, .. of the block's 32 lane groups, four
+  // in flight per lane; the eight partial dots added across the group
+  const int g = tid >> 3, b8 = tid & 7;
+  float qv[8];
+  {
+    const float* qp = Q + (size_t)m * D + h * PF_E + 8 * b8;
+    const vh_f32x4 q0 = *(const vh_f32x4*)qp, q1 = *(const vh_f32x4*)(qp + 4);
+    qv[0] = q0[0]; qv[1] = q0[1]; qv[2] = q0[2]; qv[3] = q0[3];
+    qv[4] = q1[0]; qv[5] = q1[1]; qv[6] = q1[2]; qv[7] = q1[3];
   }
+  float mx = -INFINITY;
+  for (int s0 = g; s0 <= pos; s0 += 32 * 4) {
+    vh_u32x4 kr[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = s0 + 32 * u;
+      kr[u] = s <= pos ? ld16(kc + base + (size_t)s * D + 8 * b8) : vh_u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float kv[8];
+      unpack8(kr[u], kv);
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fmaf(qv[j], kv[j], acc);
+      acc += __shfl_xor(acc, 1, 64);
+      acc += __shfl_xor(acc, 2, 64);
+      acc += __shfl_xor(acc, 4, 64);
+      const int s = s0 + 32 * u;
+      if (s <= pos) {
+        const float sc = acc * 0.125f;      // / 8, exact
+        if (b8 == 0) ws[s] = sc;
+        mx = fmaxf(mx, sc);
+      }
+    }
+  }
+  __syncthreads();                      // ws written by the groups' first lanes, read by all below
   mx = wave_red_max(mx);
   if (lane == 0) red[wave] = mx;
   __syncthreads();
