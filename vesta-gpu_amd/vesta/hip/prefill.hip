@@ -540,7 +540,9 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_frag(const float* __
 
 // ---------------------------------------------------------------- attention
 // One wave per (row m, head h): scores of the query against cache positions
-// 0 .. t0 + p (gpt2.vst Q5: dot over e, divided by 8; a lane per position),
+// 0 .. t0 + p (gpt2.vst Q5: dot over e, divided by 8; eight lanes per
+// position, each a 16-byte piece of the key row, the partial dots added
+// across them),
 // the max-subtracted softmax (Q6), and the weighted values (Q7: eight lanes
 // per position, 8 dims each), read from the fp16 cache the qkv product just
 // wrote. O[m, h * 64 + e] receives the head's output.
@@ -549,7 +551,6 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restric
                                                            const vh_half* __restrict__ vc, float* __restrict__ O,
                                                            int M, int P, const int* __restrict__ tp, int layer,
                                                            int L, int tmax, int H) {
-  __shared__ float qs[VNWAVE][PF_E];
   __shared__ float ws[VNWAVE][PF_TMAX];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
   const int item = blockIdx.x * VNWAVE + wave;
@@ -559,23 +560,44 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn(const float* __restric
   const int b = m / P, at = *tp + m % P;
   const int pos = at < tmax ? at : tmax - 1;
   const size_t base = (size_t)(b * L + layer) * tmax * D + (size_t)h * PF_E;
-  if (live) qs[wave][lane] = Q[(size_t)m * D + h * PF_E + lane];
-  vh_lds_sync();
+  // scores: eight lanes per position (lane 8g + c holds dims 8c .. 8c + 7,
+  // one 16-byte load), positions g, g + 8, .. of the wave's 8 lane groups,
+  // four in flight per lane; the eight partial dots added across the group
+  const int g = lane >> 3, c8 = lane & 7;
+  float qv[8];
+  {
+    const float* qp = Q + (size_t)m * D + h * PF_E + 8 * c8;
+    const vh_f32x4 q0 = live ? *(const vh_f32x4*)qp : vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    const vh_f32x4 q1 = live ? *(const vh_f32x4*)(qp + 4) : vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    qv[0] = q0[0]; qv[1] = q0[1]; qv[2] = q0[2]; qv[3] = q0[3];
+    qv[4] = q1[0]; qv[5] = q1[1]; qv[6] = q1[2]; qv[7] = q1[3];
+  }
   float mx = -INFINITY;
   if (live) {
-    for (int s = lane; s <= pos; s += 64) {
-      const vh_half* kr = kc + base + (size_t)s * D;
-      float acc = 0.0f;
+    for (int s0 = g; s0 <= pos; s0 += 8 * 4) {
+      vh_u32x4 kr[4];
 #pragma unroll
-      for (int e = 0; e < PF_E; e += 8) {
-        float kv[8];
-        unpack8(ld16(kr + e), kv);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc = fmaf(qs[wave][e + j], kv[j], acc);
+      for (int u = 0; u < 4; ++u) {
+        const int s = s0 + 8 * u;
+        kr[u] = s <= pos ? ld16(kc + base + (size_t)s * D + 8 * c8) : vh_u32x4{0u, 0u, 0u, 0u};
       }
-      const float sc = acc * 0.125f;      // / 8, exact
-      ws[wave][s] = sc;
-      mx = fmaxf(mx, sc);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float kv[8];
+        unpack8(kr[u], kv);
+        float acc = 0.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc = fmaf(qv[j], kv[j], acc);
+        acc += __shfl_xor(acc, 1, 64);
+        acc += __shfl_xor(acc, 2, 64);
+        acc += __shfl_xor(acc, 4, 64);
+        const int s = s0 + 8 * u;
+        if (s <= pos) {
+          const float sc = acc * 0.125f;      // / 8, exact
+          if (c8 == 0) ws[wave][s] = sc;
+          mx = fmaxf(mx, sc);
+        }
+      }
     }
   }
   mx = wave_red_max(mx);
