@@ -24,19 +24,25 @@
 
 // ---------------------------------------------------------------- embedding
 // Z[m] = wte[tok[m]] + wpe[t0 + p]   (gpt2.vst Q1; ids and positions
-// clamped into their tables). One block per row.
+// clamped into their tables). One block per row, thread t on the eight
+// consecutive values 8t .. 8t + 7 (D <= 8 * 256).
 extern "C" __global__ __launch_bounds__(256) void pf_embed(const int* __restrict__ tok, int P,
                                                             const int* __restrict__ tp,
                                                             const vh_half* __restrict__ wte,
                                                             const vh_half* __restrict__ wpe, float* __restrict__ Z,
                                                             int D, int V, int npos) {
-  const int m = blockIdx.x;
+  const int m = blockIdx.x, k8 = 8 * threadIdx.x;
   int x = tok[m];
   x = x < 0 ? 0 : (x >= V ? V - 1 : x);
   int pos = *tp + m % P;
   pos = pos < 0 ? 0 : (pos >= npos ? npos - 1 : pos);
-  for (int i = threadIdx.x; i < D; i += blockDim.x)
-    Z[(size_t)m * D + i] = h2f(wte[(size_t)x * D + i]) + h2f(wpe[(size_t)pos * D + i]);
+  if (k8 >= D) return;
+  float a[8], b[8];
+  unpack8(ld16(wte + (size_t)x * D + k8), a);
+  unpack8(ld16(wpe + (size_t)pos * D + k8), b);
+  float* z = Z + (size_t)m * D + k8;
+  *(vh_f32x4*)z = vh_f32x4{a[0] + b[0], a[1] + b[1], a[2] + b[2], a[3] + b[3]};
+  *(vh_f32x4*)(z + 4) = vh_f32x4{a[4] + b[4], a[5] + b[5], a[6] + b[6], a[7] + b[7]};
 }
 
 // ---------------------------------------------------------------- fragment order
@@ -60,59 +66,6 @@ __device__ __forceinline__ void pf_frag_put8(vh_half* __restrict__ F, int MT, in
   const size_t at = (((size_t)(m >> 4) * KT + (k8 >> 5)) * 64 + ((k8 >> 3) & 3) * 16 + (m & 15)) * 8;
   *(vh_u32x4*)(F + at) = hi;
   *(vh_u32x4*)(F + (size_t)MT * KT * 512 + at) = lo;
-}
-
-// ---------------------------------------------------------------- layer norm
-// Y[i] = (X[r] - mean) / sqrt(var + 1e-5) * w + b for r = row0 + i * rstride
-// (biased variance; mean and variance as sums of x / D and (x - mean)^2 / D,
-// as gpt2.vst Q2 writes them). One block per output row; D <= 8 * 256. With
-// F set the row goes to F in fragment order (MT m-tiles) instead of Y.
-extern "C" __global__ __launch_bounds__(256) void pf_ln(const float* __restrict__ X, int row0, int rstride,
-                                                         const vh_half* __restrict__ w, const vh_half* __restrict__ b,
-                                                         float* __restrict__ Y, int D, vh_half* __restrict__ F, int MT,
-                                                         unsigned* __restrict__ err) {
-  __shared__ float red[VNWAVE];
-  __shared__ __attribute__((aligned(16))) float out[8 * 256];
-  const float* x = X + (size_t)(row0 + (size_t)blockIdx.x * rstride) * D;
-  float* y = Y + (size_t)blockIdx.x * D;
-  const float fd = (float)D;
-  float v[8], wv[8], bv[8];
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = threadIdx.x + j * 256;
-    v[j] = i < D ? x[i] : 0.0f;
-    wv[j] = i < D ? h2f(w[i]) : 0.0f;
-    bv[j] = i < D ? h2f(b[i]) : 0.0f;
-    if (i < D) s += v[j] / fd;
-  }
-  const float mean = block_red_sum(s, red);
-  float q = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = threadIdx.x + j * 256;
-    if (i < D) q += (v[j] - mean) * (v[j] - mean) / fd;
-  }
-  vh_lds_sync();
-  const float var = block_red_sum(q, red);
-  const float sd = sqrtf(var + 0.00001f);
-  if (F == nullptr) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = threadIdx.x + j * 256;
-      if (i < D) y[i] = (v[j] - mean) / sd * wv[j] + bv[j];
-    }
-    return;
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = threadIdx.x + j * 256;
-    if (i < D) out[i] = (v[j] - mean) / sd * wv[j] + bv[j];
-  }
-  __syncthreads();
-  bool bad = false;
-  if (8 * (int)threadIdx.x < D) pf_frag_put8(F, MT, D / 32, blockIdx.x, 8 * threadIdx.x, out + 8 * threadIdx.x, bad);
-  if (bad) stc_u(err, VH_ERR_RANGE);
 }
 
 // ---------------------------------------------------------------- products
@@ -307,88 +260,103 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce(
   pf_epi(mode, m, n, c, bias, N, out, ldo, kc, vc, P, tp, layer, L, tmax);
 }
 
-// A split residual product's parts added (pf_reduce, mode 1: Z[m, n] =
-// (Z[m, n] + C) + bias[n]) and the LayerNorm that reads Z next (pf_ln into
-// Y), in one launch: one block per row, the row kept in registers between
-// the two. The same sums in the same order as the two launches it replaces,
-// so the same bits. With F set the normalised row goes to F in fragment order
-// (MT m-tiles) instead of Y.
+// ---------------------------------------------------------------- layer norm
+// Y[i] = (X[r] - mean) / sqrt(var + 1e-5) * w + b for r = row0 + i * rstride
+// (biased variance; mean and variance as sums of x / D and (x - mean)^2 / D,
+// as gpt2.vst Q2 writes them): one block per output row, D <= 8 * 256,
+// thread t holding the row's eight consecutive values 8t .. 8t + 7 (16-byte
+// loads, so a wave's load is a whole kilobyte of the row), summed per thread,
+// then over the block. With F set the row goes to F in fragment order (MT
+// m-tiles: the thread writes its own piece) instead of Y. (Thread t on values
+// t, t + 256, .., one 4-byte load each, measured slower: XL B=64 decode 4.06
+// against 3.41 ms per step with the reduction below written that way.)
+__device__ __forceinline__ void pf_ld8f(const float* p, float* v) {
+  const vh_f32x4 a = *(const vh_f32x4*)p, b = *(const vh_f32x4*)(p + 4);
+  v[0] = a[0]; v[1] = a[1]; v[2] = a[2]; v[3] = a[3]; v[4] = b[0]; v[5] = b[1]; v[6] = b[2]; v[7] = b[3];
+}
+__device__ __forceinline__ void pf_norm8_out(const float* v, const float* wv, const float* bv, bool in, int D, int i,
+                                             float* __restrict__ Y, vh_half* __restrict__ F, int MT,
+                                             unsigned* __restrict__ err, float* red) {
+  const float fd = (float)D;
+  float s = 0.0f;
+  if (in)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) s += v[j] / fd;
+  const float mean = block_red_sum(s, red);
+  float q = 0.0f;
+  if (in)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) q += (v[j] - mean) * (v[j] - mean) / fd;
+  vh_lds_sync();
+  const float sd = sqrtf(block_red_sum(q, red) + 0.00001f);
+  if (!in) return;
+  float y[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = (v[j] - mean) / sd * wv[j] + bv[j];
+  const int k8 = 8 * threadIdx.x;
+  if (F == nullptr) {
+    float* yp = Y + (size_t)i * D + k8;
+    *(vh_f32x4*)yp = vh_f32x4{y[0], y[1], y[2], y[3]};
+    *(vh_f32x4*)(yp + 4) = vh_f32x4{y[4], y[5], y[6], y[7]};
+    return;
+  }
+  bool bad = false;
+  pf_frag_put8(F, MT, D / 32, i, k8, y, bad);
+  if (bad) stc_u(err, VH_ERR_RANGE);
+}
+
+extern "C" __global__ __launch_bounds__(256) void pf_ln(const float* __restrict__ X, int row0, int rstride,
+                                                         const vh_half* __restrict__ w, const vh_half* __restrict__ b,
+                                                         float* __restrict__ Y, int D, vh_half* __restrict__ F, int MT,
+                                                         unsigned* __restrict__ err) {
+  __shared__ float red[VNWAVE];
+  const int k8 = 8 * threadIdx.x;
+  const bool in = k8 < D;
+  float v[8] = {}, wv[8] = {}, bv[8] = {};
+  if (in) {
+    pf_ld8f(X + (size_t)(row0 + (size_t)blockIdx.x * rstride) * D + k8, v);
+    unpack8(ld16(w + k8), wv);
+    unpack8(ld16(b + k8), bv);
+  }
+  pf_norm8_out(v, wv, bv, in, D, blockIdx.x, Y, F, MT, err, red);
+}
+
+// A split residual product's parts added in part order (pf_reduce, mode 1:
+// Z[m, n] = (Z[m, n] + C) + bias[n]) and the LayerNorm that reads Z next (as
+// pf_ln, into Y or F), in one launch: one block per row, the row kept in
+// registers between the two.
 extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
     const float* __restrict__ ws, int ksplit, const vh_half* __restrict__ bias, int M, int D,
     float* __restrict__ Z, const vh_half* __restrict__ w, const vh_half* __restrict__ b, float* __restrict__ Y,
     vh_half* __restrict__ F, int MT, unsigned* __restrict__ err) {
   __shared__ float red[VNWAVE];
-  __shared__ __attribute__((aligned(16))) float out[8 * 256];
-  const int m = blockIdx.x;
-  float* z = Z + (size_t)m * D;
-  float* y = Y + (size_t)m * D;
-  const float fd = (float)D;
-  // the parts of the thread's 8 values, eight parts' loads in flight at once,
-  // added in part order; the residual row, bias and LayerNorm weights are
-  // loaded with the first parts
-  float v[8], zr[8], bn[8], wv[8], bv[8];
+  const int m = blockIdx.x, k8 = 8 * threadIdx.x;
+  const bool in = k8 < D;
+  float v[8] = {}, zr[8] = {}, bn[8] = {}, wv[8] = {}, bv[8] = {};
+  if (in) {
+    pf_ld8f(ws + (size_t)m * D + k8, v);
+    pf_ld8f(Z + (size_t)m * D + k8, zr);
+    if (bias) unpack8(ld16(bias + k8), bn);
+    unpack8(ld16(w + k8), wv);
+    unpack8(ld16(b + k8), bv);
+    for (int k0 = 1; k0 < ksplit; k0 += 4) {      // four parts' loads in flight, added in part order
+      float p[4][8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = threadIdx.x + j * 256;
-    const bool in = i < D;
-    v[j] = in ? ws[(size_t)m * D + i] : 0.0f;
-    zr[j] = in ? z[i] : 0.0f;
-    bn[j] = in && bias ? h2f(bias[i]) : 0.0f;
-    wv[j] = in ? h2f(w[i]) : 0.0f;
-    bv[j] = in ? h2f(b[i]) : 0.0f;
-  }
-  for (int k0 = 1; k0 < ksplit; k0 += 8) {
-    float p[8][8];
+      for (int u = 0; u < 4; ++u)
+        if (k0 + u < ksplit) pf_ld8f(ws + ((size_t)(k0 + u) * M + m) * D + k8, p[u]);
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+      for (int u = 0; u < 4; ++u)
+        if (k0 + u < ksplit)
 #pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        const int i = threadIdx.x + j * 256;
-        p[u][j] = (k0 + u < ksplit && i < D) ? ws[((size_t)(k0 + u) * M + m) * D + i] : 0.0f;
-      }
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
-#pragma unroll
-      for (int j = 0; j < 8; ++j)
-        if (k0 + u < ksplit) v[j] += p[u][j];
-  }
-  float s = 0.0f;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = threadIdx.x + j * 256;
-    if (i < D) {
-      v[j] = (zr[j] + v[j]) + bn[j];
-      z[i] = v[j];
-      s += v[j] / fd;
+          for (int j = 0; j < 8; ++j) v[j] += p[u][j];
     }
-  }
-  const float mean = block_red_sum(s, red);
-  float q = 0.0f;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = threadIdx.x + j * 256;
-    if (i < D) q += (v[j] - mean) * (v[j] - mean) / fd;
+    for (int j = 0; j < 8; ++j) v[j] = (zr[j] + v[j]) + bn[j];
+    float* zp = Z + (size_t)m * D + k8;
+    *(vh_f32x4*)zp = vh_f32x4{v[0], v[1], v[2], v[3]};
+    *(vh_f32x4*)(zp + 4) = vh_f32x4{v[4], v[5], v[6], v[7]};
   }
-  vh_lds_sync();
-  const float var = block_red_sum(q, red);
-  const float sd = sqrtf(var + 0.00001f);
-  if (F == nullptr) {
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int i = threadIdx.x + j * 256;
-      if (i < D) y[i] = (v[j] - mean) / sd * wv[j] + bv[j];
-    }
-    return;
-  }
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    const int i = threadIdx.x + j * 256;
-    if (i < D) out[i] = (v[j] - mean) / sd * wv[j] + bv[j];
-  }
-  __syncthreads();
-  bool bad = false;
-  if (8 * (int)threadIdx.x < D) pf_frag_put8(F, MT, D / 32, m, 8 * threadIdx.x, out + 8 * threadIdx.x, bad);
-  if (bad) stc_u(err, VH_ERR_RANGE);
+  pf_norm8_out(v, wv, bv, in, D, m, Y, F, MT, err, red);
 }
 
 // ---------------------------------------------------------------- decode products
@@ -524,10 +492,10 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_frag(const float* __
   const int m = e / (N / 8), n8 = 8 * (e % (N / 8));
   float v[8];
   const float* p = ws + (size_t)m * N + n8;
-#pragma unroll
-  for (int j = 0; j < 8; ++j) v[j] = p[j];
+  pf_ld8f(p, v);
   for (int k = 1; k < ksplit; ++k) {
-    const float* q = p + (size_t)k * M * N;
+    float q[8];
+    pf_ld8f(p + (size_t)k * M * N, q);
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] += q[j];
   }
