@@ -375,6 +375,45 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
 // product (N / 32 k-steps).
 #define PF_MW 8
 #define PF_MN 2
+
+// pf_epi for eight consecutive columns n .. n + 7 of row m (one position per
+// row), modes 1 (residual) and 3 (qkv: queries, or eight values of a key /
+// value cache row as one 16-byte store); the same arithmetic per value.
+__device__ __forceinline__ void pf_epi8(int mode, int m, int n, float* v, const vh_half* __restrict__ bias, int N,
+                                        float* __restrict__ out, int ldo, vh_half* __restrict__ kc,
+                                        vh_half* __restrict__ vc, const int* __restrict__ tp, int layer, int L,
+                                        int tmax) {
+  float bn[8] = {};
+  if (bias) unpack8(ld16(bias + n), bn);
+  if (mode == 1) {
+    float* o = out + (size_t)m * ldo + n;
+    float z[8];
+    pf_ld8f(o, z);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = (z[j] + v[j]) + bn[j];
+    *(vh_f32x4*)o = vh_f32x4{v[0], v[1], v[2], v[3]};
+    *(vh_f32x4*)(o + 4) = vh_f32x4{v[4], v[5], v[6], v[7]};
+    return;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) v[j] = v[j] + bn[j];
+  const int D = N / 3;
+  if (n < D) {
+    float* o = out + (size_t)m * ldo + n;
+    *(vh_f32x4*)o = vh_f32x4{v[0], v[1], v[2], v[3]};
+    *(vh_f32x4*)(o + 4) = vh_f32x4{v[4], v[5], v[6], v[7]};
+    return;
+  }
+  const int pos = *tp;
+  if (pos < 0 || pos >= tmax) return;
+  unsigned short h[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) h[j] = f2h(v[j]);
+  const size_t at = ((size_t)(m * L + layer) * tmax + pos) * D + (n % D);
+  *(vh_u32x4*)((n < 2 * D ? kc : vc) + at) =
+      vh_u32x4{h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16), h[4] | ((unsigned)h[5] << 16),
+               h[6] | ((unsigned)h[7] << 16)};
+}
 template <int MT>
 __device__ __forceinline__ void pf_mgemm_body(
     int vb, const vh_u32x4* __restrict__ Af, const vh_u32x4* __restrict__ Wf, int KT, int NT, int ks,
@@ -457,13 +496,27 @@ __device__ __forceinline__ void pf_mgemm_body(
     if (bad) stc_u(err, VH_ERR_RANGE);
     return;
   }
+  if (ks > 1 || mode == 1 || mode == 3) {   // eight consecutive columns per thread, 16-byte stores
+    for (int e = threadIdx.x; e < 16 * MT * 2 * PF_MN; e += PF_MW * 64) {
+      const int m = e / (2 * PF_MN), c8 = 8 * (e % (2 * PF_MN)), n = n0 + c8;
+      if (m >= M || n >= N) continue;
+      float v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) v[j] = tile[m][c8 + j];
+      if (ks > 1) {
+        float* p = ws + ((size_t)part * M + m) * N + n;
+        *(vh_f32x4*)p = vh_f32x4{v[0], v[1], v[2], v[3]};
+        *(vh_f32x4*)(p + 4) = vh_f32x4{v[4], v[5], v[6], v[7]};
+      } else {
+        pf_epi8(mode, m, n, v, bias, N, out, ldo, kc, vc, tp, layer, L, tmax);
+      }
+    }
+    return;
+  }
   for (int e = threadIdx.x; e < 16 * MT * 16 * PF_MN; e += PF_MW * 64) {
     const int m = e / (16 * PF_MN), c = e % (16 * PF_MN), n = n0 + c;
     if (m >= M || n >= N) continue;
-    if (ks > 1)
-      ws[((size_t)part * M + m) * N + n] = tile[m][c];
-    else
-      pf_epi(mode, m, n, tile[m][c], bias, N, out, ldo, kc, vc, 1, tp, layer, L, tmax);
+    pf_epi(mode, m, n, tile[m][c], bias, N, out, ldo, kc, vc, 1, tp, layer, L, tmax);
   }
 }
 
