@@ -366,15 +366,19 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
 // its own accumulator and combined at the end). A block is PF_MW waves on the
 // same PF_MN n-tiles (32 columns); block vb takes n-tile pair vb / ks and fold
 // part vb % ks of ks, and its waves split that part's k-steps into PF_MW
-// consecutive runs, each wave keeping the next k-step's operands in flight
-// while it multiplies the current one. The waves' partial tiles are added in
-// LDS in wave order. Then either the part is stored (ks > 1: ws[part][m][n],
-// added by pf_reduce / pf_reduce_ln / pf_reduce_frag), or the epilogue of
-// `mode` is applied: 0, 1 and 3 as pf_epi (one position per row); 2 (GELU)
-// writes the result in fragment order into F, as the activation of the next
-// product (N / 32 k-steps).
+// consecutive runs. A wave with at most PF_WFIRST k-steps issues all its
+// weight fragments at once, then the activation fragments one k-step ahead
+// of the one it multiplies (XL B=64 decode 3.35 -> 3.10 ms per step against
+// both one k-step ahead; activations two ahead 3.15); a longer run keeps the
+// next k-step's weights and activations in flight. The waves' partial tiles
+// are added in LDS in wave order. Then either the part is stored (ks > 1:
+// ws[part][m][n], added by pf_reduce / pf_reduce_ln / pf_reduce_frag), or the
+// epilogue of `mode` is applied: 0, 1 and 3 as pf_epi (one position per row);
+// 2 (GELU) writes the result in fragment order into F, as the activation of
+// the next product (N / 32 k-steps).
 #define PF_MW 8
 #define PF_MN 2
+#define PF_WFIRST 8     // k-steps of a wave up to which all its weight fragments are loaded first
 
 // pf_epi for eight consecutive columns n .. n + 7 of row m (one position per
 // row), modes 1 (residual) and 3 (qkv: queries, or eight values of a key /
@@ -453,13 +457,45 @@ __device__ __forceinline__ void pf_mgemm_body(
         acl[t][mt] = vh_mfma(a[1][mt], w[t], acl[t][mt]);
       }
   };
-  load(wa, aa, k0);
-  for (int k = k0; k < k1; k += 2) {
-    load(wb, ab, k + 1);
-    mma(wa, aa);
-    if (k + 1 >= k1) break;
-    load(wa, aa, k + 2);
-    mma(wb, ab);
+  if (k1 - k0 <= PF_WFIRST) {
+    // all of the wave's weight fragments first (so they are in flight at once),
+    // then the activation fragments one k-step ahead
+    vh_u32x4 wall[PF_WFIRST][PF_MN];
+#pragma unroll
+    for (int j = 0; j < PF_WFIRST; ++j)
+#pragma unroll
+      for (int t = 0; t < PF_MN; ++t)
+        wall[j][t] = k0 + j < k1 && nt0 + t < NT ? Wf[((size_t)(nt0 + t) * KT + k0 + j) * 64 + lane]
+                                                 : vh_u32x4{0u, 0u, 0u, 0u};
+    auto loada = [&](vh_u32x4 (&a)[2][MT], int k) {
+      const bool in = k < k1;
+#pragma unroll
+      for (int p = 0; p < 2; ++p)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+          a[p][mt] = in ? Af[p * plane + ((size_t)mt * KT + k) * 64 + lane] : vh_u32x4{0u, 0u, 0u, 0u};
+    };
+    loada(aa, k0);
+#pragma unroll
+    for (int j = 0; j < PF_WFIRST; j += 2) {
+      if (k0 + j < k1) {
+        loada(ab, k0 + j + 1);
+        mma(wall[j], aa);
+      }
+      if (k0 + j + 1 < k1) {
+        loada(aa, k0 + j + 2);
+        mma(wall[j + 1], ab);
+      }
+    }
+  } else {
+    load(wa, aa, k0);
+    for (int k = k0; k < k1; k += 2) {
+      load(wb, ab, k + 1);
+      mma(wa, aa);
+      if (k + 1 >= k1) break;
+      load(wa, aa, k + 2);
+      mma(wb, ab);
+    }
   }
 #pragma unroll
   for (int t = 0; t < PF_MN; ++t)
