@@ -32,9 +32,9 @@ from .lower import lower
 LDS_PER_CU = 160 * 1024      # bytes of LDS one block of the persistent kernel may use
 SPILLS_LAYERED = 64          # spilled registers beyond which 'auto' takes the layered engine
 LAYERED_ROWS = {768: 12}      # rows from which 'auto' takes the layered engine, by model width (same box, ms
-LAYERED_ROWS_OTHER = 32       # per step, persistent / layered: GPT-2 small 8 rows 0.291 / 0.499, 12 rows
-                              # 0.563 / 0.504, 16 rows 0.620 / 0.519, 32 rows with a 1024-position cache 1.549 /
-                              # 0.790; medium 8 rows 0.859 / 1.287, 16 rows 1.233 / 1.326)
+LAYERED_ROWS_OTHER = 16       # per step, persistent / layered: GPT-2 small 8 rows 0.290 / 0.456, 12 rows
+                              # 0.553 / 0.461, 16 rows 0.601 / 0.472, 32 rows with a 1024-position cache 1.544 /
+                              # 0.669; medium 8 rows 0.860 / 1.092, 16 rows 1.237 / 1.128)
 
 SHAPE_PROGRAMS = {(12, 768, 12): 'gpt2.vst', (24, 1024, 16): 'gpt2_medium.vst', (48, 1600, 25): 'gpt2_xl.vst'}
 
