@@ -425,6 +425,39 @@ def test_layered_graph_replays_match_launches(small):
     assert torch.equal(k0, k1)
 
 
+@pytest.mark.parametrize('B', [13, 40])
+def test_layered_ragged_rows_match_oracle(small, B):
+    """The layered decode with a row count that is not a multiple of the
+    decode products' 16-row tiles (13 rows: one tile, 40 rows: four tiles,
+    the last 24 rows of the fragment-order activations never written):
+    the first and last rows against the oracle on the GPU's own inputs."""
+    torch = _torch()
+    from oracle import decode
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import random_prompts
+    hf, W, text = small
+    P, G, T = 7, 4, 32
+    m = VestaGPT2(hf, batch=B, tmax=T, engine='layered')
+    pr = random_prompts(B, P, 50257, seed=50 + B)
+    m.reset()
+    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32))
+    lg, ins = [m.logits().float().cpu().numpy().copy()], [m.x.cpu().numpy().copy()]
+    for _ in range(G):
+        m.step()
+        torch.cuda.synchronize()
+        lg.append(m.logits().float().cpu().numpy().copy())
+        ins.append(m.x.cpu().numpy().copy())
+    m.check()
+    for r in (0, B - 1):
+        seq = np.concatenate([pr[r], [ins[k][r] for k in range(G)]])
+        onx, olog, marg = decode.teacher_forced(text, W, seq, T)
+        got = np.stack([lg[k][r] for k in range(G + 1)])
+        err = np.abs(got - olog[P - 1:]).max()
+        assert err < LOGIT_TOL, r
+        nxt = np.array([ins[k][r] for k in range(G + 1)])
+        _tokens_match(f'layered B={B} row {r}', nxt, onx[P - 1:], marg[P - 1:], err)
+
+
 @pytest.mark.parametrize('B,engine', [(64, 'layered'), (8, 'persistent')])
 def test_xl_widths_match_oracle(B, engine):
     """GPT-2 XL widths (d 1600, 25 heads, f 6400), two layers to keep the
