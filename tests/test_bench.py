@@ -58,3 +58,43 @@ def test_pmc_summary_scales_counters_by_the_calibration_copy(tmp_path, monkeypat
     assert bench.measured_traffic('vesta_step_b8', 'aa')['traffic'] == b8['traffic']
     assert bench.measured_traffic('vesta_step_b8', 'cc') is None
     assert bench.measured_traffic('vesta_step_b4', 'aa') is None
+
+
+def test_engines_mode_times_both_engines_at_each_shape(monkeypatch):
+    """--engines parses model:rows:prompt:cache shapes and reports both
+    engines' ms per step for each (the engine runs replaced by stand-ins)."""
+    import types
+    calls = []
+
+    class FakeModel:
+        def __init__(self, hf, batch, tmax, engine):
+            calls.append((batch, tmax, engine))
+            if engine == 'persistent' and batch > 16:
+                raise RuntimeError('does not fit')
+
+        def reset(self):
+            pass
+
+        def prefill(self, prompts):
+            pass
+
+        def step(self, n, tokens=None):
+            pass
+
+        def check(self):
+            pass
+
+    torch = pytest.importorskip('torch')
+    fake_gpt2 = types.SimpleNamespace(VestaGPT2=FakeModel)
+    monkeypatch.setitem(sys.modules, 'vesta.gpt2', fake_gpt2)
+    monkeypatch.setattr(torch.cuda, 'synchronize', lambda: None)
+    monkeypatch.setattr(torch.cuda, 'empty_cache', lambda: None)
+    real_zeros, real_from_numpy = torch.zeros, torch.from_numpy
+    monkeypatch.setattr(torch, 'zeros', lambda *a, **k: real_zeros(*a, **{x: y for x, y in k.items() if x != 'device'}))
+    monkeypatch.setattr(torch.Tensor, 'to', lambda self, *a, **k: self)
+    out = bench.engines_line([('small', 8, 4, 32), ('small', 32, 4, 64)], steps=2, warmup=1)
+    rows = out['rows']
+    assert [(r['rows'], r['tmax']) for r in rows] == [(8, 32), (32, 64)]
+    assert isinstance(rows[0]['persistent'], float) and isinstance(rows[0]['layered'], float)
+    assert rows[1]['persistent'].startswith('does not fit') and isinstance(rows[1]['layered'], float)
+    assert calls == [(8, 32, 'persistent'), (8, 32, 'layered'), (32, 64, 'persistent'), (32, 64, 'layered')]
