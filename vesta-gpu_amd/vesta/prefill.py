@@ -13,6 +13,12 @@ LayerNorm and the tied output head; its argmax becomes the next input.
 Afterwards the model is in the state P decode steps would leave: cache rows
 t0 .. t0 + P - 1 written, ``x`` the token chosen after the last prompt token,
 ``t`` advanced by P, ``logits()`` that step's logits.
+
+The same launch sequence with one position per row is the layered decode
+engine (``Prefill.decode``, replayed from a captured HIP graph). Up to 64
+rows its products are ``pf_mgemm*``, which read weights packed once in the
+matrix cores' operand order (``frag_weights``) and activations that the
+LayerNorms, attention and the widening product's GELU write in that order.
 """
 from __future__ import annotations
 
@@ -33,9 +39,9 @@ ARGMAX_SPLIT = 16             # blocks per row of the output-head argmax
 SPLIT_BLOCKS = 384            # a product with fewer output tiles than this splits its fold over blocks ...
                               # (XL B=64 decode: 4.95 ms per step at 320-384, 5.18 at 256, 5.42 at 512)
 SPLIT_MIN_CHUNKS = 4          # ... into parts of at least this many 64-deep chunks
-FUSE_REDUCE_LN = True         # a split residual product's reduction makes the LayerNorm that follows (one
-                              # launch instead of two; same box: GPT-2 small B=32 1.073 -> 1.055 ms per step,
-                              # XL B=64 5.194 -> 5.212: one block per row reads all the parts of its row)
+FUSE_REDUCE_LN = True         # (prefill products) a split residual product's reduction makes the LayerNorm
+                              # that follows (one launch instead of two; same box, decode on these products:
+                              # GPT-2 small B=32 1.073 -> 1.055 ms per step, XL B=64 5.194 -> 5.212)
 MODE_PLAIN, MODE_RESID, MODE_GELU, MODE_QKV = 0, 1, 2, 3
 DECODE_ROWS = 64              # decode passes of up to this many rows run the fragment-order products (pf_mgemm*)
 MG_WAVES = 8                  # waves of a pf_mgemm block ...
