@@ -458,6 +458,40 @@ def test_layered_ragged_rows_match_oracle(small, B):
         _tokens_match(f'layered B={B} row {r}', nxt, onx[P - 1:], marg[P - 1:], err)
 
 
+def test_layered_one_pass_attention_matches_oracle(small):
+    """The layered decode over a cache long enough for the one-pass attention
+    (pf_attn1s: 600 positions) at positions 140-143, where the first 16 of
+    a block's 32 lane groups take two batches of positions and the others
+    one: rows 0 and 4 of 5 against the oracle on the GPU's own inputs."""
+    torch = _torch()
+    from oracle import decode
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import random_prompts
+    hf, W, text = small
+    B, P, G, T = 5, 140, 3, 600
+    m = VestaGPT2(hf, batch=B, tmax=T, engine='layered')
+    assert m._pf._attn1() == 'pf_attn1s'
+    pr = random_prompts(B, P, 50257, seed=77)
+    m.reset()
+    m.prefill(torch.from_numpy(pr).to('cuda', torch.int32))
+    lg, ins = [m.logits().float().cpu().numpy().copy()], [m.x.cpu().numpy().copy()]
+    for _ in range(G):
+        m.step()
+        torch.cuda.synchronize()
+        lg.append(m.logits().float().cpu().numpy().copy())
+        ins.append(m.x.cpu().numpy().copy())
+    m.check()
+    for r in (0, B - 1):
+        seq = np.concatenate([pr[r], [ins[k][r] for k in range(G)]])
+        onx, olog, marg = decode.teacher_forced(text, W, seq, T)
+        got = np.stack([lg[k][r] for k in range(G + 1)])
+        err = np.abs(got - olog[P - 1:]).max()
+        print(f'one-pass attention row {r}: max logit error {err:.2e}', flush=True)
+        assert err < LOGIT_TOL, r
+        nxt = np.array([ins[k][r] for k in range(G + 1)])
+        _tokens_match(f'one-pass attention row {r}', nxt, onx[P - 1:], marg[P - 1:], err)
+
+
 @pytest.mark.parametrize('B,engine', [(64, 'layered'), (8, 'persistent')])
 def test_xl_widths_match_oracle(B, engine):
     """GPT-2 XL widths (d 1600, 25 heads, f 6400), two layers to keep the

@@ -841,6 +841,114 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restri
   }
 }
 
+// pf_attn1 in one pass over the cache (a running softmax): lane group g
+// (eight lanes, one 16-byte piece of a row each) takes positions g, g + 32, ..
+// and loads each position's key and value pieces together, four positions a
+// batch. Per batch the group's running maximum m becomes max(m, its scores),
+// its sum l and weighted values (eight dims per lane) are rescaled by
+// exp(m_old - m) and the batch's exp(score - m) added. The 32 groups are then
+// combined in group order, each rescaled by exp(m_g - max_g m_g): the output is
+// the sum of the weighted values over the sum of the l's. One round trip to
+// the cache per batch instead of one for the keys and one for the values:
+// faster for long caches (GPT-2 small, 32 rows, 1024 positions: 0.666 -> 0.637
+// ms per step), not for short ones (XL, 64 rows, 256 positions: 3.110 ->
+// 3.128), so the decode pass takes it from ATTN_ONE_PASS_FROM positions.
+extern "C" __global__ __launch_bounds__(256) void pf_attn1s(const float* __restrict__ Q, const vh_half* __restrict__ kc,
+                                                             const vh_half* __restrict__ vc, float* __restrict__ O,
+                                                             const int* __restrict__ tp, int layer, int L, int tmax,
+                                                             int H, vh_half* __restrict__ F, int MT,
+                                                             unsigned* __restrict__ err) {
+  __shared__ float qs[PF_E];
+  __shared__ float gm[32], gl[32], gf[32];
+  __shared__ float part[32][PF_E];
+  const int tid = threadIdx.x;
+  const int m = blockIdx.x / H, h = blockIdx.x % H;      // grid: rows * H blocks exactly
+  const int D = H * PF_E;
+  const int at = *tp;
+  const int pos = at < tmax ? at : tmax - 1;
+  const size_t base = (size_t)(m * L + layer) * tmax * D + (size_t)h * PF_E;
+  const int g = tid >> 3, b8 = tid & 7;
+  float qv[8];
+  {
+    const float* qp = Q + (size_t)m * D + h * PF_E + 8 * b8;
+    const vh_f32x4 q0 = *(const vh_f32x4*)qp, q1 = *(const vh_f32x4*)(qp + 4);
+    qv[0] = q0[0]; qv[1] = q0[1]; qv[2] = q0[2]; qv[3] = q0[3];
+    qv[4] = q1[0]; qv[5] = q1[1]; qv[6] = q1[2]; qv[7] = q1[3];
+  }
+  float mx = -INFINITY, sm = 0.0f, o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  for (int s0 = g; s0 <= pos; s0 += 32 * 4) {
+    vh_u32x4 kr[4], vr[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = s0 + 32 * u;
+      const size_t at8 = base + (size_t)s * D + 8 * b8;
+      kr[u] = s <= pos ? ld16(kc + at8) : vh_u32x4{0u, 0u, 0u, 0u};
+      vr[u] = s <= pos ? ld16(vc + at8) : vh_u32x4{0u, 0u, 0u, 0u};
+    }
+    float sc[4];
+    float bm = mx;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float kv[8];
+      unpack8(kr[u], kv);
+      float acc = 0.0f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc = fmaf(qv[j], kv[j], acc);
+      acc += __shfl_xor(acc, 1, 64);
+      acc += __shfl_xor(acc, 2, 64);
+      acc += __shfl_xor(acc, 4, 64);
+      sc[u] = acc * 0.125f;                 // / 8, exact
+      if (s0 + 32 * u <= pos) bm = fmaxf(bm, sc[u]);
+    }
+    const float c = expf(mx - bm);          // 0 while mx is -inf (bm is finite: s0 <= pos)
+    sm *= c;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] *= c;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      if (s0 + 32 * u > pos) continue;
+      const float p = expf(sc[u] - bm);
+      float v[8];
+      unpack8(vr[u], v);
+      sm += p;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = fmaf(p, v[j], o[j]);
+    }
+    mx = bm;
+  }
+  if (b8 == 0) {
+    gm[g] = mx;
+    gl[g] = sm;
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) part[g][8 * b8 + j] = o[j];
+  __syncthreads();
+  if (tid < 32) {             // each group's scale (0 for a group with no position)
+    float M = gm[0];
+    for (int k = 1; k < 32; ++k) M = fmaxf(M, gm[k]);
+    gf[tid] = gm[tid] == -INFINITY ? 0.0f : expf(gm[tid] - M);
+  }
+  __syncthreads();
+  if (tid < PF_E) {
+    float l = 0.0f, r = 0.0f;
+    for (int k = 0; k < 32; ++k) {
+      l = fmaf(gl[k], gf[k], l);
+      r = fmaf(part[k][tid], gf[k], r);
+    }
+    r = r / l;
+    if (F == nullptr)
+      O[(size_t)m * D + h * PF_E + tid] = r;
+    else
+      qs[tid] = r;
+  }
+  if (F != nullptr) {       // the head's 64 outputs in fragment order, eight per thread
+    __syncthreads();
+    bool bad = false;
+    if (tid < PF_E / 8) pf_frag_put8(F, MT, D / 32, m, h * PF_E + 8 * tid, qs + 8 * tid, bad);
+    if (bad) stc_u(err, VH_ERR_RANGE);
+  }
+}
+
 // ---------------------------------------------------------------- argmax
 // Per row of logits [B, V]: the largest value, a tie to the lowest id
 // (gpt2.vst Q10), in two launches so that a row is read by S blocks at once.

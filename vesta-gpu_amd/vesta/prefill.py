@@ -34,7 +34,7 @@ TILE = 64
 CHUNK = 64                    # fold depth one product step stages in LDS
 HEAD = 64
 KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_reduce_ln', 'pf_attn', 'pf_attn1', 'pf_argmax_part',
-           'pf_argmax', 'pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_reduce_frag')
+           'pf_argmax', 'pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_reduce_frag', 'pf_attn1s')
 ARGMAX_SPLIT = 16             # blocks per row of the output-head argmax
 SPLIT_BLOCKS = 384            # a product with fewer output tiles than this splits its fold over blocks ...
                               # (XL B=64 decode: 4.95 ms per step at 320-384, 5.18 at 256, 5.42 at 512)
@@ -49,6 +49,8 @@ MG_TILES = 2                  # ... and the 16-column tiles it makes
 MG_BLOCKS = 200               # a decode product splits its fold so that it has about this many blocks, ...
 MG_MIN_STEPS = 16             # ... each part at least this many 32-deep k-steps (two per wave)
 FRAG_DECODE = True            # decode passes on the fragment-order products (else the prefill products)
+ATTN_ONE_PASS_FROM = 512      # decode passes over caches of at least this many positions read each cache row
+                              # in one pass (pf_attn1s), shorter ones in two (pf_attn1: keys, then values)
 
 
 def supported(D, H, F):
@@ -274,8 +276,8 @@ class Prefill:
             def lw(name, layer=layer):
                 return W[name][layer]
             self._mgemm(AF, D, 'qkvw', layer, 3 * D, MODE_QKV, bias=lw('qkvb'), out=Q, ldo=D, M=B)
-            self._launch('pf_attn1', B * H, [_p(Q), _p(m.keys), _p(m.vals), _p(None), _p(m.t), _i(layer), _i(L),
-                                             _i(m.tmax), _i(H), _p(AF), _i(mt), _p(err)])
+            self._launch(self._attn1(), B * H, [_p(Q), _p(m.keys), _p(m.vals), _p(None), _p(m.t), _i(layer),
+                                                _i(L), _i(m.tmax), _i(H), _p(AF), _i(mt), _p(err)])
             if not self._mgemm(AF, D, 'ow', layer, D, MODE_RESID, bias=lw('ob'), out=Z, ldo=D,
                                ln=(lw('ln2w'), lw('ln2b'), AF), M=B):
                 self._launch('pf_ln', B, [_p(Z), _i(0), _i(1), _p(lw('ln2w')), _p(lw('ln2b')), _p(None), _i(D),
@@ -292,6 +294,10 @@ class Prefill:
                                                            _p(buf['api'])])
         self._launch('pf_argmax', B, [_p(buf['apv']), _p(buf['api']), _i(ARGMAX_SPLIT), _p(m.x), _p(nxt), _p(m.t),
                                       _i(1)])
+
+    def _attn1(self):
+        """The decode attention kernel for this model's cache length."""
+        return 'pf_attn1s' if self.m.tmax >= ATTN_ONE_PASS_FROM else 'pf_attn1'
 
     def _transposed(self, name):
         """The weight copy ``name`` (``<w>__t``: [L, out, in]); the decode
@@ -430,8 +436,8 @@ class Prefill:
             self._gemm(A, D, lt('qkvw__t'), lw('qkvb'), M, 3 * D, D, MODE_QKV, Q, D, layer, P)
             if P == 1:      # a decode pass: a block per (row, head) (GPT-2 small, 32 rows, 1024
                             # positions: 1.32 -> 1.07 ms per step against a wave per (row, head))
-                self._launch('pf_attn1', M * H, [_p(Q), _p(m.keys), _p(m.vals), _p(A), _p(m.t), _i(layer), _i(L),
-                                                 _i(m.tmax), _i(H), _p(None), _i(0), _p(self.err)])
+                self._launch(self._attn1(), M * H, [_p(Q), _p(m.keys), _p(m.vals), _p(A), _p(m.t), _i(layer),
+                                                    _i(L), _i(m.tmax), _i(H), _p(None), _i(0), _p(self.err)])
             else:
                 self._launch('pf_attn', -(-M * H // (BLOCK // 64)),
                              [_p(Q), _p(m.keys), _p(m.vals), _p(A), _i(M), _i(P), _p(m.t), _i(layer), _i(L),
