@@ -171,7 +171,7 @@ def test_fitted_kernels_take_the_deepest_mfma_pipeline_that_fits(monkeypatch):
     def fake_lower(text, res, prefetch_vgprs, mfma_pipe, **kw):
         tries.append((prefetch_vgprs, mfma_pipe))
         return Low(prefetch_vgprs, mfma_pipe)
-    spills = {(64, 2): 30, (64, 1): 5}
+    spills = {(64, 2): launch.SPILLS_OK + 1, (64, 1): launch.SPILLS_OK}     # just beyond, then at the limit
     with monkeypatch.context() as mp:
         mp.setattr(launch, 'compile_code', lambda src: src)
         mp.setattr(launch, 'code_spills', lambda code: spills.get(code, 99))

@@ -30,6 +30,8 @@ import math
 
 ATTN_PREFETCH_SLOTS = 8      # cache rows per lane issued early (K and V each)
 ATTN_CHUNK = 4               # longer contexts: slots per chunk of the running (online) softmax
+ATTN_ONLINE_SHORT = True     # shorter ones: the running softmax too, as one chunk of every slot (no block-wide
+                             # maximum and sum)
 PROJ_MIN_REPLICAS = 2        # fuse the out-projection only if every leading point gets this many blocks
 PROJ_EARLY_SLOTS = 8         # projection weights issued at the barrier when a lane needs at most this many loads
 READY_ATTN = False           # attention waits for the blocks that made its rows (readiness flags) instead of
@@ -421,9 +423,10 @@ class AttnMixin:
         # more slots than registers hold: the softmax runs over chunks of slots
         # (running maximum and sum, rescaled), the rows of the next chunk in
         # flight while a chunk is used
-        online = NPS > ATTN_PREFETCH_SLOTS and self._softmax_form(at)
+        online = (NPS > ATTN_PREFETCH_SLOTS or ATTN_ONLINE_SHORT) and self._softmax_form(at)
+        chunk = ATTN_CHUNK if NPS > ATTN_PREFETCH_SLOTS else NPS
         if online:
-            NPF = min(NPF, ATTN_CHUNK)          # the first chunk at the barrier, the rest streamed
+            NPF = min(NPF, chunk)               # the first chunk at the barrier, the rest streamed
         G = self.size(lead)
         R = pj['R'] if pj is not None else 1      # blocks per leading point (each redoes its attention)
         GR = G * R
@@ -571,7 +574,7 @@ class AttnMixin:
         o.append(f'{I}}}')
         if online:
             self.attn_online(at, o, I, lenv, NPS, NPF, PPP, PPW, LPE, NW, T, nE, kq, vq, slot_env, load_kv,
-                             red_o, pj, po_ref := [])
+                             red_o, pj, po_ref := [], chunk)
             po = po_ref[0]
             if pj is not None:
                 if not early:
@@ -707,8 +710,8 @@ class AttnMixin:
         return t3[3][3] == F and at['c4'].A == ('bin', '/', F, ('idx', t3[1], at_lead))
 
     def attn_online(self, at, o, I, lenv, NPS, NPF, PPP, PPW, LPE, NW, T, nE, kq, vq, slot_env, load_kv,
-                    red_o, pj, po_ref):
-        """Scores, softmax and weighted values over chunks of ATTN_CHUNK slots:
+                    red_o, pj, po_ref, CH):
+        """Scores, softmax and weighted values over chunks of CH slots:
         each lane group keeps its positions' running maximum m, sum l of
         exp(score - m) and weighted values (rescaled by exp(m_old - m_new) when
         m grows); the groups of a wave, then the waves, are combined the same
@@ -718,7 +721,6 @@ class AttnMixin:
         LDS offset."""
         t1, t2, t3, t4 = at['t']
         c1, c4 = at['c1'], at['c4']
-        CH = ATTN_CHUNK
         NCH = -(-NPS // CH)
         o.append(f'{I}float m_ = -INFINITY, l_ = 0.0f, ov_[8];')
         o.append(f'{I}#pragma unroll')

@@ -211,7 +211,9 @@ def compile_code(src: str, arch: str = ARCH, opts=RTC_OPTS, cache: bool = True) 
 PREFETCH_BUDGETS = (64, 24, 16)   # registers per lane a site may prefetch into, tried in turn (B=8, which
                                   # spills at 64, with a 384-position cache: 308-310 us per step at 16-28,
                                   # 320 at 32, 337 at 48; with 448 positions 24 and 32 are even)
-SPILLS_OK = 8                     # spilled registers a kernel may keep (outside its hot loops)
+SPILLS_OK = 4                     # spilled registers a kernel may keep (outside its hot loops; GPT-2 small
+                                  # B=8, same box: 298.5 us per step with 8 spilled at the first try, 296.2
+                                  # with 1 at the next)
 
 
 def code_spills(code: bytes) -> int:
