@@ -569,6 +569,78 @@ PF_MGEMM(pf_mgemm1, 1)
 PF_MGEMM(pf_mgemm2, 2)
 PF_MGEMM(pf_mgemm4, 4)
 
+// The output head (a plain product with many columns: out[m, n] = C, no
+// bias): block b's wave w makes n-tiles 2 (PF_MW b + w) and the next one
+// over the whole fold, weights and activations one k-step ahead. The block's
+// waves read the same activation fragments at about the same time, so they
+// come from the CU's L1 after the first wave: the activations cross from L2
+// once per block, not once per pair of n-tiles as in pf_mgemm*. The sums go
+// straight from the accumulators to out (lane l: rows 4 (l / 16) .. +4 of
+// column l % 16).
+template <int MT>
+__device__ __forceinline__ void pf_mhead_body(const vh_u32x4* __restrict__ Af, const vh_u32x4* __restrict__ Wf, int KT,
+                                              int NT, int M, int N, float* __restrict__ out, int ldo) {
+  const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  const int nt0 = 2 * (PF_MW * (int)blockIdx.x + wave);
+  if (nt0 >= NT) return;
+  vh_f32x4 acc[2][MT], acl[2][MT];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[t][mt] = acl[t][mt] = vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const size_t plane = (size_t)MT * KT * 64;
+  vh_u32x4 wa[2], aa[2][MT], wb[2], ab[2][MT];
+  auto load = [&](vh_u32x4 (&w)[2], vh_u32x4 (&a)[2][MT], int k) {
+    const bool in = k < KT;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+      w[t] = in && nt0 + t < NT ? Wf[((size_t)(nt0 + t) * KT + k) * 64 + lane] : vh_u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int p = 0; p < 2; ++p)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt)
+        a[p][mt] = in ? Af[p * plane + ((size_t)mt * KT + k) * 64 + lane] : vh_u32x4{0u, 0u, 0u, 0u};
+  };
+  auto mma = [&](const vh_u32x4 (&w)[2], const vh_u32x4 (&a)[2][MT]) {
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        acc[t][mt] = vh_mfma(a[0][mt], w[t], acc[t][mt]);
+        acl[t][mt] = vh_mfma(a[1][mt], w[t], acl[t][mt]);
+      }
+  };
+  load(wa, aa, 0);
+  for (int k = 0; k < KT; k += 2) {
+    load(wb, ab, k + 1);
+    mma(wa, aa);
+    if (k + 1 >= KT) break;
+    load(wa, aa, k + 2);
+    mma(wb, ab);
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    const int n = 16 * (nt0 + t) + (lane & 15);
+    if (nt0 + t >= NT || n >= N) continue;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int m = 16 * mt + 4 * (lane >> 4) + v;
+        if (m < M) out[(size_t)m * ldo + n] = vh_hilo(acc[t][mt][v], acl[t][mt][v]);
+      }
+  }
+}
+#define PF_MHEAD(name, MT)                                                                                         \
+  extern "C" __global__ __launch_bounds__(PF_MW * 64) void name(const vh_u32x4* __restrict__ Af,                 \
+                                                                const vh_u32x4* __restrict__ Wf, int KT, int NT,  \
+                                                                int M, int N, float* __restrict__ out, int ldo) {  \
+    pf_mhead_body<MT>(Af, Wf, KT, NT, M, N, out, ldo);                                                           \
+  }
+PF_MHEAD(pf_mhead1, 1)
+PF_MHEAD(pf_mhead2, 2)
+PF_MHEAD(pf_mhead4, 4)
+
 // The parts of a split GELU product (ws[part][m][n], part order) with the
 // bias and GELU, written in fragment order into F like pf_mgemm's mode 2: one
 // thread per eight consecutive columns of a row.

@@ -34,7 +34,7 @@ TILE = 64
 CHUNK = 64                    # fold depth one product step stages in LDS
 HEAD = 64
 KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_reduce_ln', 'pf_attn', 'pf_attn1', 'pf_argmax_part',
-           'pf_argmax', 'pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_reduce_frag', 'pf_attn1s')
+           'pf_argmax', 'pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_reduce_frag', 'pf_attn1s', 'pf_mhead1', 'pf_mhead2', 'pf_mhead4')
 ARGMAX_SPLIT = 16             # blocks per row of the output-head argmax
 SPLIT_BLOCKS = 384            # a product with fewer output tiles than this splits its fold over blocks ...
                               # (XL B=64 decode: 4.95 ms per step at 320-384, 5.18 at 256, 5.42 at 512)
@@ -49,6 +49,7 @@ MG_TILES = 2                  # ... and the 16-column tiles it makes
 MG_BLOCKS = 200               # a decode product splits its fold so that it has about this many blocks, ...
 MG_MIN_STEPS = 16             # ... each part at least this many 32-deep k-steps (two per wave)
 FRAG_DECODE = True            # decode passes on the fragment-order products (else the prefill products)
+HEAD_SPLIT_N = True           # the decode pass's output head on pf_mhead* (waves split the columns)
 ATTN_ONE_PASS_FROM = 512      # decode passes over caches of at least this many positions read each cache row
                               # in one pass (pf_attn1s), shorter ones in two (pf_attn1: keys, then values)
 
@@ -253,6 +254,20 @@ class Prefill:
                                                             _i(layer or 0), _i(m.L), _i(m.tmax)])
         return False
 
+    def _mhead(self, Af, K, N, out, M):
+        """The output head over M rows (``pf_mhead*``): logits [M, N] = A wte^T,
+        A in fragment order (Af), the packed head weights; a block of
+        MG_WAVES waves per 2 MG_WAVES column tiles, each wave over the whole
+        fold."""
+        KT, NT = K // 32, -(-N // 16)
+        Wf = self._frag('wte')
+        mt = _mtiles(M)
+        if K % 32 or M > 16 * mt or mt > 4 or Af.numel() < 2 * 16 * mt * K or Wf.numel() < NT * KT * 512 \
+                or out.numel() < M * N:
+            raise ValueError(f'output head: operands do not cover {M}x{K} activations, {N}x{K} weights')
+        self._launch(f'pf_mhead{mt}', -(-NT // (2 * MG_WAVES)),
+                     [_p(Af), _p(Wf), _i(KT), _i(NT), _i(M), _i(N), _p(out), _i(N)], block=MG_WAVES * 64)
+
     def _build_decode(self, buf, B, tok):
         """One decode pass (one position per row, B <= DECODE_ROWS) on the
         fragment-order products: LayerNorm and attention write their outputs
@@ -289,7 +304,10 @@ class Prefill:
                 self._launch('pf_ln', B, [_p(Z), _i(0), _i(1), _p(nw), _p(nb_), _p(None), _i(D), _p(AF), _i(mt),
                                           _p(err)])
         logit, nxt = m.logits(), m.next()
-        self._mgemm(AF, D, 'wte', None, V, MODE_PLAIN, out=logit, ldo=V, M=B)
+        if HEAD_SPLIT_N:
+            self._mhead(AF, D, V, logit, B)
+        else:
+            self._mgemm(AF, D, 'wte', None, V, MODE_PLAIN, out=logit, ldo=V, M=B)
         self._launch('pf_argmax_part', B * ARGMAX_SPLIT, [_p(logit), _i(V), _i(ARGMAX_SPLIT), _p(buf['apv']),
                                                            _p(buf['api'])])
         self._launch('pf_argmax', B, [_p(buf['apv']), _p(buf['api']), _i(ARGMAX_SPLIT), _p(m.x), _p(nxt), _p(m.t),
