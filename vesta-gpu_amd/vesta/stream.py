@@ -34,6 +34,8 @@ PI_STREAM = 2                # slots whose loads are issued together when not pr
 PB_MAX = 2                   # points one lane group makes at once (each LDS read of the other factor serves them all)
                              # (B=1, the output head's stream: 229 us per step at 4 and 4, 219 at 2 and 2)
 PB_ACC = 32                  # ... holding at most this many partial sums per lane
+STREAM_ALL_WAVES = True      # a stream whose weights are not prefetched runs on every wave, the polling one
+                             # too (it polls nothing while the stream runs)
 STAGE_OUT_MAX = 8192         # floats of a stream's values a block collects in LDS before writing them out
 
 
@@ -200,6 +202,8 @@ class StreamMixin:
         ltype = self.load_type(dt, vec)
         vregs = -(-PPB // (NW * ppw)) * pl * max(1, vec * esz // 4)
         prefetch = vregs <= self.pf_budget
+        if not prefetch and STREAM_ALL_WAVES and ch is None:
+            NW = self.NWAVE
         # a long stream with several rows: a lane group makes PB points at once,
         # so each value of the other factor read from LDS serves PB weight
         # vectors (a short one keeps every wave busy instead)
