@@ -48,6 +48,9 @@ MG_WAVES = 8                  # waves of a pf_mgemm block ...
 MG_TILES = 2                  # ... and the 16-column tiles it makes
 MG_BLOCKS = 200               # a decode product splits its fold so that it has about this many blocks, ...
 MG_MIN_STEPS = 16             # ... each part at least this many 32-deep k-steps (two per wave)
+MG_MIN_STEPS_LN = 8           # ... or this many for a residual product whose reduction makes the next LayerNorm
+                              # (its split adds no launch; same box, 16 / 12 / 8: XL B=64 3.089 / 3.057 / 3.059
+                              # ms per step, small B=32 with 1024 positions 0.620 / 0.610 / 0.608)
 FRAG_DECODE = True            # decode passes on the fragment-order products (else the prefill products)
 HEAD_SPLIT_N = True           # the decode pass's output head on pf_mhead* (waves split the columns)
 ATTN_ONE_PASS_FROM = 512      # decode passes over caches of at least this many positions read each cache row
@@ -220,7 +223,8 @@ class Prefill:
         m = self.m
         KT, NT = K // 32, -(-N // 16)
         nb = -(-NT // MG_TILES)
-        ks = max(1, min(round(MG_BLOCKS / nb), KT // MG_MIN_STEPS))
+        steps = MG_MIN_STEPS_LN if mode == MODE_RESID and ln is not None else MG_MIN_STEPS
+        ks = max(1, min(round(MG_BLOCKS / nb), KT // steps))
         ws = self._workspace(ks * M * N) if ks > 1 else None
         Wf = self._frag(wname)
         Wf = Wf[layer] if layer is not None else Wf
