@@ -70,10 +70,10 @@ def test_gpt2_small_b1_plan():
     assert p['oo'] == 'attention[bt, h] projection x12'
     assert p['z1'].startswith('fixed-point sum')
     # the down-projection folds each block's own 22 widened values in the widening's
-    # phase, from pw's rows in their own layout, into z kept in 8 fixed-point copies
-    assert p['z2'] == 'local fold over the points of u (22 per block), fixed-point sum in 8 copies'
+    # phase, from pw's rows in their own layout, into z kept in 4 fixed-point copies
+    assert p['z2'] == 'local fold over the points of u (22 per block), fixed-point sum in 4 copies'
     assert low.packs == {'qkvw__t': 'qkvw', 'ow__t': 'ow', 'fcw__t': 'fcw'}
-    assert 'stage_fxc<8>' in low.src and 'clear the copies of z' in low.src
+    assert 'stage_fxc<4>' in low.src and 'clear the copies of z' in low.src
     # attention: scores, softmax statistics and weighted values in one block per (bt, h)
     assert p['sc'] == p['mx'] == p['_h1'] == p['o'] == 'attention[bt, h]'
     assert p['logit'] == 'stream'

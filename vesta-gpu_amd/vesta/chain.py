@@ -33,7 +33,9 @@ from __future__ import annotations
 from .analysis import LowerError, top_folds
 from .mfma import MFMA_ROWS_MIN
 
-FX_COPIES = 8                # copies of a local fold's fixed-point sum (one per XCD of an MI355X)
+FX_COPIES = 4                # copies of a local fold's fixed-point sum (same box, GPT-2 small B=1: 207 / 197 /
+                             # 200 / 205 us per step with 2 / 4 / 8 / 16; B=3 274.6 -> 268.7 from 8 to 4;
+                             # B=2 239.0 / 241.2, within the spread)
 CHAIN_VEC = 8                # weights per 16-byte load (fp16)
 CHAIN_STAGE_MAX = 8192       # floats of the block's own values a local fold may keep in LDS
 
