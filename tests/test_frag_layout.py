@@ -54,3 +54,18 @@ def test_fragment_tiles_multiply_like_the_plain_product():
                     for j in range(16):
                         C[16 * mt + i, 16 * nt + j] += sum(float(a[16 * q + i] @ b[16 * q + j]) for q in range(4))
     assert np.abs(C - A.astype(np.float64) @ W.T.astype(np.float64)).max() < 1e-3
+
+
+def test_decode_attention_kernel_follows_the_cache_length():
+    """The layered decode pass reads caches of ATTN_ONE_PASS_FROM positions or
+    more in one pass (pf_attn1s), shorter ones in two (pf_attn1)."""
+    from types import SimpleNamespace
+    from vesta import prefill
+    pick = lambda tmax: prefill.Prefill._attn1(SimpleNamespace(m=SimpleNamespace(tmax=tmax)))   # noqa: E731
+    assert pick(prefill.ATTN_ONE_PASS_FROM) == 'pf_attn1s'
+    assert pick(prefill.ATTN_ONE_PASS_FROM - 1) == 'pf_attn1'
+    assert pick(1024) == 'pf_attn1s' and pick(256) == 'pf_attn1'
+    assert {'pf_attn1', 'pf_attn1s', 'pf_mhead1', 'pf_mhead2', 'pf_mhead4'} <= set(prefill.KERNELS)
+    src = prefill.prefill_source(448)
+    for name in ('pf_attn1s', 'pf_mhead1', 'pf_mhead2', 'pf_mhead4'):
+        assert f'void {name}(' in src or f'PF_MHEAD({name},' in src, name
