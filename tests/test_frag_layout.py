@@ -56,15 +56,16 @@ def test_fragment_tiles_multiply_like_the_plain_product():
     assert np.abs(C - A.astype(np.float64) @ W.T.astype(np.float64)).max() < 1e-3
 
 
-def test_decode_attention_kernel_follows_the_cache_length():
-    """The layered decode pass reads caches of ATTN_ONE_PASS_FROM positions or
-    more in one pass (pf_attn1s), shorter ones in two (pf_attn1)."""
+def test_decode_attention_kernel_follows_the_block_count():
+    """The layered decode pass reads each cache row in one pass (pf_attn1s)
+    when it has at most ATTN_ONE_PASS_BLOCKS (row, head) blocks, in two
+    (pf_attn1) with more."""
     from types import SimpleNamespace
     from vesta import prefill
-    pick = lambda tmax: prefill.Prefill._attn1(SimpleNamespace(m=SimpleNamespace(tmax=tmax)))   # noqa: E731
-    assert pick(prefill.ATTN_ONE_PASS_FROM) == 'pf_attn1s'
-    assert pick(prefill.ATTN_ONE_PASS_FROM - 1) == 'pf_attn1'
-    assert pick(1024) == 'pf_attn1s' and pick(256) == 'pf_attn1'
+    pick = lambda B, H: prefill.Prefill._attn1(SimpleNamespace(m=SimpleNamespace(B=B, H=H)))   # noqa: E731
+    n = prefill.ATTN_ONE_PASS_BLOCKS
+    assert pick(n // 16, 16) == 'pf_attn1s' and pick(n // 16 + 1, 16) == 'pf_attn1'
+    assert pick(32, 12) == 'pf_attn1s' and pick(64, 25) == 'pf_attn1'
     assert {'pf_attn1', 'pf_attn1s', 'pf_mhead1', 'pf_mhead2', 'pf_mhead4'} <= set(prefill.KERNELS)
     src = prefill.prefill_source(448)
     for name in ('pf_attn1s', 'pf_mhead1', 'pf_mhead2', 'pf_mhead4'):

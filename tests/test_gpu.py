@@ -459,10 +459,10 @@ def test_layered_ragged_rows_match_oracle(small, B):
 
 
 def test_layered_one_pass_attention_matches_oracle(small):
-    """The layered decode over a cache long enough for the one-pass attention
-    (pf_attn1s: 600 positions) at positions 140-143, where the first 16 of
-    a block's 32 lane groups take two batches of positions and the others
-    one: rows 0 and 4 of 5 against the oracle on the GPU's own inputs."""
+    """The layered decode on the one-pass attention (pf_attn1s: 5 rows x 12
+    heads) over a 600-position cache at positions 140-143, where the first
+    16 of a block's 32 lane groups take two batches of positions and the
+    others one: rows 0 and 4 against the oracle on the GPU's own inputs."""
     torch = _torch()
     from oracle import decode
     from vesta.gpt2 import VestaGPT2

@@ -922,9 +922,10 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restri
 // combined in group order, each rescaled by exp(m_g - max_g m_g): the output is
 // the sum of the weighted values over the sum of the l's. One round trip to
 // the cache per batch instead of one for the keys and one for the values:
-// faster for long caches (GPT-2 small, 32 rows, 1024 positions: 0.666 -> 0.637
-// ms per step), not for short ones (XL, 64 rows, 256 positions: 3.110 ->
-// 3.128), so the decode pass takes it from ATTN_ONE_PASS_FROM positions.
+// faster where there are few (row, head) blocks (GPT-2 small, 32 rows, 1024
+// positions: 0.666 -> 0.637 ms per step), not with many (XL, 64 rows x 25
+// heads: 3.110 -> 3.128), so the decode pass takes it up to
+// ATTN_ONE_PASS_BLOCKS blocks.
 extern "C" __global__ __launch_bounds__(256) void pf_attn1s(const float* __restrict__ Q, const vh_half* __restrict__ kc,
                                                              const vh_half* __restrict__ vc, float* __restrict__ O,
                                                              const int* __restrict__ tp, int layer, int L, int tmax,

@@ -53,8 +53,11 @@ MG_MIN_STEPS_LN = 8           # ... or this many for a residual product whose re
                               # ms per step, small B=32 with 1024 positions 0.620 / 0.610 / 0.608)
 FRAG_DECODE = True            # decode passes on the fragment-order products (else the prefill products)
 HEAD_SPLIT_N = True           # the decode pass's output head on pf_mhead* (waves split the columns)
-ATTN_ONE_PASS_FROM = 512      # decode passes over caches of at least this many positions read each cache row
-                              # in one pass (pf_attn1s), shorter ones in two (pf_attn1: keys, then values)
+ATTN_ONE_PASS_BLOCKS = 1024   # decode passes with at most this many (row, head) blocks read each cache row in
+                              # one pass (pf_attn1s), more in two (pf_attn1: keys, then values; fewer
+                              # registers, more blocks resident). Same box, two -> one pass: small 16 / 24 rows
+                              # (192 / 288 blocks, 448 positions) 0.450 -> 0.436 / 0.479 -> 0.466 ms per step,
+                              # 32 rows (384, 1024 positions) 0.666 -> 0.637; XL 64 rows (1600) 3.110 -> 3.128
 
 
 def supported(D, H, F):
@@ -318,8 +321,8 @@ class Prefill:
                                       _i(1)])
 
     def _attn1(self):
-        """The decode attention kernel for this model's cache length."""
-        return 'pf_attn1s' if self.m.tmax >= ATTN_ONE_PASS_FROM else 'pf_attn1'
+        """The decode attention kernel for this model's rows and heads."""
+        return 'pf_attn1s' if self.m.B * self.m.H <= ATTN_ONE_PASS_BLOCKS else 'pf_attn1'
 
     def _transposed(self, name):
         """The weight copy ``name`` (``<w>__t``: [L, out, in]); the decode
