@@ -383,16 +383,11 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
 // pf_epi for eight consecutive columns n .. n + 7 of row m (one position per
 // row), modes 1 (residual) and 3 (qkv: queries, or eight values of a key /
 // value cache row as one 16-byte store); the same arithmetic per value.
-__device__ __forceinline__ void pf_epi8(int mode, int m, int n, float* v, const vh_half* __restrict__ bias, int N,
-                                        float* __restrict__ out, int ldo, vh_half* __restrict__ kc,
-                                        vh_half* __restrict__ vc, const int* __restrict__ tp, int layer, int L,
-                                        int tmax) {
-  float bn[8] = {};
-  if (bias) unpack8(ld16(bias + n), bn);
+__device__ __forceinline__ void pf_epi8(int mode, int m, int n, float* v, const float* bn, const float* z, int pos,
+                                        int N, float* __restrict__ out, int ldo, vh_half* __restrict__ kc,
+                                        vh_half* __restrict__ vc, int layer, int L, int tmax) {
   if (mode == 1) {
     float* o = out + (size_t)m * ldo + n;
-    float z[8];
-    pf_ld8f(o, z);
 #pragma unroll
     for (int j = 0; j < 8; ++j) v[j] = (z[j] + v[j]) + bn[j];
     *(vh_f32x4*)o = vh_f32x4{v[0], v[1], v[2], v[3]};
@@ -408,7 +403,6 @@ __device__ __forceinline__ void pf_epi8(int mode, int m, int n, float* v, const 
     *(vh_f32x4*)(o + 4) = vh_f32x4{v[4], v[5], v[6], v[7]};
     return;
   }
-  const int pos = *tp;
   if (pos < 0 || pos >= tmax) return;
   unsigned short h[8];
 #pragma unroll
@@ -436,6 +430,19 @@ __device__ __forceinline__ void pf_mgemm_body(
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = acl[t][mt] = vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const size_t plane = (size_t)MT * KT * 64;
+  // the epilogue's operands of this thread's item (a thread has at most one:
+  // 16 MT x 2 PF_MN <= PF_MW x 64), loaded before the products so that their
+  // latency is not added at the end: the bias, the residual row piece, the
+  // sequence position of the cache rows
+  const int ei = threadIdx.x, em = ei / (2 * PF_MN), ec8 = 8 * (ei % (2 * PF_MN)), en = 16 * nt0 + ec8;
+  const bool eok = ks == 1 && ei < 16 * MT * 2 * PF_MN && em < M && en < N;
+  float eb[8] = {}, ez[8] = {};
+  int epos = 0;
+  if (eok) {
+    if (bias) unpack8(ld16(bias + en), eb);
+    if (mode == 1) pf_ld8f(out + (size_t)em * ldo + en, ez);
+    if (mode == 3) epos = *tp;
+  }
   vh_u32x4 wa[PF_MN], aa[2][MT], wb[PF_MN], ab[2][MT];
   auto load = [&](vh_u32x4 (&w)[PF_MN], vh_u32x4 (&a)[2][MT], int k) {
     const bool in = k < k1;
@@ -526,7 +533,7 @@ __device__ __forceinline__ void pf_mgemm_body(
       if (m >= M || n0 + c8 >= N) continue;
       float v[8];
 #pragma unroll
-      for (int j = 0; j < 8; ++j) v[j] = pf_gelu(tile[m][c8 + j] + h2f(bias[n0 + c8 + j]));
+      for (int j = 0; j < 8; ++j) v[j] = pf_gelu(tile[m][c8 + j] + eb[j]);     // (e is this thread's item)
       pf_frag_put8(F, MT, N / 32, m, n0 + c8, v, bad);
     }
     if (bad) stc_u(err, VH_ERR_RANGE);
@@ -544,7 +551,7 @@ __device__ __forceinline__ void pf_mgemm_body(
         *(vh_f32x4*)p = vh_f32x4{v[0], v[1], v[2], v[3]};
         *(vh_f32x4*)(p + 4) = vh_f32x4{v[4], v[5], v[6], v[7]};
       } else {
-        pf_epi8(mode, m, n, v, bias, N, out, ldo, kc, vc, tp, layer, L, tmax);
+        pf_epi8(mode, m, n, v, eb, ez, epos, N, out, ldo, kc, vc, layer, L, tmax);     // (e is this thread's item)
       }
     }
     return;
