@@ -321,6 +321,38 @@ extern "C" __global__ __launch_bounds__(256) void pf_ln(const float* __restrict_
   pf_norm8_out(v, wv, bv, in, D, blockIdx.x, Y, F, MT, err, red);
 }
 
+// pf_embed and the first layer's LayerNorm into fragment order (pf_ln) in one
+// launch for a decode pass (one position per row): one block per row, the
+// row kept in registers between the two.
+extern "C" __global__ __launch_bounds__(256) void pf_embed_ln(const int* __restrict__ tok, const int* __restrict__ tp,
+                                                               const vh_half* __restrict__ wte,
+                                                               const vh_half* __restrict__ wpe, float* __restrict__ Z,
+                                                               int D, int V, int npos, const vh_half* __restrict__ w,
+                                                               const vh_half* __restrict__ b, vh_half* __restrict__ F,
+                                                               int MT, unsigned* __restrict__ err) {
+  __shared__ float red[VNWAVE];
+  const int m = blockIdx.x, k8 = 8 * threadIdx.x;
+  const bool in = k8 < D;
+  int x = tok[m];
+  x = x < 0 ? 0 : (x >= V ? V - 1 : x);
+  int pos = *tp;
+  pos = pos < 0 ? 0 : (pos >= npos ? npos - 1 : pos);
+  float v[8] = {}, wv[8] = {}, bv[8] = {};
+  if (in) {
+    float a[8], c[8];
+    unpack8(ld16(wte + (size_t)x * D + k8), a);
+    unpack8(ld16(wpe + (size_t)pos * D + k8), c);
+    unpack8(ld16(w + k8), wv);
+    unpack8(ld16(b + k8), bv);
+#pragma unroll
+    for (int j = 0; j < 8; ++j) v[j] = a[j] + c[j];
+    float* z = Z + (size_t)m * D + k8;
+    *(vh_f32x4*)z = vh_f32x4{v[0], v[1], v[2], v[3]};
+    *(vh_f32x4*)(z + 4) = vh_f32x4{v[4], v[5], v[6], v[7]};
+  }
+  pf_norm8_out(v, wv, bv, in, D, m, nullptr, F, MT, err, red);
+}
+
 // A split residual product's parts added in part order (pf_reduce, mode 1:
 // Z[m, n] = (Z[m, n] + C) + bias[n]) and the LayerNorm that reads Z next (as
 // pf_ln, into Y or F), in one launch: one block per row, the row kept in

@@ -34,7 +34,8 @@ TILE = 64
 CHUNK = 64                    # fold depth one product step stages in LDS
 HEAD = 64
 KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_reduce_ln', 'pf_attn', 'pf_attn1', 'pf_argmax_part',
-           'pf_argmax', 'pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_reduce_frag', 'pf_attn1s', 'pf_mhead1', 'pf_mhead2', 'pf_mhead4')
+           'pf_argmax', 'pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_reduce_frag', 'pf_attn1s', 'pf_mhead1', 'pf_mhead2', 'pf_mhead4',
+           'pf_embed_ln')
 ARGMAX_SPLIT = 16             # blocks per row of the output-head argmax
 SPLIT_BLOCKS = 384            # a product with fewer output tiles than this splits its fold over blocks ...
                               # (XL B=64 decode: 4.95 ms per step at 320-384, 5.18 at 256, 5.42 at 512)
@@ -290,10 +291,9 @@ class Prefill:
         fb = self._decode_buffers(B)
         AF, GF = fb['AF'], fb['GF']
         err = self.err
-        self._launch('pf_embed', B, [_p(tok), _i(1), _p(m.t), _p(W['wte']), _p(W['wpe']), _p(Z), _i(D), _i(V),
-                                     _i(W['wpe'].shape[0])])
-        self._launch('pf_ln', B, [_p(Z), _i(0), _i(1), _p(W['ln1w'][0]), _p(W['ln1b'][0]), _p(None), _i(D), _p(AF),
-                                  _i(mt), _p(err)])
+        self._launch('pf_embed_ln', B, [_p(tok), _p(m.t), _p(W['wte']), _p(W['wpe']), _p(Z), _i(D), _i(V),
+                                        _i(W['wpe'].shape[0]), _p(W['ln1w'][0]), _p(W['ln1b'][0]), _p(AF), _i(mt),
+                                        _p(err)])
         for layer in range(L):
             def lw(name, layer=layer):
                 return W[name][layer]
