@@ -117,7 +117,7 @@ class VestaGPT2:
         self._R, self._bps, self._timing = R, blocks_per_sm, timing
         self.low, self.k, self._pf = None, None, None
         self._variants = {}
-        self._pos = 0
+        self._know_pos(0)
         self.engine, self.why_layered = 'persistent', None
         from .prefill import supported
         if engine == 'layered':
@@ -159,15 +159,26 @@ class VestaGPT2:
         self.keys.zero_()
         self.vals.zero_()
         self.t.zero_()
-        self._pos = 0
+        self._know_pos(0)
+
+    def _know_pos(self, pos):
+        """The host's copy of the position is ``pos``, as of ``t``'s present
+        in-place version: a later host write to ``t`` (``fill_``, ``copy_``)
+        bumps torch's version counter of the tensor, while the kernels'
+        own advances of ``t`` do not."""
+        self._pos = pos
+        self._t_version = self.t._version if pos is not None else None
 
     def _advance(self, n, what):
-        """Keep the host's copy of the position (known after ``reset`` and
-        ``prefill``, advanced by every step this object runs; unknown after the
-        caller writes ``t`` itself until the next ``reset``/``prefill``) and
-        refuse steps past the last cache row: the engines must never be asked
-        for a position the cache does not hold."""
+        """Keep the host's copy of the position (known after ``reset``,
+        ``seek`` and ``prefill``, advanced by every step this object runs;
+        unknown once the caller writes ``t`` itself, until the next ``reset``,
+        ``seek`` or ``prefill``) and refuse steps past the last cache row: the
+        engines must never be asked for a position the cache does not hold."""
         pos = getattr(self, '_pos', None)
+        if pos is not None and getattr(self, '_t_version', None) != self.t._version:
+            self._know_pos(None)             # the caller wrote t: the host no longer knows the position
+            pos = None
         if pos is not None:
             if pos + n > self.tmax:
                 raise ValueError(f'{what}: positions {pos}..{pos + n - 1} exceed the cache (tmax {self.tmax})')
@@ -178,7 +189,7 @@ class VestaGPT2:
         if not 0 <= pos < self.tmax:
             raise ValueError(f'position {pos} outside the cache (tmax {self.tmax})')
         self.t.fill_(int(pos))
-        self._pos = int(pos)
+        self._know_pos(int(pos))
 
     def step(self, n=1, tokens=None):
         """One decode step (the reference API); ``n`` > 1 runs n steps in one
@@ -255,7 +266,7 @@ class VestaGPT2:
         t0 = int(self.t.item())
         if t0 + P > self.tmax:
             raise ValueError(f'positions {t0}..{t0 + P - 1} exceed the cache (tmax {self.tmax})')
-        self._pos = t0 + P
+        self._know_pos(t0 + P)
         if mode == 'batched' or (mode == 'auto' and tokens is None and fits):
             if self._pf is None:
                 from .prefill import Prefill

@@ -388,32 +388,46 @@ class Kernel:
         self.args = (ctypes.c_void_p * len(ptrs))(*ptrs)
         self.keep = residue
 
+    def _steps_and_tokens(self, steps, tokens, inputs, what):
+        """Host checks shared by ``launch`` and ``launch_noalloc``, made before
+        anything is enqueued: the kernel writes ``steps * history`` chosen
+        tokens into ``tokens`` and reads as many inputs from ``inputs``, so
+        both must be contiguous int32 tensors on this kernel's device holding
+        at least that many elements."""
+        if self.args is None:
+            raise RuntimeError(f'bind() the residues before {what}()')
+        steps = int(steps)
+        if steps < 1:
+            raise ValueError('steps must be at least 1')
+        need = steps * int(getattr(self.lowered, 'history', 0) or 0)
+        ptrs = []
+        for arg, t in (('tokens', tokens), ('inputs', inputs)):
+            if t is None:
+                ptrs.append(0)
+                continue
+            if not need:
+                raise ValueError(f'{arg}: {self.lowered.name} records no tokens (no token feedback)')
+            if not (getattr(t, 'is_cuda', False) and t.dtype == TORCH_DT['i32'] and t.is_contiguous()):
+                raise TypeError(f'{arg} must be a contiguous int32 device tensor')
+            if t.device.index is not None and t.device.index != self.device:
+                raise ValueError(f'{arg} is on device {t.device.index}; the kernel runs on device {self.device}')
+            if t.numel() < need:
+                raise ValueError(f'{arg} holds {t.numel()} tokens; {steps} steps of {need // steps} rows need {need}')
+            ptrs.append(t.data_ptr())
+        self._nsteps.value = steps
+        self._tok.value, self._tok_in.value = ptrs
+
     def launch(self, steps=1, tokens=None, inputs=None):
         """Run ``steps`` steps in one cooperative launch on torch's current
         stream (no sync). With token feedback, ``tokens`` (int32 device tensor,
         at least steps * B elements) receives each step's chosen tokens, and
         ``inputs`` (int32 device tensor [steps, B]) forces the input of steps
         1..steps-1 (the first step reads the residue as usual)."""
-        if self.args is None:
-            raise RuntimeError('bind() the residues before launch()')
-        if steps < 1:
-            raise ValueError('steps must be at least 1')
-        self._nsteps.value = int(steps)
-        if tokens is not None:
-            if not (tokens.is_cuda and tokens.dtype == TORCH_DT['i32'] and tokens.is_contiguous()):
-                raise TypeError('tokens must be a contiguous int32 device tensor')
-            self._tok.value = tokens.data_ptr()
-        else:
-            self._tok.value = 0
-        if inputs is not None:
-            if not (inputs.is_cuda and inputs.dtype == TORCH_DT['i32'] and inputs.is_contiguous()):
-                raise TypeError('inputs must be a contiguous int32 device tensor')
-            self._tok_in.value = inputs.data_ptr()
-        else:
-            self._tok_in.value = 0
+        self._steps_and_tokens(steps, tokens, inputs, 'launch')
         stream = _torch().cuda.current_stream().cuda_stream
         ok(lib().vh_launch_cooperative(self.fn, self.grid, self.block, self.smem, ctypes.c_void_p(stream), self.args),
            'cooperative launch')
+        self._noalloc_bar = None
 
     def __call__(self, residue):
         self.bind(residue)
@@ -423,19 +437,18 @@ class Kernel:
         """``launch`` through ``vh_launch_cooperative_noalloc``: S, bar and TS
         are the library's static per-device scratch instead of this object's
         buffers (nothing is allocated; outputs left in S are read with
-        ``read_noalloc``). Calls on one device share that scratch."""
-        if self.args is None:
-            raise RuntimeError('bind() the residues before launch_noalloc()')
-        if steps < 1:
-            raise ValueError('steps must be at least 1')
-        self._nsteps.value = int(steps)
-        self._tok.value = tokens.data_ptr() if tokens is not None else 0
-        self._tok_in.value = inputs.data_ptr() if inputs is not None else 0
+        ``read_noalloc``). Calls on one device share that scratch. The error
+        word of such a launch is in the static scratch's barrier block:
+        ``check()`` reads it there."""
+        self._steps_and_tokens(steps, tokens, inputs, 'launch_noalloc')
+        sizes = (self.S.numel() * 4, self.bar.numel() * 4, self.TS.numel() * 8)
+        bar_off, ts_off = ctypes.c_size_t(), ctypes.c_size_t()
+        ok(lib().vh_noalloc_layout(*sizes, ctypes.byref(bar_off), ctypes.byref(ts_off)), 'static scratch layout')
         stream = _torch().cuda.current_stream().cuda_stream
         ok(lib().vh_launch_cooperative_noalloc(self.fn, self.grid, self.block, self.smem, ctypes.c_void_p(stream),
-                                               self.args, len(self.args), len(self.lowered.params),
-                                               self.S.numel() * 4, self.bar.numel() * 4, self.TS.numel() * 8),
+                                               self.args, len(self.args), len(self.lowered.params), *sizes),
            'cooperative launch (static scratch)')
+        self._noalloc_bar = bar_off.value
 
     def read_noalloc(self, name, out):
         """Copy value ``name`` (a scratch value, e.g. 'logit') from the static
@@ -450,14 +463,36 @@ class Kernel:
         ok(lib().vh_noalloc_read(ctypes.c_void_p(out.data_ptr()), off * 4, out.numel() * 4, ctypes.c_void_p(stream)),
            'static scratch read')
 
+    def _error_word(self):
+        """The error word of the last launch (one device synchronisation):
+        from this object's ``bar``, or from the static scratch's barrier block
+        when the last launch was ``launch_noalloc``."""
+        from .lower import BAR_ERROR
+        bar_off = getattr(self, '_noalloc_bar', None)
+        if bar_off is None:
+            return int(self.bar[BAR_ERROR].item()) if self.bar.numel() > BAR_ERROR else 0
+        word = self._noalloc_word()
+        stream = _torch().cuda.current_stream().cuda_stream
+        ok(lib().vh_noalloc_read(ctypes.c_void_p(word.data_ptr()), bar_off + 4 * BAR_ERROR, 4,
+                                 ctypes.c_void_p(stream)), 'static scratch read')
+        return int(word.item())
+
+    def _noalloc_word(self):
+        w = getattr(self, '_noalloc_word_t', None)
+        if w is None:
+            w = self._noalloc_word_t = _torch().zeros(1, dtype=_torch().int32, device=self.bar.device)
+        return w
+
     def check(self):
         """Raise if a grid barrier of an earlier launch gave up waiting (reads
         the error word: one device synchronisation). The barrier words are
-        cleared first, so the kernel can be launched again."""
-        from .lower import BAR_ERROR, ERR_BARRIER, ERR_RANGE
-        code = int(self.bar[BAR_ERROR].item()) if self.bar.numel() > BAR_ERROR else 0
+        cleared first, so the kernel can be launched again (the static
+        scratch of ``launch_noalloc`` is cleared by its next call)."""
+        from .lower import ERR_BARRIER, ERR_RANGE
+        code = self._error_word()
         if code:
             self.bar.zero_()
+            self._noalloc_bar = None
             why = {ERR_BARRIER: f'a grid barrier gave up waiting (are all {self.grid} blocks resident on the '
                                 f'device?)',
                    ERR_RANGE: 'an activation beyond the fp16 range (65504) reached a matrix-core product'}

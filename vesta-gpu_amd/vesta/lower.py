@@ -126,6 +126,7 @@ class Lowered:
     name: str = 'vesta_step'                      # the kernel's symbol
     per_cu_max: int = 1                           # resident blocks per CU the kernel is laid out for
     packs: dict = field(default_factory=dict)     # transposed copy -> residue it is made from (at bind)
+    history: int = 0                              # tokens a step records in tok_out / reads from tok_in (0: none)
 
 
 # ------------------------------------------------------------------ AST helpers
@@ -586,43 +587,66 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
         return None
 
     # ------------------------------------------------------------ storage
+    def private_spans(self, ss):
+        """Live span (position of the defining statement, last position that
+        needs it) of every private value, positions counted over the
+        statements in program order with loop bodies inlined once.
+
+        A value made before a step loop and needed from the loop's first
+        position on is needed by every iteration, so its span reaches the
+        loop's end (the position after the body's last statement); loops are
+        visited innermost first, in program order. Values made inside a loop
+        are made again by every iteration and keep their own span."""
+        stmts, loops = [], []          # flattened statements; (first, end) of every loop, innermost first
+
+        def visit(block):
+            for s in block:
+                if s[0] != 'step':
+                    stmts.append(s)
+                    continue
+                first = len(stmts)
+                visit(s[6])
+                loops.append((first, len(stmts)))
+        visit(ss)
+        made, need = {}, {}
+        for pos, s in enumerate(stmts):
+            if s[0] == 'let' and s[1] in self.private and s[1] not in made:
+                made[s[1]] = need[s[1]] = pos
+            for n in {n for e in stmt_exprs(s) for n in self.reads(e)} & made.keys():
+                need[n] = pos
+        for first, end in loops:
+            for n, pos in made.items():
+                if pos < first <= need[n]:
+                    need[n] = max(need[n], end)
+        return {n: (made[n], need[n]) for n in made}
+
+    @staticmethod
+    def lowest_gap(busy, size, align=4):
+        """Lowest offset (a multiple of ``align`` floats, or 0) where ``size``
+        floats fit between the address ranges in ``busy`` ((offset, size)
+        pairs that do not overlap each other)."""
+        at = 0
+        for off, n in sorted(busy):
+            if at + size <= off:
+                return at
+            at = max(at, (off + n + align - 1) // align * align)
+        return at
+
     def layout(self, ss):
         """Global scratch for values shared across blocks; LDS for private
-        values (intervals over statement order, reused once dead)."""
-        order, live = [], {}
-
-        def flat(ss):
-            for s in ss:
-                if s[0] == 'step':
-                    start = len(order)
-                    flat(s[6])
-                    end = len(order)
-                    for n, (a, b) in list(live.items()):
-                        if a < start <= b < end or (a < start and b >= start):
-                            live[n] = (a, max(b, end))
-                    continue
-                order.append(s)
-                i = len(order) - 1
-                if s[0] == 'let' and s[1] in self.private:
-                    live.setdefault(s[1], (i, i))
-                for e in stmt_exprs(s):
-                    for n in self.reads(e):
-                        if n in live:
-                            live[n] = (live[n][0], i)
-        flat(ss)
-        self.lds = {}
-        used, top = [], 0
-        for n, (a, b) in sorted(live.items(), key=lambda kv: kv[1][0]):
+        values, each given the lowest free range (16-byte aligned, for vector
+        LDS reads) among the values still live when it is made, in the order
+        they are made."""
+        spans = self.private_spans(ss)
+        self.lds, placed, top = {}, [], 0        # placed: (span end, LDS offset, floats)
+        for n in sorted(spans, key=lambda v: spans[v][0]):
+            born, dies = spans[n]
             size = self.size(self.axes_of[n])
-            used = [u for u in used if u[1] >= a]
-            off = 0
-            for lo, hi, uoff, usize in sorted(used, key=lambda u: u[2]):
-                if off + size <= uoff:
-                    break
-                off = max(off, -(-(uoff + usize) // 4) * 4)     # 16-byte aligned for vector LDS reads
+            placed = [p for p in placed if p[0] >= born]
+            off = self.lowest_gap([(o, k) for _, o, k in placed], size)
             if off + size > PRIV_BUDGET:
                 raise LowerError(f'private values exceed the LDS budget at {n}')
-            used.append((a, b, off, size))
+            placed.append((dies, off, size))
             self.lds[n] = off
             top = max(top, off + size)
         self.lds_floats = -(-top // 4) * 4
@@ -2830,4 +2854,4 @@ def _lower_once(text, res, axis_max, batch, per_token, outputs, feedback, timing
             scratch[n] = (low.g[r], axes, tuple(low.static[a] for a in axes))
     return Lowered(src, params, scratch, low.goff, (low.lds_floats + low.stage_floats) * 4, low.barriers,
                    low.plan, low.sites, low.counters, BLOCK, low.grid, {n: shp for n, (shp, _) in low.res.items()},
-                   kernel_name, 1, dict(low.packs)), low
+                   kernel_name, 1, dict(low.packs), low.history or 0), low
