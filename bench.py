@@ -187,26 +187,29 @@ def run_config(B, steps, warmup, chunk, repeats=REPEATS, seed=0, single=True):
 
 
 def device_bandwidth():
-    """Copy and read bandwidth of this device through PyTorch (reference
-    g0_bench.py:60-75: 512 MB fp16 buffers, best of 20)."""
+    """Copy and read bandwidth of this device (reference g0_bench.py:60-75:
+    512 MB buffers, best of 20): the copy through PyTorch, the read with the
+    repository's own streaming-read kernel (16-byte nontemporal loads, four
+    in flight per lane; ``vesta.profile.stream_read_GBs``)."""
     import torch
+    from vesta.profile import stream_read_GBs
     n = 256 * 1024 * 1024
     a = torch.empty(n, dtype=torch.float16, device='cuda').normal_()
     b = torch.empty_like(a)
-    out = {}
-    for name, fn, mult in (('copy_GBs', lambda: b.copy_(a), 2), ('read_GBs', lambda: a.sum(), 1)):
-        for _ in range(3):
-            fn()
+    for _ in range(3):
+        b.copy_(a)
+    torch.cuda.synchronize()
+    ts = []
+    for _ in range(20):
+        t0 = time.perf_counter()
+        b.copy_(a)
         torch.cuda.synchronize()
-        ts = []
-        for _ in range(20):
-            t0 = time.perf_counter()
-            fn()
-            torch.cuda.synchronize()
-            ts.append(time.perf_counter() - t0)
-        out[name] = round(mult * n * 2 / min(ts) / 1e9, 1)
+        ts.append(time.perf_counter() - t0)
+    out = {'copy_GBs': round(2 * n * 2 / min(ts) / 1e9, 1)}
     del a, b
     torch.cuda.empty_cache()
+    out['read_GBs'] = stream_read_GBs(512 << 20)
+    out['read_probe'] = '512 MB, own kernel: 16-byte nontemporal loads, best of 20 launches (HIP events)'
     return out
 
 
@@ -718,7 +721,7 @@ def main():
         'higher_is_better': True,
         'scaling': 'weak',
         'vs_baseline': None,
-        'dtype': 'f32',
+        'dtype': 'fp32 accumulate, 22-bit split activations from 4 rows',
         'data': 'synthetic: random-init GPT-2-small fp16 weights N(0,0.02) seed 0, uniform-random prompts',
         'config': {'workload': f'GPT-2 small greedy decode, B={args.batch}, {PROMPT}-token prompts (BASELINE.json '
                                f'configs[1]: 256 generated tokens, mean context {MEAN_CTX}); the {args.steps} '

@@ -205,3 +205,32 @@ def test_check_after_a_noalloc_launch_reads_the_static_error_word(monkeypatch):
         k.check()
     assert k._noalloc_bar is None                 # the next check reads the object's own (cleared) bar
     k.check()
+
+
+@pytest.mark.parametrize('plain', [False, True])
+def test_profiling_launch_switch_picks_the_ordinary_launch(monkeypatch, plain):
+    """VESTA_PLAIN_LAUNCH=1 (profiling only) issues the same kernel, grid and
+    arguments through vh_launch instead of vh_launch_cooperative."""
+    calls = []
+
+    class FakeLib:
+        def vh_launch(self, *a):
+            calls.append(('vh_launch', a[1], a[2]))
+            return 0
+
+        def vh_launch_cooperative(self, *a):
+            calls.append(('vh_launch_cooperative', a[1], a[2]))
+            return 0
+
+    fake_torch = types.SimpleNamespace(
+        cuda=types.SimpleNamespace(current_stream=lambda: types.SimpleNamespace(cuda_stream=0)))
+    monkeypatch.setattr(launch, 'lib', FakeLib)
+    monkeypatch.setattr(launch, '_torch', lambda: fake_torch)
+    monkeypatch.setattr(launch, 'PLAIN_LAUNCH', plain)
+    k = _bound_stub()
+    k.fn, k.block, k.smem = None, 512, 0
+    k.launch(2)
+    assert calls == [('vh_launch' if plain else 'vh_launch_cooperative', 144, 512)]
+    if plain:
+        with pytest.raises(RuntimeError, match='cooperative only'):
+            k.launch_noalloc(1)

@@ -155,11 +155,13 @@ def test_config2_one_launch_per_step_matches_chunked():
     assert torch.equal(torch.stack(hist).view(-1), toks)
 
 
-def _config_model(key):
+def _config_model(key, engine='auto'):
     from vesta.gpt2 import VestaGPT2
     from vesta.weights import RandomGPT2, random_prompts
     model, B, P, _, tmax = bench.CONFIGS[key]
-    return VestaGPT2(RandomGPT2(model, 0), batch=B, tmax=tmax), random_prompts(B, P, 50257, seed=1)
+    print(f'config {key}: GPT-2 {model}, B={B}, {P}-token prompts, cache {tmax}, engine {engine}', flush=True)
+    return (VestaGPT2(RandomGPT2(model, 0), batch=B, tmax=tmax, engine=engine),
+            random_prompts(B, P, 50257, seed=1))
 
 
 def test_config3_layered_engine_long_cache_matches_oracle():
@@ -192,3 +194,17 @@ def test_config5_xl_b64_matches_oracle():
     fx = _fixture('c5')
     tokens, sig = decode_against(m, prompts, fx)
     compare('config 5 (GPT-2 XL, B=64, layered)', fx, tokens, sig)
+
+
+@pytest.mark.parametrize('key', [3, 5])
+def test_configs_3_and_5_on_the_persistent_kernel_match_oracle(key):
+    """Configs 3 (GPT-2 small, B=32, 1024-position cache) and 5 (GPT-2 XL,
+    B=64) as one persistent kernel per step: every product on the matrix
+    cores in 16-row tiles (two and four of them), the fold staged through LDS
+    in chunks where the halves of all rows do not fit; same fixtures and bar
+    as the layered engine's tests above."""
+    m, prompts = _config_model(key, engine='persistent')
+    assert m.engine == 'persistent' and 'mfma' in ' '.join(pl for _, pl in m.low.plan)
+    fx = _fixture('c3' if key == 3 else 'c5')
+    tokens, sig = decode_against(m, prompts, fx)
+    compare(f'config {key} (persistent, B={m.B}, tmax {m.tmax})', fx, tokens, sig)

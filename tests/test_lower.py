@@ -241,17 +241,25 @@ def test_c_abi_exports_every_declared_symbol():
 @pytest.mark.parametrize('budget', [16, 32, 64])
 def test_chunked_attention_loads_every_slot(budget):
     """Long caches run the softmax over chunks of slots; whatever the prefetch
-    register budget, every slot's key and value rows are loaded somewhere."""
+    register budget, every slot's key and value rows are loaded somewhere:
+    the first chunk's into kq / vq (at the barrier before, or at the start),
+    each later chunk's by the run-time chunk loop one iteration ahead."""
     import re as _re
+    from vesta.attn import ATTN_CHUNK
     from vesta.lower import lower
     text = open(os.path.join(PKG, 'vesta', 'programs', 'gpt2.vst')).read()
     low = lower(text, gpt2_spec(1, 512), {'s': 512}, batch=1, per_token=('x', 'keys', 'vals'),
                 outputs=('logit', 'next'), feedback={'x': 'next', 't': 1}, prefetch_vgprs=budget)
-    assert '// chunk 0' in low.src
-    for arr in ('kq', 'vq'):
+    nchunks = int(_re.search(r'for \(int c_ = 0; c_ < (\d+); \+\+c_\)', low.src).group(1))
+    for arr, nxt in (('kq', 'kn_'), ('vq', 'vn_')):
         name = _re.search(arr + r'_\w+\[10\];', low.src).group(0).split('[')[0]
-        loaded = {int(k) for k in _re.findall(_re.escape(name) + r'\[(\d+)\] = ldc16_h', low.src)}
-        assert loaded == set(range(10)), (arr, sorted(loaded))
+        first = {int(k) for k in _re.findall(_re.escape(name) + r'\[(\d+)\] = ldc16_h', low.src)}
+        assert first == set(range(ATTN_CHUNK)), (arr, sorted(first))
+        later = {int(j) for j in _re.findall(_re.escape(nxt) + r'\[(\d+)\] = ldc16_h', low.src)}
+        assert later == set(range(ATTN_CHUNK))
+        covered = first | {(c + 1) * ATTN_CHUNK + j for c in range(nchunks - 1) for j in later}
+        assert set(range(10)) <= covered
+    assert _re.search(r'const int sn0_ = \(\(c_ \+ 1\) \* 4 \+ 0\) \* 56', low.src)
 
 
 def test_prefill_kernels_compile_for_gfx950():
@@ -300,10 +308,32 @@ def test_grid_choice():
     assert lower_gpt2(8, grid=160).grid_max == 160
 
 
-def test_xl_widths_at_64_rows_exceed_a_cu_of_lds():
-    """GPT-2 XL widths at 64 rows need more LDS per block than a CU holds,
-    even on the widest grid: the persistent kernel cannot run there, which
-    is one of the reasons ``VestaGPT2(engine='auto')`` takes the layered engine."""
+def test_xl_widths_at_64_rows_fit_a_cu_of_lds():
+    """GPT-2 XL widths at 64 rows fit a CU's LDS on the widest grid: the
+    products stage their other factor through LDS in fold chunks (before,
+    a row stream staged 8 rows x 6400 floats, 206,592 bytes per block)."""
     from vesta.lower import LDS_BYTES
     low = lower_gpt2(64, 16, (2, 1600, 25, 6400, 50257))
-    assert low.grid_max == 256 and low.shared_bytes > LDS_BYTES
+    assert low.grid_max == 256 and low.shared_bytes <= LDS_BYTES
+
+
+def test_matrix_core_streams_beyond_16_rows():
+    """From 17 to 64 rows the products stay on the matrix cores: 16-row tiles
+    per weight fragment, the fold staged through LDS in chunks when the
+    halves of all rows do not fit, and fold splits over blocks whose tiles
+    go only to the seven compute waves (the eighth polls barriers and holds
+    no prefetched weights). GPT-2 XL at 64 rows fits a CU's LDS."""
+    from vesta.lower import LDS_BYTES
+    from vesta.mfma import MfmaMixin, MFMA_HALVES_MAX
+    assert MfmaMixin.mfma_rows(16, 24) == (1, 24, 1)
+    RT, CB, NC = MfmaMixin.mfma_rows(64, 50)
+    assert RT == 4 and CB * NC >= 50 and 2 * 64 * (CB * 64 + 16) <= MFMA_HALVES_MAX
+    for B, tmax, shape in ((32, 64, (2, 768, 12, 3072, 50257)), (64, 16, (2, 1600, 25, 6400, 50257))):
+        low = lower_gpt2(B, tmax, shape)
+        assert low.shared_bytes <= LDS_BYTES
+        pl = placements(low)
+        for name in ('qkv', 'oo', 'u', 'z2', 'logit'):
+            assert 'mfma' in pl[name], (B, name, pl[name])
+        waves = [min(int(w) for w in re.findall(r'wave < (\d+)', m))
+                 for m in re.findall(r'const bool mok_ = [^;]*;', low.src)]
+        assert waves and max(waves) <= 7, waves

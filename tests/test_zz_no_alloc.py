@@ -2,8 +2,9 @@
 the library's static per-device scratch in place of the kernel's S, bar and
 TS buffers) against the ordinary one (``vh_launch_cooperative``): the same
 tokens, cache rows and logits, bit for bit, on two calls in a row, the second
-with a smaller batch; and a kernel whose buffers exceed the static scratch is
-refused before anything is enqueued."""
+with a smaller batch; the same launch captured in a HIP graph and replayed;
+and a kernel whose buffers exceed the static scratch is refused before
+anything is enqueued."""
 import ctypes
 
 import numpy as np
@@ -86,3 +87,60 @@ def test_static_scratch_layout_and_limit():
     assert L.vh_noalloc_layout(2215552, 1280, 294912, ctypes.byref(bar), ctypes.byref(ts)) == 0   # B=8 kernel
     st = L.vh_noalloc_layout((8 << 20) - 256, 1280, 0, ctypes.byref(bar), ctypes.byref(ts))
     assert st == 20004 and b'exceed the static scratch' in L.vh_error_string(st)
+
+
+@pytest.mark.gpu
+def test_noalloc_launch_replays_from_a_hip_graph():
+    """After one eager call (which looks up the static scratch's address), the
+    fill kernel, the cooperative launch and the logits read of
+    ``launch_noalloc`` are captured on torch's capture stream and replayed
+    three times, each from the same restored state, with eager work and a
+    synchronisation between replays; every replay's tokens, cache rows,
+    position and logits equal the ordinary launch's bit for bit."""
+    torch = _torch()
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import RandomGPT2, random_prompts
+    print('noalloc graph: GPT-2 small B=2 tmax 64, 4 steps per launch', flush=True)
+    m = VestaGPT2(RandomGPT2('small', 0), batch=2, tmax=64, engine='persistent')
+    m.reset()
+    m.prefill(torch.from_numpy(random_prompts(2, 24, 50257, seed=5)).to('cuda', torch.int32))
+    torch.cuda.synchronize()
+    saved = [t.clone() for t in (m.x, m.t, m.keys, m.vals)]
+
+    def restore():
+        for dst, src in zip((m.x, m.t, m.keys, m.vals), saved):
+            dst.copy_(src)
+
+    steps = 4
+    tok_ref = torch.zeros(steps * 2, dtype=torch.int32, device='cuda')
+    m.k.launch(steps, tok_ref)
+    torch.cuda.synchronize()
+    m.check()
+    want = [tok_ref.cpu().numpy(), m.k.view('logit').reshape(-1).cpu().numpy(), m.keys.cpu().numpy(),
+            m.vals.cpu().numpy(), int(m.t.item())]
+
+    toks = torch.zeros(steps * 2, dtype=torch.int32, device='cuda')
+    logit = torch.zeros(2 * 50257, dtype=torch.float32, device='cuda')
+    restore()
+    m.k.launch_noalloc(steps, toks)                  # eager call: the scratch address is looked up here
+    torch.cuda.synchronize()
+    m.check()
+    restore()
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        m.k.launch_noalloc(steps, toks)
+        m.k.read_noalloc('logit', logit)
+    torch.cuda.synchronize()
+    for r in range(3):
+        restore()
+        toks.zero_()
+        logit.zero_()
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        m.check()
+        got = [toks.cpu().numpy(), logit.cpu().numpy(), m.keys.cpu().numpy(), m.vals.cpu().numpy(), int(m.t.item())]
+        for a, b in zip(want, got):
+            assert np.array_equal(np.asarray(a), np.asarray(b)), f'replay {r}'
+        print(f'replay {r}: tokens {got[0].tolist()} equal the ordinary launch', flush=True)

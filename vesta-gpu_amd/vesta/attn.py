@@ -30,6 +30,8 @@ import math
 
 ATTN_PREFETCH_SLOTS = 8      # cache rows per lane issued early (K and V each)
 ATTN_CHUNK = 4               # longer contexts: slots per chunk of the running (online) softmax
+ATTN_CHUNK_LOOP = 3          # from this many chunks, a run-time loop over two chunks' registers (unrolled,
+                             # the long chunk sequence spilled: GPT-2 small with a 1024-position cache)
 ATTN_ONLINE_SHORT = True     # shorter ones: the running softmax too, as one chunk of every slot (no block-wide
                              # maximum and sum)
 PROJ_MIN_REPLICAS = 2        # fuse the out-projection only if every leading point gets this many blocks
@@ -476,6 +478,25 @@ class AttnMixin:
             lines.append('}')
             return lines
 
+        def load_kv_at(tag, slot, lead_env, kd, vd):
+            """Lines loading K and V of the slot at C expression ``slot`` into
+            kd, vd (zeros where the position is out of range)."""
+            lines = [f'{{ const int s{tag}_ = ({slot}) * {PPP} + wave * {PPW} + sub_;']
+            env = slot_env(tag, lead_env)
+            env[at['E']] = ('(cl_ * 8)', 'int')
+            l1, a1 = row_index(c1.W, c1, env)
+            env4 = slot_env(tag, lead_env)
+            env4[at['E4']] = ('(cl_ * 8)', 'int')
+            l4, a4 = row_index(c4.W, c4, env4)
+            lines.append(f'  if (wave < {NW} && s{tag}_ < {T}) {{')
+            lines += ['    ' + x for x in l1 + l4]
+            lines.append(f'    {kd} = ldc16_h({rbK}, {a1});')
+            lines.append(f'    {vd} = ldc16_h({rbV}, {a4});')
+            lines.append(f'  }} else {{ {kd} = vh_u32x4{{0u, 0u, 0u, 0u}}; {vd} = vh_u32x4{{0u, 0u, 0u, 0u}}; }}')
+            lines.append('}')
+            return lines
+        self.load_kv_at = load_kv_at
+
         lane_decl = f'const int sub_ = lane / {LPE}, cl_ = lane % {LPE};'
         self.decls.append(f'vh_u32x4 {kq}[{NPS}];')
         self.decls.append(f'vh_u32x4 {vq}[{NPS}];')
@@ -730,7 +751,9 @@ class AttnMixin:
             # the first chunk's slots not loaded at the barrier
             for k in first:
                 o += [I + x for x in load_kv(k, lenv, False)]
-        for c in range(NCH):
+        if NCH >= ATTN_CHUNK_LOOP:
+            self.attn_chunk_loop(at, o, I, lenv, NPS, PPP, PPW, LPE, NW, T, kq, vq, slot_env, CH, NCH)
+        for c in (range(NCH) if NCH < ATTN_CHUNK_LOOP else ()):
             ks = list(range(c * CH, min(NPS, (c + 1) * CH)))
             nxt = [k for k in range((c + 1) * CH, min(NPS, (c + 2) * CH)) if k >= NPF]
             if nxt:
@@ -819,6 +842,64 @@ class AttnMixin:
         o.append(f'{I}vh_lds_sync();')
         self.mark(o, I, 'attention: combine')
         po_ref.append(po)
+
+    def attn_chunk_loop(self, at, o, I, lenv, NPS, PPP, PPW, LPE, NW, T, kq, vq, slot_env, CH, NCH):
+        """The chunks of ``attn_online`` as a run-time loop: the current
+        chunk's rows in kc_/vc_ (the first chunk's from kq/vq), the next
+        chunk's loaded into kn_/vn_ while the current one is used. The
+        operations and their order are those of the unrolled chunks."""
+        c1 = at['c1']
+        o.append(f'{I}vh_u32x4 kc_[{CH}], vc_[{CH}], kn_[{CH}], vn_[{CH}];')
+        for j in range(CH):
+            o.append(f'{I}kc_[{j}] = {kq}[{j}]; vc_[{j}] = {vq}[{j}];')
+        o.append(f'{I}for (int c_ = 0; c_ < {NCH}; ++c_) {{')
+        J0 = I + '  '
+        o.append(f'{J0}if ((c_ + 1) * {CH * PPP} < {T}) {{  // rows of the next chunk')
+        for j in range(CH):
+            o += [J0 + '  ' + x for x in self.load_kv_at(f'n{j}', f'(c_ + 1) * {CH} + {j}', lenv,
+                                                          f'kn_[{j}]', f'vn_[{j}]')]
+        o.append(f'{J0}}}')
+        o.append(f'{J0}if (c_ * {CH * PPP} < {T}) {{  // this chunk')
+        J = J0 + '  '
+        for j in range(CH):
+            k = f'c{j}'
+            o.append(f'{J}float sk{j}_;')
+            o.append(f'{J}{{ const int s{k}_ = (c_ * {CH} + {j}) * {PPP} + wave * {PPW} + sub_;')
+            o.append(f'{J}  float wf_[8];')
+            o.append(f'{J}  unpack8(kc_[{j}], wf_);')
+            o.append(f'{J}  float d_ = 0.0f;')
+            o.append(f'{J}  #pragma unroll')
+            o.append(f'{J}  for (int v_ = 0; v_ < 8; ++v_) d_ = fmaf(qv_[v_], wf_[v_], d_);')
+            o.append(f'{J}  d_ = group_red_sum(d_, {LPE});')
+            venv = dict(slot_env(k, lenv))
+            venv['__acc'] = ('d_', 'float')
+            pre = []
+            sv, st_ = self.expr(c1.epi, venv, pre, J + '  ')
+            o += pre
+            o.append(f'{J}  sk{j}_ = (wave < {NW} && s{k}_ < {T}) ? {self.as_float(sv, st_)} : -INFINITY;')
+            o.append(f'{J}}}')
+        o.append(f'{J}float mn_ = m_;')
+        for j in range(CH):
+            o.append(f'{J}mn_ = fmaxf(mn_, sk{j}_);')
+        o.append(f'{J}if (mn_ > -INFINITY) {{')
+        o.append(f'{J}  const float f_ = expf(m_ - mn_);')
+        o.append(f'{J}  l_ *= f_;')
+        o.append(f'{J}  #pragma unroll')
+        o.append(f'{J}  for (int v_ = 0; v_ < 8; ++v_) ov_[v_] *= f_;')
+        for j in range(CH):
+            o.append(f'{J}  {{ const float p_ = sk{j}_ > -INFINITY ? expf(sk{j}_ - mn_) : 0.0f;')
+            o.append(f'{J}    l_ += p_;')
+            o.append(f'{J}    float wf_[8];')
+            o.append(f'{J}    unpack8(vc_[{j}], wf_);')
+            o.append(f'{J}    #pragma unroll')
+            o.append(f'{J}    for (int v_ = 0; v_ < 8; ++v_) ov_[v_] = fmaf(p_, wf_[v_], ov_[v_]);')
+            o.append(f'{J}  }}')
+        o.append(f'{J}  m_ = mn_;')
+        o.append(f'{J}}}')
+        o.append(f'{J0}}}')
+        for j in range(CH):
+            o.append(f'{J0}kc_[{j}] = kn_[{j}]; vc_[{j}] = vn_[{j}];')
+        o.append(f'{I}}}')
 
     def _subst(self, e, repl):
         """e with reads of the named group values replaced by C variables:

@@ -30,6 +30,16 @@ RTC_OPTS = ('-O3', '-std=c++17', '-ffp-contract=off',
             '-mllvm', '-amdgpu-early-inline-all=true',
             '-Xclang', '-target-feature', '-Xclang', '-packed-fp32-ops')
 
+# Profiling only: issue the persistent kernels with an ordinary launch
+# (vh_launch) instead of a cooperative one, for runs under rocprofv3, whose
+# own teardown has ended in a segmentation fault after every run that made
+# cooperative launches. The kernel is the same; its grid barriers still need
+# every block resident, which holds on an otherwise idle device (the grid is
+# at most one block per CU, checked at construction). Were a block not
+# resident, the barrier's bounded wait would set error code 1 and every
+# block would exit, so the launch ends either way; check() then raises.
+PLAIN_LAUNCH = os.environ.get('VESTA_PLAIN_LAUNCH', '') == '1'
+
 _lib = None
 _lib_lock = threading.Lock()
 
@@ -334,6 +344,9 @@ class Kernel:
         if per_cu * self.cus < lowered.grid_max:
             raise RuntimeError(f'the kernel is laid out for {lowered.grid_max} resident blocks; this device holds '
                                f'{per_cu} per CU x {self.cus} CUs')
+        if PLAIN_LAUNCH and lowered.grid_max > self.cus:
+            raise RuntimeError(f'VESTA_PLAIN_LAUNCH needs at most one block per CU: {lowered.grid_max} blocks, '
+                               f'{self.cus} CUs')
         self.grid = lowered.grid_max
         self.block = block
         regs, slds, priv, mxb = (ctypes.c_int() for _ in range(4))
@@ -425,8 +438,12 @@ class Kernel:
         1..steps-1 (the first step reads the residue as usual)."""
         self._steps_and_tokens(steps, tokens, inputs, 'launch')
         stream = _torch().cuda.current_stream().cuda_stream
-        ok(lib().vh_launch_cooperative(self.fn, self.grid, self.block, self.smem, ctypes.c_void_p(stream), self.args),
-           'cooperative launch')
+        if PLAIN_LAUNCH:
+            ok(lib().vh_launch(self.fn, self.grid, self.block, self.smem, ctypes.c_void_p(stream), self.args),
+               'launch (VESTA_PLAIN_LAUNCH, profiling)')
+        else:
+            ok(lib().vh_launch_cooperative(self.fn, self.grid, self.block, self.smem, ctypes.c_void_p(stream),
+                                           self.args), 'cooperative launch')
         self._noalloc_bar = None
 
     def __call__(self, residue):
@@ -441,6 +458,8 @@ class Kernel:
         word of such a launch is in the static scratch's barrier block:
         ``check()`` reads it there."""
         self._steps_and_tokens(steps, tokens, inputs, 'launch_noalloc')
+        if PLAIN_LAUNCH:
+            raise RuntimeError('launch_noalloc is cooperative only (unset VESTA_PLAIN_LAUNCH)')
         sizes = (self.S.numel() * 4, self.bar.numel() * 4, self.TS.numel() * 8)
         bar_off, ts_off = ctypes.c_size_t(), ctypes.c_size_t()
         ok(lib().vh_noalloc_layout(*sizes, ctypes.byref(bar_off), ctypes.byref(ts_off)), 'static scratch layout')

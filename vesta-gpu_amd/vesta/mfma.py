@@ -28,7 +28,7 @@ streamed through two register sets of ``mfma_pipe`` k-blocks each.
 """
 from __future__ import annotations
 
-from .analysis import top_folds
+from .analysis import LowerError, top_folds
 
 MFMA_ROWS_MIN = 4            # rows from which a stream runs on the matrix cores
 MFMA_PIPES = (2, 1)          # k-blocks of weights per register set when not prefetched (two sets: the
@@ -37,16 +37,50 @@ MFMA_PIPES = (2, 1)          # k-blocks of weights per register set when not pre
                              # step at 2, 324.6 at 1, equal tokens and logits; 3 spills 57 registers at
                              # the full budget
 MFMA_POINTS_MIN = 8          # points a block must make (of a tile's 16 columns)
+MFMA_ROWS_MAX = 64           # rows a stream may take: beyond 16, in 16-row tiles (each a tile of its own)
+MFMA_HALVES_MAX = 96 * 1024  # bytes of LDS the fp16 halves of the other factor take at most beyond 16 rows
+                             # (the fold then goes through LDS in chunks of whole 32-deep k-blocks)
+SPLIT_ADD_BYTES = 32         # beyond 16 rows, the cost of one fixed-point add of a fold split in bytes read
 
 
 class MfmaMixin:
-    def mfma_ok(self, c, st):
+    def mfma_ok(self, c, st, points=True):
         """Can stream st (of contraction c) run on the matrix cores, with at
-        least half of a tile's 16 columns holding points of the block?"""
+        least half of a tile's 16 columns holding points of the block (unless
+        ``points`` is off: a fold split over blocks sets its own points)?"""
         R = self.size(c.reg_axes)
         PPB = -(-self.size(st.pts) // self.grid)
-        return (self.res[st.src][1] == 'f16' and MFMA_ROWS_MIN <= R <= 16 and st.K % 32 == 0
-                and st.c0 % 8 == 0 and st.rowlen % 8 == 0 and PPB >= MFMA_POINTS_MIN)
+        if not (self.res[st.src][1] == 'f16' and MFMA_ROWS_MIN <= R <= MFMA_ROWS_MAX and st.K % 32 == 0
+                and st.c0 % 8 == 0 and st.rowlen % 8 == 0 and (PPB >= MFMA_POINTS_MIN or not points)):
+            return False
+        # beyond one row tile the other factor is split into halves chunk by
+        # chunk from where it lives: a value laid out [rows, fold], read at
+        # exactly those axes (``mfma_reachable`` confirms where it is stored)
+        if R <= 16:
+            return True
+        A, want = c.A, list(c.reg_axes) + list(c.fold_axes)
+        return (A[0] == 'idx' and A[1] in self.axes_of and list(self.axes_of[self.root(A[1])]) == want
+                and list(A[2]) == [('name', a) for a in want])
+
+    def mfma_reachable(self, c, st):
+        """At code generation: a stream of more than 16 rows reads its other
+        factor in place, from LDS (private) or as plain fp32 global scratch."""
+        return (self.size(c.reg_axes) <= 16 or self.direct_lds(c, c.reg_axes) is not None
+                or self.mfma_global_src(c, c.reg_axes, st.K) is not None)
+
+    @staticmethod
+    def mfma_rows(R, nkb):
+        """(row tiles, k-blocks per fold chunk, fold chunks) of a stream of R
+        rows over nkb k-blocks: up to 16 rows one tile and the whole fold;
+        beyond, 16-row tiles and, when the halves of all rows over the whole
+        fold exceed MFMA_HALVES_MAX bytes, chunks of the fold that fit."""
+        if R <= 16:
+            return 1, nkb, 1
+        RT = -(-R // 16)
+        if 2 * R * (nkb * 64 + 16) <= MFMA_HALVES_MAX:
+            return RT, nkb, 1
+        cb = max(1, (MFMA_HALVES_MAX // (2 * R) - 16) // 64)
+        return RT, cb, -(-nkb // cb)
 
     def gen_stream_mfma(self, s, c, st, fused, out, ind):
         name = s[1]
@@ -63,16 +97,17 @@ class MfmaMixin:
         reg = c.reg_axes
         R = self.size(reg)
         NT = -(-PPB // 16)
+        RT, CB, NC = self.mfma_rows(R, NKB)   # row tiles (each tile's accumulators); k-blocks per fold chunk, chunks
         if NT >= NW:
             TPW, KW = -(-NT // NW), 1
         else:
             TPW, KW = 1, NW // NT
-        KBW = -(-NKB // KW)
-        prefetch = TPW * KBW * 4 <= self.pf_budget
+        KBW = -(-CB // KW)
+        prefetch = NC == 1 and TPW * KBW * 4 <= self.pf_budget
         sid = self.fresh('m')
         CT = NW * 64                          # the epilogue: one (row, point) item per compute thread
         NI = -(-(R * PPB) // CT)
-        geo = dict(P=P, PPB=PPB, NW=NW, NT=NT, TPW=TPW, KW=KW, NKB=NKB, KBW=KBW, R=R, reg=list(reg), CT=CT)
+        geo = dict(P=P, PPB=PPB, NW=NW, NT=NT, TPW=TPW, KW=KW, NKB=CB, KBW=KBW, R=R, reg=list(reg), CT=CT)
         rr = self.rsrc(st.src)
         rs = self.res_strides(st.src)
         w16 = self.w16('stream')
@@ -128,6 +163,7 @@ class MfmaMixin:
                     self.decls.append(f'{self.cap_ctype(k)} {n};')
         o.append(f'{ind}{{  // stream {name} on the matrix cores: {P} points x {K} from {st.src}, rows={R}, '
                  f'points/block={PPB}, tiles={NT}, tiles/wave={TPW}, waves/tile={KW}'
+                 + (f', {RT} row tiles, fold in {NC} chunks of {CB} k-blocks' if RT > 1 else '')
                  + (' prefetched' if prefetch else ''))
         o += [I + x for x in self.mfma_role(geo)]
         self.stream_part[self.root(name)] = dict(pts=list(st.pts), PPB=PPB, P=P, reg=list(reg))
@@ -140,18 +176,19 @@ class MfmaMixin:
             if src is None:
                 self.stage_A(c, reg, 0, R, R, K, str(top), o, I)
                 direct, top = str(top), top + R * K
-        SAB = K * 2 + 16                      # bytes per row of a half array (padded against bank conflicts)
+        SAB = CB * 64 + 16                    # bytes per row of a half array (padded against bank conflicts)
         packed = R <= 8                       # hi rows 0-7 and lo rows 8-15 of one A tile
         ah = top * 4
         al = ah + (8 if packed else R) * SAB
         top = (al + R * SAB) // 4
         red = top
         if KW > 1:
-            top += NW * 64 * 4
+            top += NW * 64 * 4 * RT
         accb = top                            # the sums, [row][own point]
         top += -(-R * PPB // 4) * 4
-        self.mfma_split(direct, src, R, K, SAB, ah, al, o, I, scaled=packed)
-        self.mark(o, I, f'stream {name}: halves')
+        if NC == 1:
+            self.mfma_split(direct, src, R, K, SAB, ah, al, o, I, scaled=packed)
+            self.mark(o, I, f'stream {name}: halves')
         # values of the site (as in the other streams)
         fused_ids = {id(t) for _, t, _ in fused}
         made = [s] + [t for kind, t, _ in fused if kind == 'let']
@@ -165,54 +202,83 @@ class MfmaMixin:
             top += -(-R * PPB // 4) * 4
         self.stage_floats = max(self.stage_floats, top - self.lds_floats)
         # the products
-        o.append(f'{I}vh_f32x4 acc_[{TPW}];')
-        o.append(f'{I}#pragma unroll')
-        o.append(f'{I}for (int i_ = 0; i_ < {TPW}; ++i_) acc_[i_] = vh_f32x4{{0.f, 0.f, 0.f, 0.f}};')
+        if RT == 1:
+            o.append(f'{I}vh_f32x4 acc_[{TPW}];')
+            o.append(f'{I}#pragma unroll')
+            o.append(f'{I}for (int i_ = 0; i_ < {TPW}; ++i_) acc_[i_] = vh_f32x4{{0.f, 0.f, 0.f, 0.f}};')
+        else:
+            self.mfma_acc_rows(TPW, RT, o, I)
 
         def kstep(kb, wsrc, J):
             """Lines of one k-block (C expression kb, relative to mk0_) from weight registers wsrc(i)."""
             if packed:
                 return self.mfma_kstep_packed(f'mk0_ + {kb}', wsrc, TPW, R, SAB, ah, J)
-            lines = [f'{J}{{ const int kb_ = mk0_ + {kb};',
-                     f'{J}  const int ar_ = lane & 15, ak_ = kb_ * 32 + (lane >> 4) * 8;',
-                     f'{J}  const vh_u32x4 ah_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {ah} + ar_ * {SAB} + ak_ * 2) '
-                     f': vh_u32x4{{0u, 0u, 0u, 0u}};',
-                     f'{J}  const vh_u32x4 al_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {al} + ar_ * {SAB} + ak_ * 2) '
-                     f': vh_u32x4{{0u, 0u, 0u, 0u}};']
-            for i in range(TPW):
-                lines.append(f'{J}  acc_[{i}] = vh_mfma(ah_, {wsrc(i)}, acc_[{i}]);')
-                lines.append(f'{J}  acc_[{i}] = vh_mfma(al_, {wsrc(i)}, acc_[{i}]);')
-            lines.append(f'{J}}}')
-            return lines
+            if RT == 1:
+                lines = [f'{J}{{ const int kb_ = mk0_ + {kb};',
+                         f'{J}  const int ar_ = lane & 15, ak_ = kb_ * 32 + (lane >> 4) * 8;',
+                         f'{J}  const vh_u32x4 ah_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {ah} + ar_ * {SAB} + ak_ * 2) '
+                         f': vh_u32x4{{0u, 0u, 0u, 0u}};',
+                         f'{J}  const vh_u32x4 al_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {al} + ar_ * {SAB} + ak_ * 2) '
+                         f': vh_u32x4{{0u, 0u, 0u, 0u}};']
+                for i in range(TPW):
+                    lines.append(f'{J}  acc_[{i}] = vh_mfma(ah_, {wsrc(i)}, acc_[{i}]);')
+                    lines.append(f'{J}  acc_[{i}] = vh_mfma(al_, {wsrc(i)}, acc_[{i}]);')
+                lines.append(f'{J}}}')
+                return lines
+            # row tiles: every weight fragment multiplies each 16-row tile; the
+            # halves in LDS hold the current fold chunk (columns from ck0_)
+            return self.mfma_kstep_rows(f'mk0_ + {kb}', ' - ck0_' if NC > 1 else '', wsrc, TPW, RT, R, SAB,
+                                        ah, al, J)
 
-        o.append(f'{I}if (mok_) {{')
-        J = I + '  '
-        if prefetch:
-            for j in range(KBW):
-                o.append(f'{J}if (mk0_ + {j} < mk1_)')
-                o += kstep(str(j), lambda i, j=j: f'{wm}[{i}][{j}]', J + '  ')
-        else:
+        def streamed(J):
+            """The wave's k-blocks [mk0_, mk1_) with weights streamed through two register sets."""
             D = self.mfma_pipe
             o.append(f'{J}vh_u32x4 wb0_[{TPW}][{D}], wb1_[{TPW}][{D}];')
             for i in range(TPW):
                 for d in range(D):
-                    o += [J + x for x in wload(i, f'mk0_ + {d}', f'wb0_[{i}][{d}]', f'mk0_ + {d} < mk1_')]
+                    o.extend(J + x for x in wload(i, f'mk0_ + {d}', f'wb0_[{i}][{d}]', f'mk0_ + {d} < mk1_'))
             o.append(f'{J}for (int c0_ = 0; c0_ < {KBW}; c0_ += {2 * D}) {{')
             J2 = J + '  '
             for half, (cur, nxt) in enumerate((('wb0_', 'wb1_'), ('wb1_', 'wb0_'))):
                 ahead = f'c0_ + {(half + 1) * D}'
                 for i in range(TPW):
                     for d in range(D):
-                        o += [J2 + x for x in wload(i, f'mk0_ + {ahead} + {d}', f'{nxt}[{i}][{d}]',
-                                                    f'mk0_ + {ahead} + {d} < mk1_')]
+                        o.extend(J2 + x for x in wload(i, f'mk0_ + {ahead} + {d}', f'{nxt}[{i}][{d}]',
+                                                       f'mk0_ + {ahead} + {d} < mk1_'))
                 for d in range(D):
                     kb = f'c0_ + {half * D + d}'
                     o.append(f'{J2}if (mk0_ + {kb} < mk1_)')
-                    o += kstep(kb, lambda i, cur=cur, d=d: f'{cur}[{i}][{d}]', J2 + '  ')
+                    o.extend(kstep(kb, lambda i, cur=cur, d=d: f'{cur}[{i}][{d}]', J2 + '  '))
             o.append(f'{J}}}')
-        o.append(f'{I}}}')
+
+        if NC == 1:
+            o.append(f'{I}if (mok_) {{')
+            J = I + '  '
+            if prefetch:
+                for j in range(KBW):
+                    o.append(f'{J}if (mk0_ + {j} < mk1_)')
+                    o += kstep(str(j), lambda i, j=j: f'{wm}[{i}][{j}]', J + '  ')
+            else:
+                streamed(J)
+            o.append(f'{I}}}')
+        else:
+            # the fold in chunks: each chunk's halves into LDS, then every wave
+            # takes its part of the chunk's k-blocks (parts in the same order
+            # in every chunk, so each wave's sum covers the same part of each)
+            o.append(f'{I}for (int ch_ = 0; ch_ < {NC}; ++ch_) {{')
+            J0 = I + '  '
+            o.append(f'{J0}const int ck0_ = ch_ * {CB}, ckn_ = min({CB}, {NKB} - ck0_);')
+            self.mfma_split_chunk(direct, src, R, K, SAB, ah, al, o, J0)
+            o.append(f'{J0}if (mok_) {{')
+            J = J0 + '  '
+            o.append(f'{J}const int mk0_ = ck0_ + mkp_ * ckn_ / {KW}, mk1_ = ck0_ + (mkp_ + 1) * ckn_ / {KW};')
+            streamed(J)
+            o.append(f'{J0}}}')
+            o.append(f'{I}}}')
         self.mark(o, I, f'stream {name}: products')
-        if KW > 1:
+        if KW > 1 and RT > 1:
+            self.mfma_parts_rows(KW, NT, RT, red, o, I)
+        elif KW > 1:
             # partial tiles of the later parts of the fold, added in part order
             o.append(f'{I}if (mok_ && mkp_ > 0) *(vh_f32x4*)(sh_f + {red} + (wave * 64 + lane) * 4) = acc_[0];')
             o.append(f'{I}vh_lds_sync();')
@@ -231,8 +297,13 @@ class MfmaMixin:
             o.append(f'{I}    if (({self.mfma_tile(geo, i)}) < {NT} && n_ < {PPB}) {{')
             o.append(f'{I}      #pragma unroll')
             o.append(f'{I}      for (int v_ = 0; v_ < 4; ++v_) {{')
-            o.append(f'{I}        const int r_ = (lane >> 4) * 4 + v_;')
-            o.append(f'{I}        if (r_ < {R}) sh_f[{accb} + r_ * {PPB} + n_] = acc_[{i}][v_];')
+            if RT == 1:
+                o.append(f'{I}        const int r_ = (lane >> 4) * 4 + v_;')
+                o.append(f'{I}        if (r_ < {R}) sh_f[{accb} + r_ * {PPB} + n_] = acc_[{i}][v_];')
+            else:
+                for rt in range(RT):
+                    o.append(f'{I}        {{ const int r_ = {rt * 16} + (lane >> 4) * 4 + v_;')
+                    o.append(f'{I}          if (r_ < {R}) sh_f[{accb} + r_ * {PPB} + n_] = acc_[{i}][{rt}][v_]; }}')
             o.append(f'{I}      }}')
             o.append(f'{I}    }}')
             o.append(f'{I}  }}')
@@ -355,6 +426,82 @@ class MfmaMixin:
         o.append(f'{I}}}')
         o.append(f'{I}vh_lds_sync();')
 
+    @staticmethod
+    def mfma_acc_rows(TPW, RT, o, I):
+        """Accumulators of TPW column tiles x RT row tiles."""
+        o.append(f'{I}vh_f32x4 acc_[{TPW}][{RT}];')
+        o.append(f'{I}#pragma unroll')
+        o.append(f'{I}for (int i_ = 0; i_ < {TPW}; ++i_)')
+        o.append(f'{I}  #pragma unroll')
+        o.append(f'{I}  for (int r_ = 0; r_ < {RT}; ++r_) acc_[i_][r_] = vh_f32x4{{0.f, 0.f, 0.f, 0.f}};')
+
+    @staticmethod
+    def mfma_kstep_rows(kb, rel, wsrc, TPW, RT, R, SAB, ah, al, J):
+        """One k-block (C expression kb; its LDS column ``kb{rel}``) of TPW
+        column tiles over RT row tiles: lane l reads rows rt * 16 + l % 16 of
+        the hi and lo arrays, and each weight fragment meets every row tile."""
+        lines = [f'{J}{{ const int kb_ = {kb};',
+                 f'{J}  const int ak_ = (kb_{rel}) * 32 + (lane >> 4) * 8;',
+                 f'{J}  vh_u32x4 ah_[{RT}], al_[{RT}];',
+                 f'{J}  #pragma unroll',
+                 f'{J}  for (int rt_ = 0; rt_ < {RT}; ++rt_) {{',
+                 f'{J}    const int ar_ = rt_ * 16 + (lane & 15);',
+                 f'{J}    ah_[rt_] = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {ah} + ar_ * {SAB} + ak_ * 2) '
+                 f': vh_u32x4{{0u, 0u, 0u, 0u}};',
+                 f'{J}    al_[rt_] = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {al} + ar_ * {SAB} + ak_ * 2) '
+                 f': vh_u32x4{{0u, 0u, 0u, 0u}};',
+                 f'{J}  }}']
+        for i in range(TPW):
+            lines += [f'{J}  #pragma unroll',
+                      f'{J}  for (int rt_ = 0; rt_ < {RT}; ++rt_) {{',
+                      f'{J}    acc_[{i}][rt_] = vh_mfma(ah_[rt_], {wsrc(i)}, acc_[{i}][rt_]);',
+                      f'{J}    acc_[{i}][rt_] = vh_mfma(al_[rt_], {wsrc(i)}, acc_[{i}][rt_]);',
+                      f'{J}  }}']
+        lines.append(f'{J}}}')
+        return lines
+
+    @staticmethod
+    def mfma_parts_rows(KW, NT, RT, red, o, I):
+        """Partial tiles (all row tiles) of the later parts of the fold added
+        to the first part's, in part order, through LDS (one tile per wave)."""
+        o.append(f'{I}if (mok_ && mkp_ > 0) {{')
+        for rt in range(RT):
+            o.append(f'{I}  *(vh_f32x4*)(sh_f + {red} + ((wave * {RT} + {rt}) * 64 + lane) * 4) = acc_[0][{rt}];')
+        o.append(f'{I}}}')
+        o.append(f'{I}vh_lds_sync();')
+        o.append(f'{I}if (mok_ && mkp_ == 0) {{')
+        for q in range(1, KW):
+            for rt in range(RT):
+                o.append(f'{I}  acc_[0][{rt}] += *(const vh_f32x4*)(sh_f + {red} + (((wave + {q * NT}) * {RT} + {rt}) * 64 '
+                         f'+ lane) * 4);')
+        o.append(f'{I}}}')
+
+    def mfma_split_chunk(self, direct, src, R, K, SAB, ah, al, o, I):
+        """The fold chunk of k-blocks [ck0_, ck0_ + ckn_) (C variables) of the
+        other factor (R rows x K fp32, in LDS at float offset ``direct`` or in
+        global scratch at ``src``) into fp16 hi and lo halves in LDS, chunk
+        column 0 first."""
+        o.append(f'{I}vh_lds_sync();')
+        o.append(f'{I}for (int e_ = tid; e_ < {R} * ckn_ * 4; e_ += {self.BLOCK}) {{')
+        o.append(f'{I}  const int r_ = e_ / (ckn_ * 4), k8_ = e_ - r_ * (ckn_ * 4);')
+        o.append(f'{I}  const int col_ = ck0_ * 32 + k8_ * 8;')
+        o.append(f'{I}  float v_[8];')
+        if direct is not None:
+            o.append(f'{I}  const float* s_ = sh_f + {direct} + r_ * {K} + col_;')
+            o.append(f'{I}  {self.lds_vec_load(8, "s_", "v_")}')
+        else:
+            o.append(f'{I}  const vh_f32x4 x0_ = ldc4(rb_S, {src}u + (unsigned)(r_ * {K} + col_)), '
+                     f'x1_ = ldc4(rb_S, {src}u + (unsigned)(r_ * {K} + col_ + 4));')
+            o.append(f'{I}  v_[0] = x0_.x; v_[1] = x0_.y; v_[2] = x0_.z; v_[3] = x0_.w; '
+                     f'v_[4] = x1_.x; v_[5] = x1_.y; v_[6] = x1_.z; v_[7] = x1_.w;')
+        o.append(f'{I}  vh_u32x4 h_, l_;')
+        o.append(f'{I}  vh_split8(v_, h_, l_);')
+        o.append(f'{I}  if (vh_beyond_half8(v_)) stc_u(bar + VH_BAR_ERROR, VH_ERR_RANGE);')
+        o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {ah} + r_ * {SAB} + k8_ * 16) = h_;')
+        o.append(f'{I}  *(vh_u32x4*)((char*)sh_f + {al} + r_ * {SAB} + k8_ * 16) = l_;')
+        o.append(f'{I}}}')
+        o.append(f'{I}vh_lds_sync();')
+
     # ------------------------------------------------------------ fold split over blocks
     def split_of(self, s):
         """A multi-row stream with too few points per block for a matrix tile
@@ -373,8 +520,10 @@ class MfmaMixin:
         name, r = s[1], self.root(s[1])
         R = self.size(c.reg_axes)
         P = self.size(st.pts)
-        if not (self.res[st.src][1] == 'f16' and MFMA_ROWS_MIN <= R <= 16 and st.K % 32 == 0
+        if not (self.res[st.src][1] == 'f16' and MFMA_ROWS_MIN <= R <= MFMA_ROWS_MAX and st.K % 32 == 0
                 and st.c0 % 8 == 0 and st.rowlen % 8 == 0):
+            return None
+        if R > 16 and not self.mfma_ok(c, st, points=False):
             return None
         if -(-P // self.grid) >= MFMA_POINTS_MIN:
             return None
@@ -389,13 +538,19 @@ class MfmaMixin:
         # point groups of NTS tiles, the fold in KS slices: the fewest bytes per block
         NKB, K = st.K // 32, st.K
         best = None
-        for NTS in range(1, 5):
+        for NTS in range(1, 5 if R <= 16 else 17):
             NPG = -(-P // (16 * NTS))
             KS = min(self.grid // NPG, NKB)
             if KS < 2:
                 continue
             KSL = -(-NKB // KS)
             cost = R * KSL * 32 * 4 + 16 * NTS * KSL * 32 * 2
+            if R > 16:
+                # the halves of the block's slice must fit, and every block adds
+                # R x its points into the sum (KS adds meet at each address)
+                if 2 * R * (KSL * 64 + 16) > MFMA_HALVES_MAX:
+                    continue
+                cost += R * 16 * NTS * SPLIT_ADD_BYTES
             if best is None or cost < best[0]:
                 best = (cost, NTS, NPG, KS, KSL)
         if best is None:
@@ -458,6 +613,7 @@ class MfmaMixin:
         R, P, K, NKB = self.size(reg), self.size(st.pts), st.K, st.K // 32
         NTS, NPG, KS, KSL, PG = sk['NTS'], sk['NPG'], sk['KS'], sk['KSL'], sk['PG']
         NW = self.NWAVE - 1
+        RT = 1 if R <= 16 else -(-R // 16)    # row tiles (each tile's accumulators)
         if NTS >= NW:
             TPW, KW = -(-NTS // NW), 1
         else:
@@ -491,7 +647,7 @@ class MfmaMixin:
         rr, rs = self.rsrc(st.src), self.res_strides(st.src)
         role = [f'const int sg_ = (int)blockIdx.x / {KS}, ss_ = (int)blockIdx.x % {KS};',
                 f'const int kb0_ = ss_ * {NKB} / {KS}, nk_ = (ss_ + 1) * {NKB} / {KS} - kb0_;',
-                f'const bool mok_ = (int)blockIdx.x < {NPG * KS} && wave < {NTS * KW};',
+                f'const bool mok_ = (int)blockIdx.x < {NPG * KS} && wave < {min(NTS * KW, NW)};',
                 f'const int mkp_ = wave / {NTS}, mt_ = wave % {NTS};' if KW > 1 else
                 f'const int mkp_ = 0, mt_ = wave;',
                 f'const int mk0_ = mkp_ * nk_ / {KW}, mk1_ = (mkp_ + 1) * nk_ / {KW};']
@@ -536,6 +692,8 @@ class MfmaMixin:
         direct = self.direct_lds(c, reg)
         src = None if direct is not None else self.mfma_global_src(c, reg, K)
         if direct is None and src is None:
+            if RT > 1:
+                raise LowerError(f'split {name}: beyond 16 rows the other factor must be a plain value')
             self.stage_A(c, reg, 0, R, R, K, str(top), o, I)
             direct, top = str(top), top + R * K
         SAB = KSL * 64 + 16
@@ -544,7 +702,7 @@ class MfmaMixin:
         al = ah + (8 if packed else R) * SAB
         top = (al + R * SAB) // 4
         red = top
-        top += NW * 64 * 4 if KW > 1 else 0
+        top += NW * 64 * 4 * RT if KW > 1 else 0
         self.stage_floats = max(self.stage_floats, top - self.lds_floats)
         # the block's slice of the other factor into fp16 halves
         K8 = KSL * 4
@@ -571,9 +729,12 @@ class MfmaMixin:
         o.append(f'{I}}}')
         o.append(f'{I}vh_lds_sync();')
         self.mark(o, I, f'stream {name}: halves')
-        o.append(f'{I}vh_f32x4 acc_[{TPW}];')
-        o.append(f'{I}#pragma unroll')
-        o.append(f'{I}for (int i_ = 0; i_ < {TPW}; ++i_) acc_[i_] = vh_f32x4{{0.f, 0.f, 0.f, 0.f}};')
+        if RT == 1:
+            o.append(f'{I}vh_f32x4 acc_[{TPW}];')
+            o.append(f'{I}#pragma unroll')
+            o.append(f'{I}for (int i_ = 0; i_ < {TPW}; ++i_) acc_[i_] = vh_f32x4{{0.f, 0.f, 0.f, 0.f}};')
+        else:
+            self.mfma_acc_rows(TPW, RT, o, I)
         o.append(f'{I}if (mok_) {{')
         for j in range(KBW):
             if packed:
@@ -582,6 +743,11 @@ class MfmaMixin:
                                             I + '    ')
                 continue
             o.append(f'{I}  if (mk0_ + {j} < mk1_) {{')
+            if RT > 1:
+                o += self.mfma_kstep_rows(f'mk0_ + {j}', '', lambda i, j=j: f'{wm}[{i}][{j}]', TPW, RT, R, SAB,
+                                          ah, al, I + '    ')
+                o.append(f'{I}  }}')
+                continue
             o.append(f'{I}    const int ar_ = lane & 15, ak_ = (mk0_ + {j}) * 32 + (lane >> 4) * 8;')
             o.append(f'{I}    const vh_u32x4 ah_ = ar_ < {R} ? *(const vh_u32x4*)((const char*)sh_f + {ah} + ar_ * {SAB} '
                      f'+ ak_ * 2) : vh_u32x4{{0u, 0u, 0u, 0u}};')
@@ -593,7 +759,9 @@ class MfmaMixin:
             o.append(f'{I}  }}')
         o.append(f'{I}}}')
         self.mark(o, I, f'stream {name}: products')
-        if KW > 1:
+        if KW > 1 and RT > 1:
+            self.mfma_parts_rows(KW, NTS, RT, red, o, I)
+        elif KW > 1:
             o.append(f'{I}if (mok_ && mkp_ > 0) *(vh_f32x4*)(sh_f + {red} + (wave * 64 + lane) * 4) = acc_[0];')
             o.append(f'{I}vh_lds_sync();')
             o.append(f'{I}if (mok_ && mkp_ == 0) {{')
@@ -609,6 +777,15 @@ class MfmaMixin:
             o.append(f'{I}    if (({tile(i)}) < {NTS} && p_ < {P}) {{')
             o.append(f'{I}      #pragma unroll')
             o.append(f'{I}      for (int v_ = 0; v_ < 4; ++v_) {{')
+            if RT > 1:
+                for rt in range(RT):
+                    o.append(f'{I}        {{ const int r_ = {rt * 16} + (lane >> 4) * 4 + v_;')
+                    o.append(f'{I}          if (r_ < {R}) fxadd(S, {self.gadd(z)} + 2u * (unsigned)(r_ * {P} + p_), '
+                             f'acc_[{i}][{rt}][v_]); }}')
+                o.append(f'{I}      }}')
+                o.append(f'{I}    }}')
+                o.append(f'{I}  }}')
+                continue
             o.append(f'{I}        const int r_ = (lane >> 4) * 4 + v_;')
             o.append(f'{I}        if (r_ < {R}) fxadd(S, {self.gadd(z)} + 2u * (unsigned)(r_ * {P} + p_), acc_[{i}][v_]);')
             o.append(f'{I}      }}')

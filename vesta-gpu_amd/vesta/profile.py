@@ -128,3 +128,65 @@ def main():
 
 if __name__ == '__main__':
     main()
+
+
+# ------------------------------------------------------------------ device read bandwidth
+READ_PROBE_SRC = r'''
+typedef unsigned int vh_u32x4 __attribute__((ext_vector_type(4)));
+// Streaming read of n16 16-byte words: every lane issues four nontemporal
+// 16-byte loads per round (consecutive lanes, consecutive words), folding
+// them into one XOR so no load is dead; one store if the fold hits a value
+// the data never gives.
+extern "C" __global__ __launch_bounds__(256) void vesta_read_probe(const vh_u32x4* __restrict__ p,
+                                                                   unsigned long long n16,
+                                                                   unsigned* __restrict__ out) {
+  const unsigned long long stride = (unsigned long long)gridDim.x * 256ull;
+  unsigned long long i = (unsigned long long)blockIdx.x * 256ull + threadIdx.x;
+  vh_u32x4 acc = {0u, 0u, 0u, 0u};
+  for (; i + 3 * stride < n16; i += 4 * stride) {
+    const vh_u32x4 a = __builtin_nontemporal_load(p + i), b = __builtin_nontemporal_load(p + i + stride);
+    const vh_u32x4 c = __builtin_nontemporal_load(p + i + 2 * stride), d = __builtin_nontemporal_load(p + i + 3 * stride);
+    acc ^= a ^ b ^ c ^ d;
+  }
+  for (; i < n16; i += stride) acc ^= __builtin_nontemporal_load(p + i);
+  if ((acc.x ^ acc.y ^ acc.z ^ acc.w) == 0x9e3779b9u) out[0] = 1u;
+}
+'''
+
+
+def stream_read_GBs(nbytes=512 << 20, blocks_per_cu=8, reps=20):
+    """HBM read bandwidth of this device with the repository's own streaming
+    read (``READ_PROBE_SRC``: 16-byte nontemporal loads, four in flight per
+    lane), best of ``reps`` launches timed with HIP events on the launch
+    stream; the buffer is ``nbytes`` of random data (well beyond the caches
+    at the default 512 MB)."""
+    import ctypes
+    import torch
+    from . import launch
+    L = launch.lib()
+    code = launch.compile_code(READ_PROBE_SRC)
+    mod, fn = ctypes.c_void_p(), ctypes.c_void_p()
+    launch.ok(L.vh_module_load(code, ctypes.byref(mod)), 'read probe load')
+    try:
+        launch.ok(L.vh_module_get_function(mod, b'vesta_read_probe', ctypes.byref(fn)), 'read probe function')
+        n16 = nbytes // 16
+        buf = torch.randint(-2 ** 31, 2 ** 31 - 1, (n16 * 4,), dtype=torch.int32, device='cuda')
+        out = torch.zeros(1, dtype=torch.int32, device='cuda')
+        grid = launch.device_info()['cu_count'] * blocks_per_cu
+        vals = [ctypes.c_void_p(buf.data_ptr()), ctypes.c_ulonglong(n16), ctypes.c_void_p(out.data_ptr())]
+        args = (ctypes.c_void_p * 3)(*[ctypes.cast(ctypes.pointer(v), ctypes.c_void_p) for v in vals])
+        stream = torch.cuda.current_stream()
+        best = None
+        for r in range(reps + 3):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record(stream)
+            launch.ok(L.vh_launch(fn, grid, 256, 0, ctypes.c_void_p(stream.cuda_stream), args), 'read probe')
+            e1.record(stream)
+            e1.synchronize()
+            if r >= 3:
+                ms = e0.elapsed_time(e1)
+                best = ms if best is None else min(best, ms)
+        del buf, out
+        return round(n16 * 16 / (best * 1e-3) / 1e9, 1)
+    finally:
+        launch.unload(mod)

@@ -164,7 +164,7 @@ class StreamMixin:
 
     # ------------------------------------------------------------ codegen
     def gen_stream(self, s, c, st, fused, out, ind):
-        if self.mfma_ok(c, st):
+        if self.mfma_ok(c, st) and self.mfma_reachable(c, st):
             return self.gen_stream_mfma(s, c, st, fused, out, ind)
         name = s[1]
         ch = self.chain_src.get(id(s))
