@@ -38,7 +38,7 @@ MFMA_PIPES = (2, 1)          # k-blocks of weights per register set when not pre
                              # the full budget
 MFMA_POINTS_MIN = 8          # points a block must make (of a tile's 16 columns)
 MFMA_ROWS_MAX = 64           # rows a stream may take: beyond 16, in 16-row tiles (each a tile of its own)
-MFMA_HALVES_MAX = 96 * 1024  # bytes of LDS the fp16 halves of the other factor take at most beyond 16 rows
+MFMA_HALVES_MAX = 100 * 1024  # bytes of LDS the fp16 halves of the other factor take at most beyond 16 rows
                              # (the fold then goes through LDS in chunks of whole 32-deep k-blocks)
 SPLIT_ADD_BYTES = 32         # beyond 16 rows, the cost of one fixed-point add of a fold split in bytes read
 

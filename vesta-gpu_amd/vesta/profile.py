@@ -76,14 +76,14 @@ def barrier_trace(m, steps=8):
     return rows
 
 
-def _model(batch, tmax, timing):
+def _model(batch, tmax, timing, model='small', prompt=128, warm=118):
     import torch
     from .gpt2 import VestaGPT2
     from .weights import RandomGPT2, random_prompts
-    m = VestaGPT2(RandomGPT2('small', 0), batch=batch, tmax=tmax, timing=timing, engine='persistent')
+    m = VestaGPT2(RandomGPT2(model, 0), batch=batch, tmax=tmax, timing=timing, engine='persistent')
     m.reset()
-    m.prefill(torch.from_numpy(random_prompts(batch, 128, 50257, seed=1)).to('cuda', torch.int32))
-    m.warm(118)                        # to position 246: the benchmark's timed steps start there
+    m.prefill(torch.from_numpy(random_prompts(batch, prompt, 50257, seed=1)).to('cuda', torch.int32))
+    m.warm(warm)                       # by default to position 246: the benchmark's timed steps start there
     return m
 
 
@@ -93,11 +93,14 @@ def main():
     ap.add_argument('--batch', type=int, default=8)
     ap.add_argument('--steps', type=int, default=20)
     ap.add_argument('--tmax', type=int, default=448)
+    ap.add_argument('--model', default='small', choices=('small', 'medium', 'xl'))
+    ap.add_argument('--prompt', type=int, default=128)
+    ap.add_argument('--warm', type=int, default=118)
     a = ap.parse_args()
     if a.what == 'sites':
-        m = _model(a.batch, a.tmax, True)
+        m = _model(a.batch, a.tmax, True, a.model, a.prompt, a.warm)
         labels, us, wall = site_times(m, a.steps)
-        print(f'GPT-2 small B={a.batch}, grid {m.k.grid}: wall {wall:.1f} us/step with timing marks; '
+        print(f'GPT-2 {a.model} B={a.batch}, grid {m.k.grid}: wall {wall:.1f} us/step with timing marks; '
               f'block 0 sites sum to {us[:, 0].sum():.1f} us/step')
         agg = {}
         for lab, v in zip(labels, us[:, 0]):
@@ -107,7 +110,7 @@ def main():
         for key, v in sorted(agg.items(), key=lambda x: -x[1]):
             print(f'| {key} | {v:.1f} |')
         return
-    m = _model(a.batch, a.tmax, 'trace')
+    m = _model(a.batch, a.tmax, 'trace', a.model, a.prompt, a.warm)
     rows = barrier_trace(m, a.steps)
     agg = {}
     for lab, work, spread, rel in rows:
@@ -116,8 +119,8 @@ def main():
         d[1] += work or 0.0
         d[2] += spread
         d[3] += rel
-    print(f'GPT-2 small B={a.batch}, grid {m.k.grid}: {len(rows)} barriers in the last of {a.steps} steps '
-          f'of one launch (positions from 246)')
+    print(f'GPT-2 {a.model} B={a.batch}, grid {m.k.grid}: {len(rows)} barriers in the last of {a.steps} steps '
+          f'of one launch (positions from {a.prompt + a.warm})')
     print('| phase ends at the barrier before | barriers | work us (slowest block) | arrival spread us | '
           'release us |\n|---|---|---|---|---|')
     for lab, (n, w, s, r) in agg.items():
