@@ -349,6 +349,7 @@ class AttnMixin:
                 or z1 in self.readers:
             raise ChainError(f'attention {t1[1]}: its phase would need a barrier after all')
         n4 = self.fx_words(z1) // 4
+        self.trace.append(('clear', z1, None, 1))
         out.append(f'{ind}for (int e_ = (int)blockIdx.x + (int)nblk * tid; e_ < {n4}; e_ += nthr) '
                    f'stz4(rb_S, {self.gofs(z1, ahead=1)} + 4u * (unsigned)e_);  // clear the next layer\'s {z1}')
         G = self.size(lead)
@@ -360,6 +361,11 @@ class AttnMixin:
         for const, coefs in rd['deps']:
             lo, hi = self.dep_range(const, coefs, vals)
             ranges.append((f'({lo}) / {PPB}', f'({hi}) / {PPB}'))
+        self.trace.append(('flags', t1[1], frozenset({rd['U']} | set(rd['emits']))))
+        self.trace.append(('flagrange', 'attention', ranges, f'(int)blockIdx.x < {G * pj["R"]}', tuple(setup),
+                           dict(lead=list(lead), ext=[self.static[a] for a in lead], G=G, PPB=PPB, deps=rd['deps'],
+                                free={a: self.static[a] for _, co in rd['deps'] for a in co if a not in lead},
+                                grid=self.grid)))
         self.ready_point(t1[1], ranges, f'(int)blockIdx.x < {G * pj["R"]}', out, ind, rd['u'][1], setup)
 
     def dep_range(self, const, coefs, lead_vals):

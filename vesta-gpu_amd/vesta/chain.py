@@ -203,6 +203,7 @@ class ChainMixin:
         layer's reads took (in an earlier phase), which the next layer's adds
         will use."""
         if z in self.fx_parity and self.fx_parity[z][3] == 'carry':
+            self.trace.append(('clear', z, None, 0))
             n4 = self.fx_words(z) // 4
             out.append(f'{ind}for (int e_ = (int)blockIdx.x + (int)nblk * tid; e_ < {n4}; e_ += nthr) '
                        f'stz4(rb_S, {self.gofs(z)} + 4u * (unsigned)e_);  // clear the buffer of {z} read '
@@ -217,6 +218,7 @@ class ChainMixin:
         if z in slot['readers'] or z in slot['dirty'] or z in self.readers or z in self.dirty:
             raise ChainError(f'local fold into {z}: {z} is used in the phase before')
         n4 = self.fx_words(z) // 4
+        self.trace.append(('clear', z, k, 0))
         slot['pre'].append(f'for (int e_ = (int)blockIdx.x + (int)nblk * tid; e_ < {n4}; e_ += nthr) '
                            f'stz4(rb_S, {self.g[z]}u + 4u * (unsigned)e_);  // clear the copies of {z}')
 
@@ -229,6 +231,7 @@ class ChainMixin:
             self.plan.append((self.show_stmt(ch['sz']), 'fixed-point sum in two layer buffers: base and '
                               'projection added'))
         early = self.early_spread_loads(axes, ch['base'], out, ind)
+        self.trace.append(('adds', z, frozenset(self.root_reads([ch['base']]))))
         I = ind + '  '
         out.append(f'{ind}{{ const unsigned cz_ = {self.fx_copy_base(z)};')
         out.append(f'{ind}for (int p_ = (int)blockIdx.x + (int)nblk * tid; p_ < {self.count_c(axes)}; '

@@ -256,6 +256,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
         self.proj = {}                # id(first attention statement) -> projection it also does
         self.fx = set()               # values kept as 64-bit fixed-point sums in global scratch
         self.elided = set()           # ids of statements another site computes
+        self.trace = []               # code-generation events in kernel order, for the phase emulator (vesta.phases)
         self.elided_vals = set()      # values no site stores
         self.scan(stmts)
         stmts = self.normalise(stmts)
@@ -988,8 +989,10 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
             self.head_io[0] |= gl_reads
             self.head_io[1] |= gl_writes
         self.readers |= gl_reads
+        self.trace.append(('site', what, frozenset(gl_reads), frozenset(gl_writes)))
 
     def barrier(self, out, ind, what='', pre_wait=()):
+        self.trace.append(('barrier', what, len(self.pf_slots)))
         out.append(f'{ind}/*@PZ{len(self.pf_slots)}@*/')   # code that must end before the arrival
         out.append(f'{ind}bk_ += 1u; grid_arrive(bar);' + (f'  // before {what}' if what else ''))
         self.mark(out, ind, f'arrive before {what}')
@@ -1308,6 +1311,8 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
 
     def note(self, reads, writes):
         self.dirty |= {n for n in writes if n not in self.private}
+        self.trace.append(('note', frozenset(n for n in reads if n not in self.private),
+                           frozenset(n for n in writes if n not in self.private)))
 
     # -- tile
     def gen_tile(self, s, c, fused, out, ind):
@@ -1786,6 +1791,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
         reads = self.root_reads([base])
         if sync:
             self.sync(reads, {z}, out, ind, f'{z} base')
+        self.trace.append(('store', z))
         if shown is not None:
             self.plan.append((show_stmt(shown), 'fixed-point sum: base here, projection adds'))
         early = self.early_spread_loads(axes, base, out, ind)
@@ -2577,6 +2583,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
             self.plan.append((show_stmt(pe), f'first value of {carry}, made where read'))
             self.peel_active[self.root(carry)] = (lv, pe)
         self.mult *= n
+        self.trace.append(('loop', var, n))
         self.loops.append({'id': self.fresh('loop'), 'var': var, 'lv': lv, 'n': self.ext_c(var),
                            'pf_before': self.last_pf, 'body_barrier': False, 'end_prefetch': [],
                            'end_dirty': self.writes_of(blk)})
@@ -2588,6 +2595,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
         lp = self.loops[-1]
         self.peel_active.pop(self.root(carry), None)
         self.barrier(out, ind + '  ', f'next {var}', pre_wait=lp['end_prefetch'])
+        self.trace.append(('endloop', var))
         self.loops.pop()
         self.mult //= n
         out.append(f'{ind}}}')
@@ -2656,8 +2664,10 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
             # what this step's last phase wrote or read
             hr, hw = self.head_io
             self.wrap_barrier = bool(hr & self.dirty or hw & (self.readers | self.dirty))
+            self.trace.append(('feedback', True, frozenset(self.local_fb)))
         elif feedback:
             self.barrier(body, ind, 'feedback')
+            self.trace.append(('feedback', False, frozenset(feedback)))
             for dst, src in feedback.items():
                 dt = self.res[dst][1]
                 if isinstance(src, int):

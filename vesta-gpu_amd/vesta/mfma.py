@@ -636,9 +636,12 @@ class MfmaMixin:
             if not sk.get('base_done'):
                 self.chain_base(sk, out, ind)
             PPB, NKB, KS = pp['PPB'], sk['st'].K // 32, sk['KS']
-            self.ready_point(name, [(f'((int)blockIdx.x % {KS} * {NKB} / {KS}) * 32 / {PPB}',
-                                     f'(((int)blockIdx.x % {KS} + 1) * {NKB} / {KS} * 32 - 1) / {PPB}')],
-                             f'(int)blockIdx.x < {sk["NPG"] * KS}', out, ind, pp['g'])
+            self.trace.append(('flags', name, frozenset({pp['g']})))
+            ranges = [(f'((int)blockIdx.x % {KS} * {NKB} / {KS}) * 32 / {PPB}',
+                       f'(((int)blockIdx.x % {KS} + 1) * {NKB} / {KS} * 32 - 1) / {PPB}')]
+            active = f'(int)blockIdx.x < {sk["NPG"] * KS}'
+            self.trace.append(('flagrange', 'split', ranges, active, (), dict(KS=KS, NKB=NKB, PPB=PPB, grid=self.grid)))
+            self.ready_point(name, ranges, active, out, ind, pp['g'])
         else:
             if not sk.get('base_done'):
                 self.emit_base(None, z, list(s[2]), sk['base'], out, ind, sync=True)
