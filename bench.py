@@ -541,13 +541,14 @@ def engines_line(shapes, steps=64, warmup=8, seed=0):
     return dict(metric='decode ms per step, both engines forced', unit='ms', rows=out)
 
 
-def config_line(key, steps=None, warmup=8, chunk=32, seed=0):
+def config_line(key, steps=None, warmup=8, chunk=32, seed=0, engine='auto'):
     """Greedy decode throughput of one of BASELINE.json's other configurations
     (random-init weights of that model, uniform-random prompts fed by the
     batched prefill, ``warmup`` untimed steps, then ``steps`` timed steps,
-    ``chunk`` per launch). Where the persistent kernel does not fit (GPT-2 XL
-    at 64 rows: its LDS need exceeds a CU's) the model runs each step as
-    per-layer launches; the line says which engine ran."""
+    ``chunk`` per launch), on the engine ``VestaGPT2(engine='auto')`` picks
+    (from 12 rows of GPT-2 small and 16 of wider models the layered engine,
+    which measured faster there, runs each step as per-layer launches); the
+    line says which engine ran, and ``engine`` forces one."""
     import torch
     from vesta.gpt2 import VestaGPT2
     from vesta.weights import RandomGPT2, random_prompts
@@ -555,7 +556,7 @@ def config_line(key, steps=None, warmup=8, chunk=32, seed=0):
     steps = min(gen, tmax - prompt - warmup) if steps is None else steps
     if prompt + warmup + steps > tmax:
         sys.exit(f'prompt + warmup + steps must stay within the {tmax}-position cache of this configuration')
-    m = VestaGPT2(RandomGPT2(model, seed), batch=batch, tmax=tmax)
+    m = VestaGPT2(RandomGPT2(model, seed), batch=batch, tmax=tmax, engine=engine)
     prompts = torch.from_numpy(random_prompts(batch, prompt, 50257, seed=1)).to('cuda', torch.int32)
     m.reset()
     m.prefill(prompts)
@@ -588,6 +589,32 @@ def config_line(key, steps=None, warmup=8, chunk=32, seed=0):
                      'flop_per_step_G': round(nflop / steps / 1e9, 3)},
             'storage': STORAGE,
             'data': f'synthetic: random-init GPT-2-{model} fp16 weights N(0,0.02) seed {seed}, uniform-random prompts'}
+
+
+def configs_summary():
+    """BASELINE.json's other configurations in the default bench line (so
+    the driver's own run measures them): each on the engine 'auto' picks,
+    with the full step count of ``config_line``; for configurations 3 and 5,
+    where 'auto' takes the layered engine, the persistent kernel's figure
+    beside it."""
+    import torch
+    out = {}
+    for key in (3, 4, '4b1', 5):
+        try:
+            c = config_line(key)
+            row = {k: c[k] for k in ('value', 'unit', 'ms_per_step', 'steps', 'engine')}
+            row['hbm_frac'] = c['hbm']['frac']
+            row['mfma_frac'] = c['mfma']['frac']
+            row['workload'] = c['metric'].split('(')[0].replace('decode tok/s, ', '').strip()
+            if c['engine'] == 'layered':
+                p = config_line(key, engine='persistent')
+                row['persistent'] = {'ms_per_step': p['ms_per_step'], 'value': p['value'],
+                                     'hbm_frac': p['hbm']['frac'], 'mfma_frac': p['mfma']['frac']}
+        except Exception as e:           # one configuration failing must not take the benchmark line with it
+            row = {'error': f'{type(e).__name__}: {e}'[:200]}
+        out[str(key)] = row
+        torch.cuda.empty_cache()
+    return out
 
 
 def xl_line(steps, warmup):
@@ -642,6 +669,7 @@ def main():
     ap.add_argument('--repeats', type=int, default=REPEATS)
     ap.add_argument('--cpu-steps', type=int, default=8)
     ap.add_argument('--no-cpu', action='store_true')
+    ap.add_argument('--no-configs', action='store_true', help='leave configurations 3-5 out of the benchmark line')
     ap.add_argument('--pmc-summary', nargs=3, metavar=('FETCH_CSV', 'WRITE_CSV', 'BENCH_LOG'),
                     help='summarise two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of '
                          '"bench.py --calibrate-copy N" into profiles/traffic.json and exit')
@@ -663,6 +691,8 @@ def main():
     ap.add_argument('--config', default='', metavar='KEY',
                     help='instead of the benchmark line, measure decode of another configuration: 3 (small, '
                          'B=32, 768-token prompts), 4 / 4b1 (medium, B=8 / B=1), 5 (XL, B=64)')
+    ap.add_argument('--engine', default='auto', choices=('auto', 'persistent', 'layered'),
+                    help='with --config: the decode engine (default: the one VestaGPT2 picks)')
     ap.add_argument('--engines', default='', metavar='MODEL:B:P:T,...',
                     help='instead of the benchmark line, time both decode engines forced at these shapes '
                          '(model, rows, prompt length, cache positions), e.g. small:16:128:448')
@@ -675,8 +705,8 @@ def main():
         key = int(args.config) if args.config.isdigit() else args.config
         if key not in CONFIGS:
             sys.exit(f'unknown configuration {args.config}')
-        print(json.dumps(config_line(key, None if '--steps' not in sys.argv else args.steps, args.warmup)),
-              flush=True)
+        print(json.dumps(config_line(key, None if '--steps' not in sys.argv else args.steps, args.warmup,
+                                     engine=args.engine)), flush=True)
         return
     if args.xl:
         print(json.dumps(xl_line(args.steps, args.warmup)), flush=True)
@@ -740,6 +770,8 @@ def main():
                'one_launch_per_step': b1.get('one_launch_per_step'), **roofline(b1, peak)},
     }
     line['device_bandwidth'] = device_bandwidth()
+    if not args.no_configs:
+        line['configs'] = configs_summary()
     if not args.no_cpu:
         line['cpu_baseline'] = cpu_baseline(args.batch, args.cpu_steps)
     print(json.dumps(line), flush=True)

@@ -78,8 +78,12 @@ int vh_device_info(int dev, int* cu_count, int* coop, int* lds_per_block, char* 
  * value of argument i; it is read before the call returns. */
 int vh_launch_cooperative(void* fn, unsigned grid, unsigned block, unsigned dyn_lds, void* stream, void** args);
 
-/* One ordinary (non-cooperative) launch, same arguments. Only for kernels
- * that do not wait on other blocks. No counterpart in the reference. */
+/* One ordinary (non-cooperative) launch, same arguments. For kernels that
+ * do not wait on other blocks, and (profiling only, where a profiler's
+ * teardown fails after cooperative launches) for a persistent kernel whose
+ * grid is at most one block per CU on an otherwise idle device: its grid
+ * barriers' bounded waits end a launch whose blocks are not all resident.
+ * No counterpart in the reference. */
 int vh_launch(void* fn, unsigned grid, unsigned block, unsigned dyn_lds, void* stream, void** args);
 
 /* ---- Allocation-free launch. No counterpart in the reference: for callers

@@ -13,8 +13,9 @@ Bar: tokens identical to the oracle's; logits within max-abs 2e-2 at the
 fixture's signature ids (each step's top-16 ids and 48 fixed ids). A token
 may differ only at a step whose oracle top-2 margin is below twice the
 largest logit error measured in the same test (a near-tie the tolerance
-itself allows); the test prints how many steps it waived, and a row is not
-compared past such a step (its inputs differ from then on).
+itself allows); the test prints how many steps it waived, a row is not
+compared past such a step (its inputs differ from then on), and at most one
+row in four (at least one) may be waived.
 """
 import hashlib
 import os
@@ -104,6 +105,8 @@ def compare(label, fx, tokens, got_sig):
           f'{len(waived)} near-tie steps waived (margin < 2 x error): {waived}')
     assert err < LOGIT_TOL, f'{label}: logits differ by {err:.3e}'
     assert not bad, f'{label}: tokens differ from the oracle at (row, step, margin) {bad}'
+    # a waiver stops the comparison of its row: at most one row in four may end early
+    assert len(waived) <= max(1, len(rows) // 4), f'{label}: {len(waived)} rows waived'
     return err, waived
 
 
@@ -167,7 +170,7 @@ def _config_model(key, engine='auto'):
 def test_config3_layered_engine_long_cache_matches_oracle():
     """B=32, 768-token prompts, 1024-position cache, on
     the engine 'auto' picks there (layered: block-per-(row, head) attention
-    over 768+ positions); rows 0, 1 and 31, 4 greedy tokens."""
+    over 768+ positions); rows 0, 1, 7, 15, 16, 24, 30 and 31, 12 greedy tokens."""
     m, prompts = _config_model(3)
     assert m.engine == 'layered'
     fx = _fixture('c3')
@@ -187,8 +190,9 @@ def test_config4_medium_matches_oracle(key):
 
 def test_config5_xl_b64_matches_oracle():
     """GPT-2 XL, all 48 layers, B=64, 128-token prompts,
-    256-position cache (layered engine: the persistent kernel's LDS need
-    exceeds a CU's there); rows 0, 1 and 63, 2 greedy tokens."""
+    256-position cache, on the engine 'auto' picks there (layered: the
+    persistent kernel fits, below, but is slower); rows 0, 1, 15, 31, 32, 47,
+    62 and 63, 8 greedy tokens."""
     m, prompts = _config_model(5)
     assert m.engine == 'layered'
     fx = _fixture('c5')
