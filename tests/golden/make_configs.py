@@ -35,10 +35,10 @@ N_TOP, N_FIXED = 16, 48
 CONFIGS = {
     'c1': ('small', 1, 128, 256, (0,), None),
     'c2': ('small', 8, 128, 256, tuple(range(8)), None),
-    'c3': ('small', 32, 768, 4, (0, 1, 31), None),
-    'c4': ('medium', 8, 256, 4, (0, 7), None),
-    'c4b1': ('medium', 1, 256, 4, (0,), None),
-    'c5': ('xl', 64, 128, 2, (0, 1, 63), None),
+    'c3': ('small', 32, 768, 12, (0, 1, 7, 15, 16, 24, 30, 31), None),
+    'c4': ('medium', 8, 256, 8, tuple(range(8)), None),
+    'c4b1': ('medium', 1, 256, 8, (0,), None),
+    'c5': ('xl', 64, 128, 8, (0, 1, 15, 31, 32, 47, 62, 63), None),
 }
 N_LAYER = {'small': 12, 'medium': 24, 'xl': 48}
 
@@ -110,4 +110,4 @@ if __name__ == '__main__':
     keys = sys.argv[1:] or list(CONFIGS)
     workers = int(os.environ.get('WORKERS', '8'))
     for key in keys:
-        make(key, 2 if CONFIGS[key][0] == 'xl' else workers)
+        make(key, min(workers, 4) if CONFIGS[key][0] == 'xl' else workers)   # XL: ~7 GB per worker

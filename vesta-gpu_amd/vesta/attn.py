@@ -501,7 +501,6 @@ class AttnMixin:
             lines.append(f'  }} else {{ {kd} = vh_u32x4{{0u, 0u, 0u, 0u}}; {vd} = vh_u32x4{{0u, 0u, 0u, 0u}}; }}')
             lines.append('}')
             return lines
-        self.load_kv_at = load_kv_at
 
         lane_decl = f'const int sub_ = lane / {LPE}, cl_ = lane % {LPE};'
         self.decls.append(f'vh_u32x4 {kq}[{NPS}];')
@@ -601,7 +600,7 @@ class AttnMixin:
         o.append(f'{I}}}')
         if online:
             self.attn_online(at, o, I, lenv, NPS, NPF, PPP, PPW, LPE, NW, T, nE, kq, vq, slot_env, load_kv,
-                             red_o, pj, po_ref := [], chunk)
+                             red_o, pj, po_ref := [], chunk, load_kv_at)
             po = po_ref[0]
             if pj is not None:
                 if not early:
@@ -737,7 +736,7 @@ class AttnMixin:
         return t3[3][3] == F and at['c4'].A == ('bin', '/', F, ('idx', t3[1], at_lead))
 
     def attn_online(self, at, o, I, lenv, NPS, NPF, PPP, PPW, LPE, NW, T, nE, kq, vq, slot_env, load_kv,
-                    red_o, pj, po_ref, CH):
+                    red_o, pj, po_ref, CH, load_kv_at):
         """Scores, softmax and weighted values over chunks of CH slots:
         each lane group keeps its positions' running maximum m, sum l of
         exp(score - m) and weighted values (rescaled by exp(m_old - m_new) when
@@ -758,7 +757,7 @@ class AttnMixin:
             for k in first:
                 o += [I + x for x in load_kv(k, lenv, False)]
         if NCH >= ATTN_CHUNK_LOOP:
-            self.attn_chunk_loop(at, o, I, lenv, NPS, PPP, PPW, LPE, NW, T, kq, vq, slot_env, CH, NCH)
+            self.attn_chunk_loop(at, o, I, lenv, PPP, PPW, LPE, NW, T, kq, vq, slot_env, CH, NCH, load_kv_at)
         for c in (range(NCH) if NCH < ATTN_CHUNK_LOOP else ()):
             ks = list(range(c * CH, min(NPS, (c + 1) * CH)))
             nxt = [k for k in range((c + 1) * CH, min(NPS, (c + 2) * CH)) if k >= NPF]
@@ -849,11 +848,12 @@ class AttnMixin:
         self.mark(o, I, 'attention: combine')
         po_ref.append(po)
 
-    def attn_chunk_loop(self, at, o, I, lenv, NPS, PPP, PPW, LPE, NW, T, kq, vq, slot_env, CH, NCH):
+    def attn_chunk_loop(self, at, o, I, lenv, PPP, PPW, LPE, NW, T, kq, vq, slot_env, CH, NCH, load_kv_at):
         """The chunks of ``attn_online`` as a run-time loop: the current
         chunk's rows in kc_/vc_ (the first chunk's from kq/vq), the next
-        chunk's loaded into kn_/vn_ while the current one is used. The
-        operations and their order are those of the unrolled chunks."""
+        chunk's loaded into kn_/vn_ (``load_kv_at``: the rows of a slot given
+        as a C expression) while the current one is used. The operations and
+        their order are those of the unrolled chunks."""
         c1 = at['c1']
         o.append(f'{I}vh_u32x4 kc_[{CH}], vc_[{CH}], kn_[{CH}], vn_[{CH}];')
         for j in range(CH):
@@ -862,7 +862,7 @@ class AttnMixin:
         J0 = I + '  '
         o.append(f'{J0}if ((c_ + 1) * {CH * PPP} < {T}) {{  // rows of the next chunk')
         for j in range(CH):
-            o += [J0 + '  ' + x for x in self.load_kv_at(f'n{j}', f'(c_ + 1) * {CH} + {j}', lenv,
+            o += [J0 + '  ' + x for x in load_kv_at(f'n{j}', f'(c_ + 1) * {CH} + {j}', lenv,
                                                           f'kn_[{j}]', f'vn_[{j}]')]
         o.append(f'{J0}}}')
         o.append(f'{J0}if (c_ * {CH * PPP} < {T}) {{  // this chunk')

@@ -1,8 +1,9 @@
 """Streamed contractions with several rows on the matrix cores.
 
-A stream ``y[r.., p] = EPI(fold sum k: A[r.., k] * W[p, k])`` with 4 to 16
+A stream ``y[r.., p] = EPI(fold sum k: A[r.., k] * W[p, k])`` with 4 to 64
 rows r (the batch) and fp16 weights runs on ``v_mfma_f32_16x16x32_f16``:
-rows are the MFMA's M (padded to 16 with zeros), a tile of 16 consecutive
+rows are the MFMA's M (padded to 16 with zeros; beyond 16 rows, one tile per
+16 rows, each with its own accumulators), a tile of 16 consecutive
 output points its N, and the fold its K, 32 at a time. Lane l of a wave holds
 A[l % 16][k0 + 8 (l / 16) ..+8], W[k0 + 8 (l / 16) ..+8][point l % 16] (one
 16-byte load from the point's row of the weight copy) and, after the loop,
@@ -24,7 +25,13 @@ fewer, KW waves share a tile, each over its own range of the fold, and the
 partial tiles are added through LDS in wave order (a fixed order, so results
 do not depend on timing). The weights of a wave's share are loaded at the
 barrier before the site when they fit in the prefetch register budget, else
-streamed through two register sets of ``mfma_pipe`` k-blocks each.
+streamed through two register sets of ``mfma_pipe`` k-blocks each. Every
+weight fragment a wave loads meets all of its row tiles.
+
+The halves of the other factor live in LDS. When those of all rows over the
+whole fold would exceed ``MFMA_HALVES_MAX`` bytes (beyond 16 rows only), the
+fold goes through LDS in chunks of whole k-blocks, every wave taking the
+same part of each chunk, and the weights are streamed.
 """
 from __future__ import annotations
 

@@ -81,7 +81,6 @@ def _expand(trace):
             cur = node[3]
         elif ev[0] == 'endloop':
             cur = stack.pop()
-            cur.append(('endloop_barrier_done',))
         else:
             cur.append(ev)
     if stack:
@@ -169,8 +168,6 @@ class PhaseEmulator:
                 for _ in range(n):
                     self._block(body)
                     self.layer += 1
-                continue
-            if kind == 'endloop_barrier_done':
                 continue
             if kind == 'barrier':
                 self._barrier(ev[2])
