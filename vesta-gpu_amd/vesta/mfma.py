@@ -48,6 +48,7 @@ MFMA_ROWS_MAX = 64           # rows a stream may take: beyond 16, in 16-row tile
 MFMA_HALVES_MAX = 100 * 1024  # bytes of LDS the fp16 halves of the other factor take at most beyond 16 rows
                              # (the fold then goes through LDS in chunks of whole 32-deep k-blocks)
 SPLIT_ADD_BYTES = 32         # beyond 16 rows, the cost of one fixed-point add of a fold split in bytes read
+SPLIT_TILES = 4              # column tiles a fold split's point group takes at most, up to 16 rows (16 beyond)
 
 
 class MfmaMixin:
@@ -545,7 +546,7 @@ class MfmaMixin:
         # point groups of NTS tiles, the fold in KS slices: the fewest bytes per block
         NKB, K = st.K // 32, st.K
         best = None
-        for NTS in range(1, 5 if R <= 16 else 17):
+        for NTS in range(1, (SPLIT_TILES if R <= 16 else 16) + 1):
             NPG = -(-P // (16 * NTS))
             KS = min(self.grid // NPG, NKB)
             if KS < 2:
