@@ -19,10 +19,14 @@ SMALL = (12, 768, 12, 3072, 50257)
 
 
 def lowering(shape, B, tmax=64):
+    """The Lowering behind ``LM.lower``'s kernel: the same fallback without
+    local folds and the same switch to the wide grid."""
     L, D, H, F, V = shape
-    _, low = LM._lower_once(gpt2_program(L, D, H, F, V), gpt2_spec(B, tmax, L, D, H, F, V), {'s': tmax}, B,
-                            ('x', 'keys', 'vals'), ('logit', 'next'), {'x': 'next', 't': 1}, False, 'k',
-                            None, None, None, True)
+    args = (gpt2_program(L, D, H, F, V), gpt2_spec(B, tmax, L, D, H, F, V), {'s': tmax}, B,
+            ('x', 'keys', 'vals'), ('logit', 'next'), {'x': 'next', 't': 1}, False, 'k')
+    out, low = LM._lower(*args, None, None, None)
+    if low.grid_auto and low.grid != LM.GRID_WIDE and (low.proj_wider or out.shared_bytes > LM.LDS_BYTES):
+        out, low = LM._lower(*args, LM.GRID_WIDE, None, None)
     return low
 
 
@@ -47,6 +51,20 @@ def test_lowered_plans_order_every_access(shape, B, ready_attn):
         assert ('attention' in waits) == ready_attn
         assert bool(low.fx_parity) == ready_attn
         assert any(e[0] == 'clear' for e in low.trace)
+
+
+@pytest.mark.parametrize('shape,B,tmax', [
+    (SMALL, 32, 1024),                          # configuration 3: 16-row tiles, runtime attention chunks
+    ((24, 1024, 16, 4096, 50257), 8, 512),      # configuration 4
+    ((24, 1024, 16, 4096, 50257), 1, 512),      # configuration 4, one row
+    ((48, 1600, 25, 6400, 50257), 64, 256),     # configuration 5: 64 rows, fold chunks
+], ids=['c3', 'c4', 'c4b1', 'c5'])
+def test_benchmark_configurations_order_every_access(shape, B, tmax):
+    """The persistent kernels of the benchmark configurations, at their real
+    cache lengths and widths, as ``lower`` builds them."""
+    low = lowering(shape, B, tmax)
+    assert not phases.check(low, steps=2)
+    assert not phases.flag_range_gaps(low)
 
 
 def _barrier_labels(shape, B, monkeypatch):
