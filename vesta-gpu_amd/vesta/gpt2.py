@@ -81,7 +81,7 @@ class VestaGPT2:
         for widths not listed; where it is faster) and
         the persistent kernel below, unless that does not fit the device (LDS
         beyond a CU's 160 KB, or more than ``SPILLS_LAYERED`` spilled
-        registers), as for GPT-2 XL at 64 rows. With the layered engine ``low`` and ``k``
+        registers), as for GPT-2 XL at one row. With the layered engine ``low`` and ``k``
         are None."""
         import torch
         if engine not in ('auto', 'persistent', 'layered'):
