@@ -83,9 +83,10 @@ def _barrier_labels(shape, B, monkeypatch):
 @pytest.mark.parametrize('B', [1, 8])
 def test_a_dropped_barrier_is_caught(B, monkeypatch):
     """Each grid barrier of the plan in turn is left out of the kernel (the
-    lowering's own bookkeeping is not told): either the lowering refuses the
-    plan (its local-fold checks) or the emulator reports a race; and for
-    most barriers it is the emulator."""
+    lowering's own bookkeeping is not told): the emulator reports a race for
+    every one. (Where the lowering's local-fold checks refuse such a plan,
+    ``lower`` falls back to the plan without local folds, and it is that
+    plan, still one barrier short, that the emulator sees.)"""
     orig = LM.Lowering.barrier
     labels = _barrier_labels(SMALL, B, monkeypatch)
     caught = {}
@@ -104,7 +105,7 @@ def test_a_dropped_barrier_is_caught(B, monkeypatch):
         assert races, f'barrier before {drop} dropped, no race found'
         caught[drop] = 'emulator'
     print(f'B={B}: {caught}')
-    assert sum(v == 'emulator' for v in caught.values()) >= len(caught) // 2
+    assert caught and all(v == 'emulator' for v in caught.values()), caught
 
 
 def test_a_flag_range_one_block_short_is_caught():
