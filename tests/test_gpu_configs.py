@@ -178,11 +178,16 @@ def test_config3_layered_engine_long_cache_matches_oracle():
     compare('config 3 (layered, B=32, tmax 1024)', fx, tokens, sig)
 
 
+@pytest.mark.parametrize('engine', ['auto', 'layered'])
 @pytest.mark.parametrize('key', [4, '4b1'])
-def test_config4_medium_matches_oracle(key):
+def test_config4_medium_matches_oracle(key, engine):
     """GPT-2 medium, 256-token prompts, 512-position
-    cache, at B=8 (rows 0 and 7) and B=1; 4 greedy tokens."""
-    m, prompts = _config_model(key)
+    cache, at B=8 (all rows) and B=1; 8 greedy tokens. On the engine 'auto'
+    picks there (the persistent kernel) and on the layered engine forced
+    (its one-tile products and output head at medium's widths)."""
+    m, prompts = _config_model(key, engine)
+    if engine == 'layered':
+        assert m.engine == 'layered'
     fx = _fixture('c4' if key == 4 else 'c4b1')
     tokens, sig = decode_against(m, prompts, fx)
     compare(f'config 4 (GPT-2 medium, B={m.B}, {m.engine})', fx, tokens, sig)
