@@ -402,9 +402,12 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
 // the weights streamed from memory straight into the matrix cores' registers,
 // the activations read as they are (hi and lo planes, each multiplied into
 // its own accumulator and combined at the end). A block is PF_MW waves on the
-// same PF_MN n-tiles (32 columns); block vb takes n-tile pair vb / ks and fold
-// part vb % ks of ks, and its waves split that part's k-steps into PF_MW
-// consecutive runs. A wave with at most PF_WFIRST k-steps issues all its
+// same MN n-tiles of 16 columns, MN = 1 up to 32 rows and 2 at 64 rows (with
+// MN = 2 throughout, same box: GPT-2 small at 32 rows 0.585 -> 0.601 ms per
+// step, medium at 16 rows 0.969 -> 1.058, XL at 64 rows even; with MN = 1 at
+// 64 rows XL 3.02 -> 3.79, the activation rows re-read by twice the blocks);
+// block vb takes n-tiles MN (vb / ks) .. + MN and fold part vb % ks of ks,
+// and its waves split that part's k-steps into PF_MW consecutive runs. A wave with at most PF_WFIRST k-steps issues all its
 // weight fragments at once, then the activation fragments one k-step ahead
 // of the one it multiplies (XL B=64 decode 3.35 -> 3.10 ms per step against
 // both one k-step ahead; activations two ahead 3.15); a longer run keeps the
@@ -415,7 +418,6 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
 // 2 (GELU) writes the result in fragment order into F, as the activation of
 // the next product (N / 32 k-steps).
 #define PF_MW 8
-#define PF_MN 2
 #define PF_WFIRST 8     // k-steps of a wave up to which all its weight fragments are loaded first
 
 // pf_epi for eight consecutive columns n .. n + 7 of row m (one position per
@@ -450,48 +452,48 @@ __device__ __forceinline__ void pf_epi8(int mode, int m, int n, float* v, const 
       vh_u32x4{h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16), h[4] | ((unsigned)h[5] << 16),
                h[6] | ((unsigned)h[7] << 16)};
 }
-template <int MT>
+template <int MT, int MN>
 __device__ __forceinline__ void pf_mgemm_body(
     int vb, const vh_u32x4* __restrict__ Af, const vh_u32x4* __restrict__ Wf, int KT, int NT, int ks,
     const vh_half* __restrict__ bias, int M, int N, int mode, float* __restrict__ out, int ldo,
     vh_half* __restrict__ kc, vh_half* __restrict__ vc, const int* __restrict__ tp, int layer, int L, int tmax,
     float* __restrict__ ws, vh_half* __restrict__ F, unsigned* __restrict__ err) {
-  __shared__ __attribute__((aligned(16))) vh_f32x4 red[PF_MW][PF_MN * MT * 64];
-  __shared__ __attribute__((aligned(16))) float tile[16 * MT][16 * PF_MN + 4];
+  __shared__ __attribute__((aligned(16))) vh_f32x4 red[PF_MW][MN * MT * 64];
+  __shared__ __attribute__((aligned(16))) float tile[16 * MT][16 * MN + 4];
   const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-  const int part = vb % ks, nt0 = (vb / ks) * PF_MN;
+  const int part = vb % ks, nt0 = (vb / ks) * MN;
   const int ka = part * KT / ks, kb = (part + 1) * KT / ks;
   const int k0 = ka + (kb - ka) * wave / PF_MW, k1 = ka + (kb - ka) * (wave + 1) / PF_MW;
-  vh_f32x4 acc[PF_MN][MT], acl[PF_MN][MT];
+  vh_f32x4 acc[MN][MT], acl[MN][MT];
 #pragma unroll
-  for (int t = 0; t < PF_MN; ++t)
+  for (int t = 0; t < MN; ++t)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[t][mt] = acl[t][mt] = vh_f32x4{0.0f, 0.0f, 0.0f, 0.0f};
   const size_t plane = (size_t)MT * KT * 64;
   // the epilogue's operands of this thread's item (a thread has at most one:
-  // 16 MT x 2 PF_MN <= PF_MW x 64), loaded before the products so that their
+  // 16 MT x 2 MN <= PF_MW x 64), loaded before the products so that their
   // latency is not added at the end: the bias, the residual row piece, the
   // sequence position of the cache rows
-  const int ei = threadIdx.x, em = ei / (2 * PF_MN), ec8 = 8 * (ei % (2 * PF_MN)), en = 16 * nt0 + ec8;
-  const bool eok = ks == 1 && ei < 16 * MT * 2 * PF_MN && em < M && en < N;
+  const int ei = threadIdx.x, em = ei / (2 * MN), ec8 = 8 * (ei % (2 * MN)), en = 16 * nt0 + ec8;
+  const bool eok = ks == 1 && ei < 16 * MT * 2 * MN && em < M && en < N;
   float eb[8] = {}, ez[8] = {};
   int epos = 0;
   // the GELU product adds the bias and applies GELU where the waves' sums are
-  // added (every thread has at most one item there: PF_MN MT 64 <= PF_MW 64),
+  // added (every thread has at most one item there: MN MT 64 <= PF_MW 64),
   // so that all threads share that work; this thread's item's column bias:
   const bool gelu_red = ks == 1 && mode == 2;
   const int rn = 16 * (nt0 + (threadIdx.x >> 6) / MT) + (threadIdx.x & 15);
-  const float rb = gelu_red && bias != nullptr && threadIdx.x < PF_MN * MT * 64 && rn < N ? h2f(bias[rn]) : 0.0f;
+  const float rb = gelu_red && bias != nullptr && threadIdx.x < MN * MT * 64 && rn < N ? h2f(bias[rn]) : 0.0f;
   if (eok) {
     if (bias && mode != 2) unpack8(ld16(bias + en), eb);
     if (mode == 1) pf_ld8f(out + (size_t)em * ldo + en, ez);
     if (mode == 3) epos = *tp;
   }
-  vh_u32x4 wa[PF_MN], aa[2][MT], wb[PF_MN], ab[2][MT];
-  auto load = [&](vh_u32x4 (&w)[PF_MN], vh_u32x4 (&a)[2][MT], int k) {
+  vh_u32x4 wa[MN], aa[2][MT], wb[MN], ab[2][MT];
+  auto load = [&](vh_u32x4 (&w)[MN], vh_u32x4 (&a)[2][MT], int k) {
     const bool in = k < k1;
 #pragma unroll
-    for (int t = 0; t < PF_MN; ++t)
+    for (int t = 0; t < MN; ++t)
       w[t] = in && nt0 + t < NT ? Wf[((size_t)(nt0 + t) * KT + k) * 64 + lane] : vh_u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int p = 0; p < 2; ++p)
@@ -499,11 +501,11 @@ __device__ __forceinline__ void pf_mgemm_body(
       for (int mt = 0; mt < MT; ++mt)
         a[p][mt] = in ? Af[p * plane + ((size_t)mt * KT + k) * 64 + lane] : vh_u32x4{0u, 0u, 0u, 0u};
   };
-  auto mma = [&](const vh_u32x4 (&w)[PF_MN], const vh_u32x4 (&a)[2][MT]) {
+  auto mma = [&](const vh_u32x4 (&w)[MN], const vh_u32x4 (&a)[2][MT]) {
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-      for (int t = 0; t < PF_MN; ++t) {
+      for (int t = 0; t < MN; ++t) {
         acc[t][mt] = vh_mfma(a[0][mt], w[t], acc[t][mt]);
         acl[t][mt] = vh_mfma(a[1][mt], w[t], acl[t][mt]);
       }
@@ -511,11 +513,11 @@ __device__ __forceinline__ void pf_mgemm_body(
   if (k1 - k0 <= PF_WFIRST) {
     // all of the wave's weight fragments first (so they are in flight at once),
     // then the activation fragments one k-step ahead
-    vh_u32x4 wall[PF_WFIRST][PF_MN];
+    vh_u32x4 wall[PF_WFIRST][MN];
 #pragma unroll
     for (int j = 0; j < PF_WFIRST; ++j)
 #pragma unroll
-      for (int t = 0; t < PF_MN; ++t)
+      for (int t = 0; t < MN; ++t)
         wall[j][t] = k0 + j < k1 && nt0 + t < NT ? Wf[((size_t)(nt0 + t) * KT + k0 + j) * 64 + lane]
                                                  : vh_u32x4{0u, 0u, 0u, 0u};
     auto loada = [&](vh_u32x4 (&a)[2][MT], int k) {
@@ -549,7 +551,7 @@ __device__ __forceinline__ void pf_mgemm_body(
     }
   }
 #pragma unroll
-  for (int t = 0; t < PF_MN; ++t)
+  for (int t = 0; t < MN; ++t)
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
       const vh_f32x4 h = acc[t][mt], l = acl[t][mt];
@@ -557,7 +559,7 @@ __device__ __forceinline__ void pf_mgemm_body(
           vh_f32x4{vh_hilo(h[0], l[0]), vh_hilo(h[1], l[1]), vh_hilo(h[2], l[2]), vh_hilo(h[3], l[3])};
     }
   __syncthreads();
-  for (int i = threadIdx.x; i < PF_MN * MT * 64; i += PF_MW * 64) {
+  for (int i = threadIdx.x; i < MN * MT * 64; i += PF_MW * 64) {
     vh_f32x4 s = red[0][i];
 #pragma unroll
     for (int w = 1; w < PF_MW; ++w) {
@@ -575,8 +577,8 @@ __device__ __forceinline__ void pf_mgemm_body(
   const int n0 = 16 * nt0;
   if (ks == 1 && mode == 2) {
     bool bad = false;
-    for (int e = threadIdx.x; e < 16 * MT * 2 * PF_MN; e += PF_MW * 64) {
-      const int m = e / (2 * PF_MN), c8 = 8 * (e % (2 * PF_MN));
+    for (int e = threadIdx.x; e < 16 * MT * 2 * MN; e += PF_MW * 64) {
+      const int m = e / (2 * MN), c8 = 8 * (e % (2 * MN));
       if (m >= M || n0 + c8 >= N) continue;
       float v[8];
 #pragma unroll
@@ -587,8 +589,8 @@ __device__ __forceinline__ void pf_mgemm_body(
     return;
   }
   if (ks > 1 || mode == 1 || mode == 3) {   // eight consecutive columns per thread, 16-byte stores
-    for (int e = threadIdx.x; e < 16 * MT * 2 * PF_MN; e += PF_MW * 64) {
-      const int m = e / (2 * PF_MN), c8 = 8 * (e % (2 * PF_MN)), n = n0 + c8;
+    for (int e = threadIdx.x; e < 16 * MT * 2 * MN; e += PF_MW * 64) {
+      const int m = e / (2 * MN), c8 = 8 * (e % (2 * MN)), n = n0 + c8;
       if (m >= M || n >= N) continue;
       float v[8];
 #pragma unroll
@@ -603,25 +605,25 @@ __device__ __forceinline__ void pf_mgemm_body(
     }
     return;
   }
-  for (int e = threadIdx.x; e < 16 * MT * 16 * PF_MN; e += PF_MW * 64) {
-    const int m = e / (16 * PF_MN), c = e % (16 * PF_MN), n = n0 + c;
+  for (int e = threadIdx.x; e < 16 * MT * 16 * MN; e += PF_MW * 64) {
+    const int m = e / (16 * MN), c = e % (16 * MN), n = n0 + c;
     if (m >= M || n >= N) continue;
     pf_epi(mode, m, n, tile[m][c], bias, N, out, ldo, kc, vc, 1, tp, layer, L, tmax);
   }
 }
 
-#define PF_MGEMM(name, MT)                                                                                         \
+#define PF_MGEMM(name, MT, MN)                                                                                       \
   extern "C" __global__ __launch_bounds__(PF_MW * 64) void name(                                                  \
       const vh_u32x4* __restrict__ Af, const vh_u32x4* __restrict__ Wf, int KT, int NT, int ks,                    \
       const vh_half* __restrict__ bias, int M, int N, int mode, float* __restrict__ out, int ldo,                 \
       vh_half* __restrict__ kc, vh_half* __restrict__ vc, const int* __restrict__ tp, int layer, int L, int tmax, \
       float* __restrict__ ws, vh_half* __restrict__ F, unsigned* __restrict__ err) {                              \
-    pf_mgemm_body<MT>(blockIdx.x, Af, Wf, KT, NT, ks, bias, M, N, mode, out, ldo, kc, vc, tp, layer, L, tmax, ws, \
+    pf_mgemm_body<MT, MN>(blockIdx.x, Af, Wf, KT, NT, ks, bias, M, N, mode, out, ldo, kc, vc, tp, layer, L, tmax, ws, \
                       F, err);                                                                                    \
   }
-PF_MGEMM(pf_mgemm1, 1)
-PF_MGEMM(pf_mgemm2, 2)
-PF_MGEMM(pf_mgemm4, 4)
+PF_MGEMM(pf_mgemm1, 1, 1)
+PF_MGEMM(pf_mgemm2, 2, 1)
+PF_MGEMM(pf_mgemm4, 4, 2)
 
 // The output head (a plain product with many columns: out[m, n] = C, no
 // bias): block b's wave w makes n-tiles 2 (PF_MW b + w) and the next one

@@ -46,7 +46,7 @@ FUSE_REDUCE_LN = True         # (prefill products) a split residual product's re
 MODE_PLAIN, MODE_RESID, MODE_GELU, MODE_QKV = 0, 1, 2, 3
 DECODE_ROWS = 64              # decode passes of up to this many rows run the fragment-order products (pf_mgemm*)
 MG_WAVES = 8                  # waves of a pf_mgemm block ...
-MG_TILES = 2                  # ... and the 16-column tiles it makes
+MG_TILES = {1: 1, 2: 1, 4: 2}  # ... and the 16-column tiles it makes, by 16-row tiles (pf_mgemm1/2/4's MN)
 MG_BLOCKS = 200               # a decode product splits its fold so that it has about this many blocks, ...
 MG_MIN_STEPS = 16             # ... each part at least this many 32-deep k-steps (two per wave)
 MG_MIN_STEPS_LN = 8           # ... or this many for a residual product whose reduction makes the next LayerNorm
@@ -226,13 +226,13 @@ class Prefill:
         GELU product, ``pf_reduce`` otherwise."""
         m = self.m
         KT, NT = K // 32, -(-N // 16)
-        nb = -(-NT // MG_TILES)
+        mt = _mtiles(M)
+        nb = -(-NT // MG_TILES[mt])
         steps = MG_MIN_STEPS_LN if mode == MODE_RESID and ln is not None else MG_MIN_STEPS
         ks = max(1, min(round(MG_BLOCKS / nb), KT // steps))
         ws = self._workspace(ks * M * N) if ks > 1 else None
         Wf = self._frag(wname)
         Wf = Wf[layer] if layer is not None else Wf
-        mt = _mtiles(M)
         # the extents pf_mgemm* indexes, checked before the launch is recorded
         if K % 32 or M > 16 * mt or mt > 4:
             raise ValueError(f'decode product: K={K} must be a multiple of 32 and M={M} at most 64')
