@@ -22,7 +22,8 @@ def _engine(frag_numel=None):
     order of the right (or the given) size, a CPU workspace."""
     e = pf.Prefill.__new__(pf.Prefill)
     e._plan, e._own, e._bufs = [], {}, {}
-    e.fn = {n: None for n in ('pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_reduce_ln', 'pf_reduce_frag', 'pf_reduce',
+    e.fn = {n: None for n in ('pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_mgemm1n', 'pf_mgemm2n', 'pf_mgemm4n',
+                              'pf_reduce_ln', 'pf_reduce_frag', 'pf_reduce',
                               'pf_mhead1', 'pf_mhead2', 'pf_mhead4')}
     e.err = torch.zeros(1, dtype=torch.int32)
     e.m = types.SimpleNamespace(keys=torch.zeros(1), vals=torch.zeros(1), t=torch.zeros(1, dtype=torch.int32),
@@ -84,3 +85,15 @@ def test_mis_sized_output_heads_are_refused(case):
     with pytest.raises(ValueError, match='output head'):
         e._mhead(Af, K, V, out, B)
     assert e._plan == []
+
+
+@pytest.mark.parametrize('weight_bytes,kernel', [(247_000_000, 'pf_mgemm1'), (707_000_000, 'pf_mgemm1n')])
+def test_products_load_weights_nontemporal_beyond_the_memory_side_cache(weight_bytes, kernel):
+    """A model whose weights fit the device's memory-side cache keeps the
+    default policy for the products' weight loads; a larger one gets the
+    nontemporal variant of the same kernel."""
+    e = _engine()
+    e.m.weight_bytes = weight_bytes
+    e._mgemm(_af(B, D), D, 'qkvw', 0, 3 * D, pf.MODE_QKV, bias=torch.zeros(3 * D), out=torch.zeros(B, D), ldo=D,
+             M=B)
+    assert e._plan[0][0] == kernel

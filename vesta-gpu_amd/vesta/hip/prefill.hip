@@ -452,7 +452,7 @@ __device__ __forceinline__ void pf_epi8(int mode, int m, int n, float* v, const 
       vh_u32x4{h[0] | ((unsigned)h[1] << 16), h[2] | ((unsigned)h[3] << 16), h[4] | ((unsigned)h[5] << 16),
                h[6] | ((unsigned)h[7] << 16)};
 }
-template <int MT, int MN>
+template <int MT, int MN, bool WNT>
 __device__ __forceinline__ void pf_mgemm_body(
     int vb, const vh_u32x4* __restrict__ Af, const vh_u32x4* __restrict__ Wf, int KT, int NT, int ks,
     const vh_half* __restrict__ bias, int M, int N, int mode, float* __restrict__ out, int ldo,
@@ -489,12 +489,20 @@ __device__ __forceinline__ void pf_mgemm_body(
     if (mode == 1) pf_ld8f(out + (size_t)em * ldo + en, ez);
     if (mode == 3) epos = *tp;
   }
+  // weight fragments: nontemporal (WNT) where the model's weights cannot stay
+  // in the memory-side cache between steps (the host picks the kernel)
+  auto wld = [&](size_t i) {
+    if constexpr (WNT)
+      return __builtin_nontemporal_load(Wf + i);
+    else
+      return Wf[i];
+  };
   vh_u32x4 wa[MN], aa[2][MT], wb[MN], ab[2][MT];
   auto load = [&](vh_u32x4 (&w)[MN], vh_u32x4 (&a)[2][MT], int k) {
     const bool in = k < k1;
 #pragma unroll
     for (int t = 0; t < MN; ++t)
-      w[t] = in && nt0 + t < NT ? Wf[((size_t)(nt0 + t) * KT + k) * 64 + lane] : vh_u32x4{0u, 0u, 0u, 0u};
+      w[t] = in && nt0 + t < NT ? wld(((size_t)(nt0 + t) * KT + k) * 64 + lane) : vh_u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int p = 0; p < 2; ++p)
 #pragma unroll
@@ -518,7 +526,7 @@ __device__ __forceinline__ void pf_mgemm_body(
     for (int j = 0; j < PF_WFIRST; ++j)
 #pragma unroll
       for (int t = 0; t < MN; ++t)
-        wall[j][t] = k0 + j < k1 && nt0 + t < NT ? Wf[((size_t)(nt0 + t) * KT + k0 + j) * 64 + lane]
+        wall[j][t] = k0 + j < k1 && nt0 + t < NT ? wld(((size_t)(nt0 + t) * KT + k0 + j) * 64 + lane)
                                                  : vh_u32x4{0u, 0u, 0u, 0u};
     auto loada = [&](vh_u32x4 (&a)[2][MT], int k) {
       const bool in = k < k1;
@@ -612,18 +620,21 @@ __device__ __forceinline__ void pf_mgemm_body(
   }
 }
 
-#define PF_MGEMM(name, MT, MN)                                                                                       \
+#define PF_MGEMM(name, MT, MN, WNT)                                                                                     \
   extern "C" __global__ __launch_bounds__(PF_MW * 64) void name(                                                  \
       const vh_u32x4* __restrict__ Af, const vh_u32x4* __restrict__ Wf, int KT, int NT, int ks,                    \
       const vh_half* __restrict__ bias, int M, int N, int mode, float* __restrict__ out, int ldo,                 \
       vh_half* __restrict__ kc, vh_half* __restrict__ vc, const int* __restrict__ tp, int layer, int L, int tmax, \
       float* __restrict__ ws, vh_half* __restrict__ F, unsigned* __restrict__ err) {                              \
-    pf_mgemm_body<MT, MN>(blockIdx.x, Af, Wf, KT, NT, ks, bias, M, N, mode, out, ldo, kc, vc, tp, layer, L, tmax, ws, \
-                      F, err);                                                                                    \
+    pf_mgemm_body<MT, MN, WNT>(blockIdx.x, Af, Wf, KT, NT, ks, bias, M, N, mode, out, ldo, kc, vc, tp, layer, L,    \
+                               tmax, ws, F, err);                                                                 \
   }
-PF_MGEMM(pf_mgemm1, 1, 1)
-PF_MGEMM(pf_mgemm2, 2, 1)
-PF_MGEMM(pf_mgemm4, 4, 2)
+PF_MGEMM(pf_mgemm1, 1, 1, false)
+PF_MGEMM(pf_mgemm2, 2, 1, false)
+PF_MGEMM(pf_mgemm4, 4, 2, false)
+PF_MGEMM(pf_mgemm1n, 1, 1, true)
+PF_MGEMM(pf_mgemm2n, 2, 1, true)
+PF_MGEMM(pf_mgemm4n, 4, 2, true)
 
 // The output head (a plain product with many columns: out[m, n] = C, no
 // bias): block b's wave w makes n-tiles 2 (PF_MW b + w) and the next one

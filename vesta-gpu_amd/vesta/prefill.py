@@ -34,8 +34,8 @@ TILE = 64
 CHUNK = 64                    # fold depth one product step stages in LDS
 HEAD = 64
 KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_reduce_ln', 'pf_attn', 'pf_attn1', 'pf_argmax_part',
-           'pf_argmax', 'pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_reduce_frag', 'pf_attn1s', 'pf_mhead1', 'pf_mhead2', 'pf_mhead4',
-           'pf_embed_ln')
+           'pf_argmax', 'pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_mgemm1n', 'pf_mgemm2n', 'pf_mgemm4n', 'pf_reduce_frag',
+           'pf_attn1s', 'pf_mhead1', 'pf_mhead2', 'pf_mhead4', 'pf_embed_ln')
 ARGMAX_SPLIT = 16             # blocks per row of the output-head argmax
 SPLIT_BLOCKS = 384            # a product with fewer output tiles than this splits its fold over blocks ...
                               # (XL B=64 decode: 4.95 ms per step at 320-384, 5.18 at 256, 5.42 at 512)
@@ -52,6 +52,10 @@ MG_MIN_STEPS = 16             # ... each part at least this many 32-deep k-steps
 MG_MIN_STEPS_LN = 8           # ... or this many for a residual product whose reduction makes the next LayerNorm
                               # (its split adds no launch; same box, 16 / 12 / 8: XL B=64 3.089 / 3.057 / 3.059
                               # ms per step, small B=32 with 1024 positions 0.620 / 0.610 / 0.608)
+MEM_CACHE_BYTES = 256 << 20   # the device's memory-side cache: decode products of a model whose weights are
+                              # larger load them nontemporal (same box: XL B=64 3.000 -> 2.944 ms per step,
+                              # medium B=16 0.958 -> 0.916; GPT-2 small's 247 MB stay in that cache between
+                              # steps, nontemporal there: 32 rows 0.548 -> 0.553)
 FRAG_DECODE = True            # decode passes on the fragment-order products (else the prefill products)
 HEAD_SPLIT_N = True           # the decode pass's output head on pf_mhead* (waves split the columns)
 ATTN_ONE_PASS_BLOCKS = 1024   # decode passes with at most this many (row, head) blocks read each cache row in
@@ -243,7 +247,7 @@ class Prefill:
         if mode in (MODE_PLAIN, MODE_RESID, MODE_QKV) and out.numel() < M * ldo:
             raise ValueError(f'decode product {wname}: output smaller than {M} rows of {ldo}')
         t_args = [_p(m.keys), _p(m.vals), _p(m.t), _i(layer or 0), _i(m.L), _i(m.tmax)]
-        self._launch(f'pf_mgemm{mt}', nb * ks,
+        self._launch(f'pf_mgemm{mt}' + ('n' if self._weights_nt() else ''), nb * ks,
                      [_p(Af), _p(Wf), _i(KT), _i(NT), _i(ks), _p(bias), _i(M), _i(N), _i(mode), _p(out), _i(ldo)]
                      + t_args + [_p(ws), _p(F), _p(self.err)], block=MG_WAVES * 64)
         if ks == 1:
@@ -261,6 +265,12 @@ class Prefill:
                                                             _i(ldo), _p(m.keys), _p(m.vals), _i(1), _p(m.t),
                                                             _i(layer or 0), _i(m.L), _i(m.tmax)])
         return False
+
+    def _weights_nt(self):
+        """Whether the decode products load their weights nontemporal
+        (``pf_mgemm*n``): when the model's weights do not fit the memory-side
+        cache."""
+        return getattr(self.m, 'weight_bytes', 0) > MEM_CACHE_BYTES
 
     def _mhead(self, Af, K, N, out, M):
         """The output head over M rows (``pf_mhead*``): logits [M, N] = A wte^T,
