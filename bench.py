@@ -546,8 +546,9 @@ def config_line(key, steps=None, warmup=8, chunk=32, seed=0, engine='auto'):
     (random-init weights of that model, uniform-random prompts fed by the
     batched prefill, ``warmup`` untimed steps, then ``steps`` timed steps,
     ``chunk`` per launch), on the engine ``VestaGPT2(engine='auto')`` picks
-    (from 12 rows of GPT-2 small and 16 of wider models the layered engine,
-    which measured faster there, runs each step as per-layer launches); the
+    (from 11 rows of GPT-2 small, 9 of medium and at any row count of XL the
+    layered engine, which measured faster there, runs each step as per-layer
+    launches); the
     line says which engine ran, and ``engine`` forces one."""
     import torch
     from vesta.gpt2 import VestaGPT2

@@ -31,10 +31,12 @@ from .lower import lower
 
 LDS_PER_CU = 160 * 1024      # bytes of LDS one block of the persistent kernel may use
 SPILLS_LAYERED = 64          # spilled registers beyond which 'auto' takes the layered engine
-LAYERED_ROWS = {768: 12}      # rows from which 'auto' takes the layered engine, by model width (same box, ms
-LAYERED_ROWS_OTHER = 16       # per step, persistent / layered: GPT-2 small 8 rows 0.290 / 0.456, 12 rows
-                              # 0.553 / 0.461, 16 rows 0.601 / 0.472, 32 rows with a 1024-position cache 1.544 /
-                              # 0.669; medium 8 rows 0.860 / 1.092, 16 rows 1.237 / 1.128)
+LAYERED_ROWS = {768: 11, 1024: 9, 1600: 1}   # rows from which 'auto' takes the layered engine, by model
+LAYERED_ROWS_OTHER = 9        # width (same box, ms per step, persistent / layered: GPT-2 small 8 rows 0.288 /
+                              # 0.395, 10 rows 0.372 / 0.399, 11 rows 0.545 / 0.398, 16 rows 0.594 / 0.403, 32
+                              # rows with a 1024-position cache 0.867 / 0.546; medium 8 rows 0.864 / 0.893, 9
+                              # rows 1.253 / 0.903, 16 rows 1.246 / 0.919; XL 2 rows 2.601 / 2.124, 8 rows
+                              # 3.182 / 2.099, 64 rows 7.321 / 3.070)
 
 SHAPE_PROGRAMS = {(12, 768, 12): 'gpt2.vst', (24, 1024, 16): 'gpt2_medium.vst', (48, 1600, 25): 'gpt2_xl.vst'}
 
