@@ -407,7 +407,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_reduce_ln(
 // step, medium at 16 rows 0.969 -> 1.058, XL at 64 rows even; with MN = 1 at
 // 64 rows XL 3.02 -> 3.79, the activation rows re-read by twice the blocks);
 // block vb takes n-tiles MN (vb / ks) .. + MN and fold part vb % ks of ks,
-// and its waves split that part's k-steps into PF_MW consecutive runs. A wave with at most PF_WFIRST k-steps issues all its
+// and its waves split that part's k-steps into PF_MW consecutive runs. A
+// wave with at most PF_WFIRST k-steps issues all its
 // weight fragments at once, then the activation fragments one k-step ahead
 // of the one it multiplies (XL B=64 decode 3.35 -> 3.10 ms per step against
 // both one k-step ahead; activations two ahead 3.15); a longer run keeps the
