@@ -36,7 +36,8 @@ HEAD = 64
 KERNELS = ('pf_embed', 'pf_ln', 'pf_gemm', 'pf_reduce', 'pf_reduce_ln', 'pf_attn', 'pf_attn1', 'pf_argmax_part',
            'pf_argmax', 'pf_mgemm1', 'pf_mgemm2', 'pf_mgemm4', 'pf_mgemm1n', 'pf_mgemm2n', 'pf_mgemm4n',
            'pf_reduce_frag', 'pf_attn1s', 'pf_mhead1', 'pf_mhead2', 'pf_mhead4', 'pf_embed_ln')
-ARGMAX_SPLIT = 16             # blocks per row of the output-head argmax
+ARGMAX_SPLIT = 32             # blocks per row of the output-head argmax (same box, 16 -> 32: GPT-2 small 32 rows
+                              # 547.6 -> 545.8 us per step, 8 rows 396.3 -> 395.5, XL 64 rows even)
 SPLIT_BLOCKS = 384            # a product with fewer output tiles than this splits its fold over blocks ...
                               # (XL B=64 decode: 4.95 ms per step at 320-384, 5.18 at 256, 5.42 at 512)
 SPLIT_MIN_CHUNKS = 4          # ... into parts of at least this many 64-deep chunks
