@@ -97,3 +97,18 @@ def test_products_load_weights_nontemporal_beyond_the_memory_side_cache(weight_b
     e._mgemm(_af(B, D), D, 'qkvw', 0, 3 * D, pf.MODE_QKV, bias=torch.zeros(3 * D), out=torch.zeros(B, D), ldo=D,
              M=B)
     assert e._plan[0][0] == kernel
+
+
+@pytest.mark.parametrize('rows,tiles', [(8, 1), (32, 1), (64, 2)])
+def test_products_take_one_column_tile_per_block_up_to_32_rows(rows, tiles):
+    """A decode product's block makes one 16-column tile up to 32 rows (two
+    row tiles) and two at 64 rows (four): the grid is the column tiles over
+    that, times the fold parts."""
+    e = _engine()
+    e.m.B = rows
+    e._mgemm(_af(rows, D), D, 'qkvw', 0, 3 * D, pf.MODE_QKV, bias=torch.zeros(3 * D), out=torch.zeros(rows, D),
+             ldo=D, M=rows)
+    name, _, grid, args, _ = e._plan[0]
+    ks = args.vals[4].value
+    assert name == f'pf_mgemm{pf._mtiles(rows)}'
+    assert grid == -(-(3 * D // 16) // tiles) * ks
