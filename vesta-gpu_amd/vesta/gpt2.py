@@ -27,7 +27,7 @@ from __future__ import annotations
 from . import PROGRAMS
 from .gpt2_program import gpt2_program
 from .launch import TORCH_DT, Kernel, code_spills, compile_code, lower_fitted
-from .lower import lower
+from .lower import GRID_FEW_ROWS, GRID_WIDE, lower
 
 LDS_PER_CU = 160 * 1024      # bytes of LDS one block of the persistent kernel may use
 SPILLS_LAYERED = 64          # spilled registers beyond which 'auto' takes the layered engine
@@ -37,6 +37,21 @@ LAYERED_ROWS_OTHER = 9        # width (same box, ms per step, persistent / layer
                               # rows with a 1024-position cache 0.867 / 0.546; medium 8 rows 0.864 / 0.893, 9
                               # rows 1.253 / 0.903, 16 rows 1.246 / 0.919; XL 2 rows 2.601 / 2.124, 8 rows
                               # 3.182 / 2.099, 64 rows 7.321 / 3.070)
+
+FEW_ROWS_REPLICAS = 12       # below 4 rows the persistent kernel's grid gives each attention head this many
+                              # replica blocks (at least the lowering's 144 blocks, at most one per CU):
+                              # GPT-2 small 144, medium 192 (same box, ms per step, medium at
+                              # one row: 0.598 on 144 blocks, 0.582 on 128, 0.553 on 160, 0.544-0.562 on 192,
+                              # 0.545 on 208, 0.550 on 224, 0.602 on 256; small: 0.199 on 144, 0.207 on 160,
+                              # 0.213 on 192)
+
+
+def persistent_grid(batch, heads):
+    """The persistent kernel's grid for ``batch`` rows of a model with
+    ``heads`` attention heads: FEW_ROWS_REPLICAS blocks per head below 4 rows,
+    else the lowering's own choice (None)."""
+    return min(GRID_WIDE, max(GRID_FEW_ROWS, FEW_ROWS_REPLICAS * heads)) if batch < 4 else None
+
 
 SHAPE_PROGRAMS = {(12, 768, 12): 'gpt2.vst', (24, 1024, 16): 'gpt2_medium.vst', (48, 1600, 25): 'gpt2_xl.vst'}
 
@@ -113,9 +128,10 @@ class VestaGPT2:
                 else gpt2_program(L, D, H, F, V, 'custom')
         else:
             text = open(program, encoding='utf-8').read()
+        grid = persistent_grid(batch, H)
         self._lower_args = (text, spec, dict(axis_max={'s': tmax}, batch=batch, per_token=('x', 'keys', 'vals'),
                                              outputs=('logit', 'next'),
-                                             feedback={'x': 'next', 't': 1} if feedback else None))
+                                             feedback={'x': 'next', 't': 1} if feedback else None, grid=grid))
         self._R, self._bps, self._timing = R, blocks_per_sm, timing
         self.low, self.k, self._pf = None, None, None
         self._variants = {}
