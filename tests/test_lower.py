@@ -119,7 +119,8 @@ def test_gpt2_small_b8_plan():
     assert p['u'].endswith('mfma +1 fused')
     # few points per block: the fold is split over blocks too, partial tiles added
     # into a fixed-point residual
-    assert p['z2'].startswith('stream (transposed copy) mfma, fold in 16 slices, fixed-point sum')
+    # (point groups of two 16-column tiles at 8 rows: 24 groups, the fold in 8 slices)
+    assert p['z2'].startswith('stream (transposed copy) mfma, fold in 8 slices, fixed-point sum')
     assert low.barriers_per_launch <= 75
     assert low.scratch['logit'][2] == (8, 50257) and low.scratch['next'][2] == (8,)
 

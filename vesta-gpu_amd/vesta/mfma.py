@@ -49,6 +49,9 @@ MFMA_HALVES_MAX = 100 * 1024  # bytes of LDS the fp16 halves of the other factor
                              # (the fold then goes through LDS in chunks of whole 32-deep k-blocks)
 SPLIT_ADD_BYTES = 32         # beyond 16 rows, the cost of one fixed-point add of a fold split in bytes read
 SPLIT_TILES = 4              # column tiles a fold split's point group takes at most, up to 16 rows (16 beyond)
+SPLIT_TILES_PACKED = 2       # the same at 8 rows or fewer: GPT-2 medium at 8 rows 848.8 -> 741.9 us per
+                             # step (3 tiles 744.7, 1 tile 872.0), small at 8 rows 293.9 -> 290.6, at 4
+                             # and 6 rows 1% better; at 10 rows 2 tiles lose (382.8 -> 391.7)
 
 
 class MfmaMixin:
@@ -546,7 +549,7 @@ class MfmaMixin:
         # point groups of NTS tiles, the fold in KS slices: the fewest bytes per block
         NKB, K = st.K // 32, st.K
         best = None
-        for NTS in range(1, (SPLIT_TILES if R <= 16 else 16) + 1):
+        for NTS in range(1, (SPLIT_TILES_PACKED if R <= 8 else SPLIT_TILES if R <= 16 else 16) + 1):
             NPG = -(-P // (16 * NTS))
             KS = min(self.grid // NPG, NKB)
             if KS < 2:
