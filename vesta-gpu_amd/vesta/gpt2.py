@@ -32,9 +32,9 @@ from .lower import GRID_FEW_ROWS, GRID_WIDE, lower
 LDS_PER_CU = 160 * 1024      # bytes of LDS one block of the persistent kernel may use
 SPILLS_LAYERED = 64          # spilled registers beyond which 'auto' takes the layered engine
 LAYERED_ROWS = {768: 11, 1024: 9, 1600: 1}   # rows from which 'auto' takes the layered engine, by model
-LAYERED_ROWS_OTHER = 9        # width (same box, ms per step, persistent / layered: GPT-2 small 8 rows 0.288 /
+LAYERED_ROWS_OTHER = 9        # width (same box, ms per step, persistent / layered: GPT-2 small 8 rows 0.283 /
                               # 0.395, 10 rows 0.372 / 0.399, 11 rows 0.545 / 0.398, 16 rows 0.594 / 0.403, 32
-                              # rows with a 1024-position cache 0.867 / 0.546; medium 8 rows 0.864 / 0.893, 9
+                              # rows with a 1024-position cache 0.867 / 0.546; medium 8 rows 0.744 / 0.893, 9
                               # rows 1.253 / 0.903, 16 rows 1.246 / 0.919; XL 2 rows 2.601 / 2.124, 8 rows
                               # 3.182 / 2.099, 64 rows 7.321 / 3.070)
 
