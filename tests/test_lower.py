@@ -11,7 +11,7 @@ import re
 import pytest
 
 from vesta import stream
-from vesta import launch
+from vesta import launch, mfma
 from vesta.gpt2_program import gpt2_program
 from vesta.interp import parse
 from vesta.lower import LowerError, Lowering, batch_lift, lower
@@ -123,6 +123,24 @@ def test_gpt2_small_b8_plan():
     assert p['z2'].startswith('stream (transposed copy) mfma, fold in 8 slices, fixed-point sum')
     assert low.barriers_per_launch <= 75
     assert low.scratch['logit'][2] == (8, 50257) and low.scratch['next'][2] == (8,)
+
+
+@pytest.mark.parametrize('B,tiles', [(4, 2), (8, 2), (12, 4)])
+def test_fold_split_point_groups_by_rows(B, tiles, monkeypatch):
+    """A fold split's point groups take at most two 16-column tiles at 8 rows
+    or fewer and four up to 16 rows (``SPLIT_TILES_PACKED``, ``SPLIT_TILES``),
+    and the cost model goes up to that bound here."""
+    chosen = []
+    orig = mfma.MfmaMixin.split_of
+
+    def spy(self, s):
+        r = orig(self, s)
+        if r is not None:
+            chosen.append(r['NTS'])
+        return r
+    monkeypatch.setattr(mfma.MfmaMixin, 'split_of', spy)
+    lower_gpt2(B)
+    assert chosen and max(chosen) == tiles
 
 
 def test_params_and_abi():
