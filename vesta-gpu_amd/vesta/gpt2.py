@@ -43,7 +43,8 @@ FEW_ROWS_REPLICAS = 12       # below 4 rows the persistent kernel's grid gives e
                               # GPT-2 small 144, medium 192 (same box, ms per step, medium at
                               # one row: 0.598 on 144 blocks, 0.582 on 128, 0.553 on 160, 0.544-0.562 on 192,
                               # 0.545 on 208, 0.550 on 224, 0.602 on 256; small: 0.199 on 144, 0.207 on 160,
-                              # 0.213 on 192)
+                              # 0.213 on 192, and on another box 0.195 on 144, 0.201 on 132, 0.203 on 120,
+                              # 0.218 on 108, 0.211 on 96)
 
 
 def persistent_grid(batch, heads):
