@@ -94,6 +94,8 @@ GRIDRED_MIN = 1 << 14         # grid reduction for a fold at least this long int
 GRIDRED_POINTS = 8
 REPL_MAX = 1 << 14            # points a replicated (every-block) statement may have
 PRIV_GROUP = 8                # elementwise private: leading points whose reads are issued together
+HOIST_IN_REGISTERS = True     # a private statement over one leading point whose divisors and calls read
+                              # only values every wave holds makes them in each thread (no LDS, no block sync)
 BTRACE = 96                   # timing: barriers of the last step traced per block
 UNROLL = 8                    # rows (tile) / vectors (lane) whose loads are issued together
 TILE_LANES = 8                # tile: lanes per row (8 x 16 bytes = one 128-byte line of a weight row)
@@ -1850,6 +1852,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
         # point), 'wave' (point p in wave p % NWAVE) or 'thread' (any thread);
         # a statement waits for the block only when it may read another wave's writes
         wmap = {}
+        self.run_wmap = wmap
         for s in run:
             self.plan.append((show_stmt(s), 'private'))
             name, axes, e = s[1], list(s[2]), s[3]
@@ -2040,6 +2043,24 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
         invs = self.lead_invariants(e, lead) if nlead <= self.BLOCK else []
         if not invs:
             return []
+        held = getattr(self, 'run_wmap', {})
+        if HOIST_IN_REGISTERS and nlead == 1 and all(
+                held.get(n[1]) == 'all' for node, _ in invs for n in nodes(node)
+                if n[0] in ('name', 'idx') and self.is_value(n[1])):
+            # every wave holds what they read (folds into one point): each
+            # thread makes the values itself, the same operations in the same order
+            sid = self.fresh('hv')
+            env = self.decode('0', lead, o, ind, prefix=f'{sid}_')
+            hv = []
+            for k, (node, is_div) in enumerate(invs):
+                pre = []
+                v, t = self.expr(node, env, pre, ind)
+                o += pre
+                o.append(f'{ind}const float {sid}_{k} = {self.as_float(v, t)};')
+                if is_div:
+                    o.append(f'{ind}const float {sid}_{k}r = 1.0f / {sid}_{k};')
+                hv.append((node, f'{sid}_{k}', f'{sid}_{k}r' if is_div else None, True))
+            return hv
         base = self.lds_floats + self.priv_stage_end
         I = ind + '  '
         o.append(f'{ind}if (tid < {nlead}) {{  // once per leading point')
@@ -2067,7 +2088,13 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
     def bind_invariants(self, hv, pl):
         """The hoisted values of leading point ``pl`` (a C expression)."""
         self.invs, self.divr = {}, {}
-        for node, off, roff in hv:
+        for node, off, roff, *reg in hv:
+            if reg:             # made in this thread's registers
+                if roff is None:
+                    self.invs[show(node)] = off
+                else:
+                    self.divr[show(node)] = (off, roff)
+                continue
             val = self.lds_read(f'sh_f[{off} + {pl}]')
             if roff is None:
                 self.invs[show(node)] = val
