@@ -2039,7 +2039,9 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
         point (thread p makes point p) into LDS: [(node, LDS offset, offset of
         the reciprocal or None)]; ``bind_invariants`` then makes the code for
         e's points read them, and divide by such a divisor through its
-        reciprocal with the exact residual step."""
+        reciprocal with the exact residual step. Over one leading point whose
+        inputs every wave holds, each thread makes them in registers instead:
+        [(node, register, reciprocal register or None, True)]."""
         invs = self.lead_invariants(e, lead) if nlead <= self.BLOCK else []
         if not invs:
             return []
