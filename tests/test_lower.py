@@ -143,6 +143,16 @@ def test_fold_split_point_groups_by_rows(B, tiles, monkeypatch):
     assert chosen and max(chosen) == tiles
 
 
+def test_layer_norm_square_roots_per_thread_at_one_row():
+    """At one row every wave folds the LayerNorm statistics itself, so each
+    thread makes sqrt(v + eps) and its reciprocal in registers (no LDS slot,
+    no block sync); from two rows one thread per row makes them into LDS."""
+    one = lower_gpt2(1).src
+    assert 'once per leading point' not in one
+    assert len(re.findall(r'const float (hv\d+_0)r = 1\.0f / \1;', one)) == 3     # LN1, LN2, final LN
+    assert lower_gpt2(8).src.count('once per leading point') == 3
+
+
 def test_params_and_abi():
     low = lower_gpt2(1)
     names = [n for n, _, _ in low.params]
