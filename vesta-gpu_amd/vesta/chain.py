@@ -38,6 +38,9 @@ FX_COPIES = 4                # copies of a local fold's fixed-point sum (same bo
                              # B=2 239.0 / 241.2, within the spread)
 CHAIN_VEC = 8                # weights per 16-byte load (fp16)
 CHAIN_STAGE_MAX = 8192       # floats of the block's own values a local fold may keep in LDS
+FOLD_ROTATE = 64             # the blocks that add into one copy start their adds this many elements apart
+                             # (0: all in the same order; same box, GPT-2 small B=1 with 0 / 64, six models
+                             # built alternately, twice: 196.1 / 193.0 us per step; 256 as 64; medium B=1 even)
 
 
 class ChainError(LowerError):
@@ -344,7 +347,16 @@ class ChainMixin:
         # the row groups' partials, added in group order, into the block's copy
         o.append(f'{I}if (nf_ > 0) {{')
         o.append(f'{I}  const unsigned cz_ = {self.fx_copy_base(z)};')
-        o.append(f'{I}  for (int e_ = tid; e_ < {R * D}; e_ += {self.BLOCK}) {{')
+        if FOLD_ROTATE:
+            # the blocks sharing a copy start at different elements, so that
+            # their adds do not queue at the same lines at once (any order of
+            # integer adds gives the same sum)
+            C = self.fx_copies.get(z, 1)
+            o.append(f'{I}  const int ro_ = (int)((blockIdx.x / {C}u) * {FOLD_ROTATE}u % {R * D}u);')
+            o.append(f'{I}  for (int i_ = tid; i_ < {R * D}; i_ += {self.BLOCK}) {{')
+            o.append(f'{I}    const int e_ = i_ + ro_ < {R * D} ? i_ + ro_ : i_ + ro_ - {R * D};')
+        else:
+            o.append(f'{I}  for (int e_ = tid; e_ < {R * D}; e_ += {self.BLOCK}) {{')
         o.append(f'{I}    float v_ = sh_f[{red} + e_];')
         for q in range(1, RG):
             o.append(f'{I}    v_ += sh_f[{red} + {q * R * D} + e_];')
