@@ -35,7 +35,8 @@ from .mfma import MFMA_ROWS_MIN
 
 FX_COPIES = 4                # copies of a local fold's fixed-point sum (same box, GPT-2 small B=1: 207 / 197 /
                              # 200 / 205 us per step with 2 / 4 / 8 / 16; B=3 274.6 -> 268.7 from 8 to 4;
-                             # B=2 239.0 / 241.2, within the spread)
+                             # B=2 239.0 / 241.2, within the spread; with the rotated adds below, four models
+                             # each built alternately: 2 / 4 / 8 copies 202.8 / 194.1 / 196.4)
 CHAIN_VEC = 8                # weights per 16-byte load (fp16)
 CHAIN_STAGE_MAX = 8192       # floats of the block's own values a local fold may keep in LDS
 FOLD_ROTATE = 64             # the blocks that add into one copy start their adds this many elements apart
