@@ -153,6 +153,28 @@ def test_layer_norm_square_roots_per_thread_at_one_row():
     assert lower_gpt2(8).src.count('once per leading point') == 3
 
 
+def test_local_fold_adds_cover_each_element_once_per_block():
+    """The local fold's rotated adds (blocks sharing a fixed-point copy start
+    apart): read the rotation and the loop out of the generated B=1 source
+    and evaluate them for every block and thread; each block adds every
+    element of its row exactly once, and blocks of one copy do start apart."""
+    src = lower_gpt2(1).src
+    rot = re.search(r'const int ro_ = \(int\)\(\(blockIdx\.x / (\d+)u\) \* (\d+)u % (\d+)u\);', src)
+    loop = re.search(r'for \(int i_ = tid; i_ < (\d+); i_ \+= (\d+)\) \{\s*'
+                     r'const int e_ = i_ \+ ro_ < (\d+) \? i_ \+ ro_ : i_ \+ ro_ - (\d+);', src)
+    assert rot and loop
+    copies, step, n = map(int, rot.groups())
+    lim, stride, lt, sub = map(int, loop.groups())
+    assert n == lim == lt == sub == 768 and stride == 512
+    starts = set()
+    for b in range(144):
+        ro = (b // copies) * step % n
+        got = sorted(i + ro if i + ro < lt else i + ro - sub for t in range(512) for i in range(t, lim, stride))
+        assert got == list(range(n)), b
+        starts.add((b % copies, ro))
+    assert len(starts) > copies
+
+
 def test_params_and_abi():
     low = lower_gpt2(1)
     names = [n for n, _, _ in low.params]
