@@ -1906,6 +1906,7 @@ class Lowering(Analysis, StreamMixin, MfmaMixin, AttnMixin, ChainMixin):
                 info['base_done'] = True
         out.append(f'{ind}vh_lds_sync();')
         self.staged = {}
+        self.run_wmap = {}          # which waves hold what holds within this run only
 
     def private_points(self, s, npts, o, ind):
         """An elementwise private statement: the last axis runs over the threads
