@@ -144,6 +144,29 @@ def test_batch8_rows_match_oracle(small):
         _tokens_match(f'B=8 row {r}', nx[:, r], onx, marg, err)
 
 
+@pytest.mark.parametrize('B', [2, 3])
+def test_few_rows_match_oracle(small, B):
+    """Two and three rows: the grid of twelve replica blocks per head, the
+    LayerNorm statistics one row per wave, and the down-projection's local
+    fold with its fixed-point adds started apart by block. Every row against
+    the oracle, teacher-forced."""
+    from oracle import decode
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import random_prompts
+    hf, W, text = small
+    P, G = 6, 5
+    m = VestaGPT2(hf, batch=B, tmax=64)
+    assert m.engine == 'persistent' and m.k.grid == 144
+    m.reset()
+    pr = random_prompts(B, P, 50257, seed=11 + B)
+    ins, lg, nx = _run_steps(m, [pr[:, i] for i in range(P)], P + G - 1)
+    for r in range(B):
+        onx, olog, marg = decode.teacher_forced(text, W, ins[:, r], 64)
+        err = np.abs(lg[:, r] - olog).max()
+        assert err < LOGIT_TOL, (B, r, err)
+        _tokens_match(f'B={B} row {r}', nx[:, r], onx, marg, err)
+
+
 @pytest.mark.parametrize('B', [4, 8])
 def test_matrix_core_rows_long_context_match_oracle(small, B):
     """Batches on the matrix-core streams (B >= 4: MFMA tiles, the feed-forward
