@@ -167,6 +167,29 @@ def test_few_rows_match_oracle(small, B):
         _tokens_match(f'B={B} row {r}', nx[:, r], onx, marg, err)
 
 
+def test_medium_two_rows_match_oracle():
+    """GPT-2 medium at 2 rows: the local fold at width 1024 and 16 heads, on
+    twelve replica blocks per head (192 blocks). Both rows against the oracle,
+    teacher-forced."""
+    from oracle import decode
+    from vesta.gpt2 import VestaGPT2
+    from vesta.weights import RandomGPT2, random_prompts, stacked
+    hf = RandomGPT2('medium', 0)
+    W = decode.oracle_weights(stacked(hf.numpy_state(), 24))
+    text = open(os.path.join(PKG, 'vesta', 'programs', 'gpt2_medium.vst')).read()
+    B, P, G = 2, 6, 5
+    m = VestaGPT2(hf, batch=B, tmax=64)
+    assert m.engine == 'persistent' and m.k.grid == 192
+    m.reset()
+    pr = random_prompts(B, P, 50257, seed=13)
+    ins, lg, nx = _run_steps(m, [pr[:, i] for i in range(P)], P + G - 1)
+    for r in range(B):
+        onx, olog, marg = decode.teacher_forced(text, W, ins[:, r], 64)
+        err = np.abs(lg[:, r] - olog).max()
+        assert err < LOGIT_TOL, (r, err)
+        _tokens_match(f'medium B=2 row {r}', nx[:, r], onx, marg, err)
+
+
 @pytest.mark.parametrize('B', [4, 8])
 def test_matrix_core_rows_long_context_match_oracle(small, B):
     """Batches on the matrix-core streams (B >= 4: MFMA tiles, the feed-forward
