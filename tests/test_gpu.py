@@ -127,21 +127,24 @@ def test_local_checkpoint_matches_oracle(tmp_path):
         _tokens_match(f'local checkpoint row {r}', nx[:, r], onx, marg, err)
 
 
-def test_batch8_rows_match_oracle(small):
+@pytest.mark.parametrize('B', [8, 6])
+def test_batch_rows_match_oracle(small, B):
+    """Rows on the matrix cores: 8, and 6 (a 16-row tile with 6 rows); the
+    down-projection's fold split in point groups of two column tiles."""
     from oracle import decode
     from vesta.gpt2 import VestaGPT2
     from vesta.weights import random_prompts
     hf, W, text = small
-    B, P, G = 8, 6, 5
+    P, G = 6, 5
     m = VestaGPT2(hf, batch=B, tmax=64)
     m.reset()
     pr = random_prompts(B, P, 50257, seed=7)
     ins, lg, nx = _run_steps(m, [pr[:, i] for i in range(P)], P + G - 1)
-    for r in (0, 5):
+    for r in (0, B - 1):
         onx, olog, marg = decode.teacher_forced(text, W, ins[:, r], 64)
         err = np.abs(lg[:, r] - olog).max()
         assert err < LOGIT_TOL, r
-        _tokens_match(f'B=8 row {r}', nx[:, r], onx, marg, err)
+        _tokens_match(f'B={B} row {r}', nx[:, r], onx, marg, err)
 
 
 @pytest.mark.parametrize('B', [2, 3])
