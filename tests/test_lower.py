@@ -232,11 +232,17 @@ def test_fitted_kernels_take_the_deepest_mfma_pipeline_that_fits(monkeypatch):
         tries.clear()
         last = launch.lower_fitted(fake_lower, '', {}).src
         assert tries == [(b, d) for b in launch.PREFETCH_BUDGETS for d in (2, 1)] and last == tries[-1]
+        # 4 to 8 rows start from their own budgets, other row counts from the default ones
+        for batch, budgets in ((4, launch.PREFETCH_BUDGETS_PACKED), (8, launch.PREFETCH_BUDGETS_PACKED),
+                               (3, launch.PREFETCH_BUDGETS), (9, launch.PREFETCH_BUDGETS)):
+            tries.clear()
+            launch.lower_fitted(fake_lower, '', {}, batch=batch)
+            assert tries == [(b, d) for b in budgets for d in (2, 1)], batch
     # GPT-2 small B=8: the first try within the limit, every earlier one beyond it
     small = launch.lower_fitted(lower, gpt2_program(12, 768, 12, 3072, 50257), gpt2_spec(8, 448),
                                 axis_max={'s': 448}, batch=8, per_token=('x', 'keys', 'vals'),
                                 outputs=('logit', 'next'), feedback={'x': 'next', 't': 1})
-    for b, d in [(b, d) for b in launch.PREFETCH_BUDGETS for d in (2, 1)]:
+    for b, d in [(b, d) for b in launch.PREFETCH_BUDGETS_PACKED for d in (2, 1)]:
         src = lower_gpt2(8, 448, prefetch_vgprs=b, mfma_pipe=d).src
         if src == small.src:
             assert launch.code_spills(launch.compile_code(src)) <= launch.SPILLS_OK

@@ -221,6 +221,10 @@ def compile_code(src: str, arch: str = ARCH, opts=RTC_OPTS, cache: bool = True) 
 PREFETCH_BUDGETS = (64, 24, 16)   # registers per lane a site may prefetch into, tried in turn (B=8, which
                                   # spills at 64, with a 384-position cache: 308-310 us per step at 16-28,
                                   # 320 at 32, 337 at 48; with 448 positions 24 and 32 are even)
+PREFETCH_BUDGETS_PACKED = (24, 16)   # ... the same from 4 to 8 rows (same box, four models each built
+                                     # alternately, 24 against 64: small at 8 rows 285.3 / 289.4 us per step, at 4
+                                     # rows 255.5 / 257.8, medium at 8 rows 730.9 / 735.1; 16 and 28 at 8 rows
+                                     # 290.5 / 290.2; at one row 64 stays, 195.0 against 200.2)
 SPILLS_OK = 4                     # spilled registers a kernel may keep (outside its hot loops; GPT-2 small
                                   # B=8, same box: 298.5 us per step with 8 spilled at the first try, 296.2
                                   # with 1 at the next)
@@ -242,12 +246,14 @@ def code_spills(code: bytes) -> int:
 
 
 def lower_fitted(lower_fn, text, res, **kw):
-    """``lower_fn(text, res, **kw)`` with the largest prefetch register budget,
+    """``lower_fn(text, res, **kw)`` with the largest prefetch register budget
+    (of PREFETCH_BUDGETS, or PREFETCH_BUDGETS_PACKED from 4 to 8 rows),
     and at it the deepest unprefetched MFMA pipeline (``MFMA_PIPES``), whose
     kernel spills at most SPILLS_OK registers (compiling each try; the code
     objects are cached, so the chosen one is not compiled again)."""
-    from .mfma import MFMA_PIPES
-    tries = [(b, d) for b in PREFETCH_BUDGETS for d in MFMA_PIPES]
+    from .mfma import MFMA_PIPES, MFMA_ROWS_MIN
+    budgets = PREFETCH_BUDGETS_PACKED if MFMA_ROWS_MIN <= kw.get('batch', 1) <= 8 else PREFETCH_BUDGETS
+    tries = [(b, d) for b in budgets for d in MFMA_PIPES]
     for budget, pipe in tries:
         low = lower_fn(text, res, prefetch_vgprs=budget, mfma_pipe=pipe, **kw)
         if (budget, pipe) == tries[-1] or code_spills(compile_code(low.src)) <= SPILLS_OK:
