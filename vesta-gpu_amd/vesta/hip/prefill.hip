@@ -875,12 +875,13 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restri
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
   const int m = blockIdx.x / H, h = blockIdx.x % H;      // grid: rows * H blocks exactly
   const int D = H * PF_E;
-  const int at = *tp;
-  const int pos = at < tmax ? at : tmax - 1;
   const size_t base = (size_t)(m * L + layer) * tmax * D + (size_t)h * PF_E;
   // scores: eight lanes per position (lane 8g + b holds dims 8b .. 8b + 7, one
   // 16-byte load), positions g, g + 32, .. of the block's 32 lane groups, four
-  // in flight per lane; the eight partial dots added across the group
+  // in flight per lane; the eight partial dots added across the group. The
+  // query and the first batch (positions below 128, clamped into the cache) are
+  // loaded before the position is read, so that their round trips overlap;
+  // the batch's positions beyond the step's are loaded but not used.
   const int g = tid >> 3, b8 = tid & 7;
   float qv[8];
   {
@@ -889,13 +890,24 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restri
     qv[0] = q0[0]; qv[1] = q0[1]; qv[2] = q0[2]; qv[3] = q0[3];
     qv[4] = q1[0]; qv[5] = q1[1]; qv[6] = q1[2]; qv[7] = q1[3];
   }
-  float mx = -INFINITY;
-  for (int s0 = g; s0 <= pos; s0 += 32 * 4) {
-    vh_u32x4 kr[4];
+  vh_u32x4 kr[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int s = s0 + 32 * u;
-      kr[u] = s <= pos ? ld16_nt(kc + base + (size_t)s * D + 8 * b8) : vh_u32x4{0u, 0u, 0u, 0u};
+  for (int u = 0; u < 4; ++u) {
+    const int s = g + 32 * u < tmax ? g + 32 * u : tmax - 1;     // clamped: loads without a branch
+    kr[u] = ld16_nt(kc + base + (size_t)s * D + 8 * b8);
+  }
+  __builtin_amdgcn_sched_barrier(0);    // the loads above issued before the position is waited for
+  const int at = *tp;
+  const int pos = at < tmax ? at : tmax - 1;
+  float mx = -INFINITY;
+  int s0 = g;
+  do {                                  // the first batch even where g > pos (then none of it is used)
+    if (s0 != g) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = s0 + 32 * u;
+        kr[u] = s <= pos ? ld16_nt(kc + base + (size_t)s * D + 8 * b8) : vh_u32x4{0u, 0u, 0u, 0u};
+      }
     }
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -914,7 +926,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restri
         mx = fmaxf(mx, sc);
       }
     }
-  }
+    s0 += 32 * 4;
+  } while (s0 <= pos);
   __syncthreads();                      // ws written by the groups' first lanes, read by all below
   mx = wave_red_max(mx);
   if (lane == 0) red[wave] = mx;
@@ -997,7 +1010,10 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1(const float* __restri
 // faster where there are few (row, head) blocks (GPT-2 small, 32 rows, 1024
 // positions: 0.666 -> 0.637 ms per step), not with many (XL, 64 rows x 25
 // heads: 3.110 -> 3.128), so the decode pass takes it up to
-// ATTN_ONE_PASS_BLOCKS blocks.
+// ATTN_ONE_PASS_BLOCKS blocks. The first batch (positions below 128, clamped into
+// the cache) is loaded before the position is read, so that its round trip
+// overlaps that read and the query's; its positions beyond the step's are
+// loaded but not used.
 extern "C" __global__ __launch_bounds__(256) void pf_attn1s(const float* __restrict__ Q, const vh_half* __restrict__ kc,
                                                              const vh_half* __restrict__ vc, float* __restrict__ O,
                                                              const int* __restrict__ tp, int layer, int L, int tmax,
@@ -1009,8 +1025,6 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1s(const float* __restr
   const int tid = threadIdx.x;
   const int m = blockIdx.x / H, h = blockIdx.x % H;      // grid: rows * H blocks exactly
   const int D = H * PF_E;
-  const int at = *tp;
-  const int pos = at < tmax ? at : tmax - 1;
   const size_t base = (size_t)(m * L + layer) * tmax * D + (size_t)h * PF_E;
   const int g = tid >> 3, b8 = tid & 7;
   float qv[8];
@@ -1020,15 +1034,28 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1s(const float* __restr
     qv[0] = q0[0]; qv[1] = q0[1]; qv[2] = q0[2]; qv[3] = q0[3];
     qv[4] = q1[0]; qv[5] = q1[1]; qv[6] = q1[2]; qv[7] = q1[3];
   }
-  float mx = -INFINITY, sm = 0.0f, o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-  for (int s0 = g; s0 <= pos; s0 += 32 * 4) {
-    vh_u32x4 kr[4], vr[4];
+  vh_u32x4 kr[4], vr[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int s = s0 + 32 * u;
-      const size_t at8 = base + (size_t)s * D + 8 * b8;
-      kr[u] = s <= pos ? ld16_nt(kc + at8) : vh_u32x4{0u, 0u, 0u, 0u};
-      vr[u] = s <= pos ? ld16_nt(vc + at8) : vh_u32x4{0u, 0u, 0u, 0u};
+  for (int u = 0; u < 4; ++u) {
+    const int s = g + 32 * u < tmax ? g + 32 * u : tmax - 1;     // clamped: loads without a branch
+    const size_t at8 = base + (size_t)s * D + 8 * b8;
+    kr[u] = ld16_nt(kc + at8);
+    vr[u] = ld16_nt(vc + at8);
+  }
+  __builtin_amdgcn_sched_barrier(0);    // the loads above issued before the position is waited for
+  const int at = *tp;
+  const int pos = at < tmax ? at : tmax - 1;
+  float mx = -INFINITY, sm = 0.0f, o[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+  int s0 = g;
+  do {                                      // the first batch even where g > pos (then none of it is used)
+    if (s0 != g) {
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = s0 + 32 * u;
+        const size_t at8 = base + (size_t)s * D + 8 * b8;
+        kr[u] = s <= pos ? ld16_nt(kc + at8) : vh_u32x4{0u, 0u, 0u, 0u};
+        vr[u] = s <= pos ? ld16_nt(vc + at8) : vh_u32x4{0u, 0u, 0u, 0u};
+      }
     }
     float sc[4];
     float bm = mx;
@@ -1045,7 +1072,7 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1s(const float* __restr
       sc[u] = acc * 0.125f;                 // / 8, exact
       if (s0 + 32 * u <= pos) bm = fmaxf(bm, sc[u]);
     }
-    const float c = expf(mx - bm);          // 0 while mx is -inf (bm is finite: s0 <= pos)
+    const float c = bm == -INFINITY ? 0.0f : expf(mx - bm);   // 0 while mx is -inf, or no position yet
     sm *= c;
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] *= c;
@@ -1060,7 +1087,8 @@ extern "C" __global__ __launch_bounds__(256) void pf_attn1s(const float* __restr
       for (int j = 0; j < 8; ++j) o[j] = fmaf(p, v[j], o[j]);
     }
     mx = bm;
-  }
+    s0 += 32 * 4;
+  } while (s0 <= pos);
   if (b8 == 0) {
     gm[g] = mx;
     gl[g] = sm;
